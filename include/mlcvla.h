@@ -1,0 +1,154 @@
+/*
+ * mlcvla.h -- C ABI of the MI355X (gfx950) pi0.5 M1 denoise library.
+ *
+ * Drop-in for the TVM Relax VM entry points of mlc-vla's M1 path.  In the
+ * reference every entry point is a PackedFunc called as
+ *     vm["<fn>"](*tensors, params)
+ * (python/mlc_vla/sample.py:128,158-160,184-186), with signatures fixed by
+ * Pi0Model.get_default_spec (python/mlc_vla/model/pi0/pi0_model.py:197-255).
+ * Here the parameters are bound once to a context and the tensors are passed
+ * as plain device pointers; outputs are caller-allocated.
+ *
+ * Conventions
+ *  - Every function returns 0 on success, a negative code on failure
+ *    (-1 HIP runtime error, -2 invalid argument, -3 not bound / unsupported);
+ *    mlcv_last_error() returns the message of the last failure on this thread.
+ *  - All tensor pointers are device pointers (HBM), row-major, no padding.
+ *    "f16" is IEEE binary16, "f32" IEEE binary32.
+ *  - `stream` is a hipStream_t (0 = the null stream).  Work is asynchronous
+ *    with respect to the host; order with the stream.
+ *  - One context is not thread-safe; use it from one thread / one stream.
+ *  - Kernels and their workspaces are sized at mlcv_create from the config.
+ */
+#ifndef MLCVLA_H_
+#define MLCVLA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLCV_DTYPE_F16 1
+#define MLCV_QUANT_NONE 0
+#define MLCV_QUANT_Q4F16_1 1
+
+/* Model dimensions: Pi0Config + GemmaExpertConfig
+ * (python/mlc_vla/model/pi0/pi0_config.py:15-170). */
+typedef struct mlcv_config {
+  int32_t vlm_width;     /* expert-0 width (gemma_2b: 2048)              */
+  int32_t vlm_mlp;       /* expert-0 mlp_dim (16384)                     */
+  int32_t ae_width;      /* expert-1 width (gemma_300m: 1024)            */
+  int32_t ae_mlp;        /* expert-1 mlp_dim (4096)                      */
+  int32_t depth;         /* shared depth (18)                            */
+  int32_t num_heads;     /* shared query heads (8)                       */
+  int32_t num_kv_heads;  /* shared kv heads (1)                          */
+  int32_t head_dim;      /* shared head_dim (256)                        */
+  int32_t prefix_len;    /* Pi0Config.prefix_len (968)                   */
+  int32_t suffix_len;    /* Pi0Config.suffix_len = action_horizon        */
+  int32_t action_dim;    /* 32                                           */
+  int32_t num_steps;     /* num_denoise_steps (10)                       */
+  float rms_norm_eps;    /* 1e-6                                         */
+  float rope_theta;      /* 10000                                        */
+  int32_t dtype;         /* MLCV_DTYPE_F16                               */
+  int32_t quant;         /* MLCV_QUANT_NONE or MLCV_QUANT_Q4F16_1        */
+} mlcv_config;
+
+typedef struct mlcv_ctx mlcv_ctx;
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* mlcv_last_error(void);
+
+/* Number of parameter pointers mlcv_bind_params expects for `cfg`:
+ * 18*depth + 11 for fp16 weights (the named_params of the reference's
+ * backbone + action head, pi0_model.py:81-88), one extra pointer per Linear
+ * weight for q4f16_1 (q_weight + q_scale, quant.py:269-288). */
+int mlcv_param_count(const mlcv_config* cfg, int32_t* count);
+
+/* Create / destroy a context (allocates activations and workspaces). */
+int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out);
+int mlcv_destroy(mlcv_ctx* ctx);
+
+/* Bind the parameters, in named_params order, as device pointers.  Replaces the
+ * `params` argument the reference passes on every VM call.  Pointers are
+ * borrowed: the caller keeps the tensors alive and unchanged.  Rebinding
+ * invalidates captured graphs. */
+int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void* stream);
+
+/* Options: MLCV_OPT_USE_GRAPH (default 1): capture step / loop / chunk as hipGraphs.
+ * MLCV_OPT_HOIST_MODULATION (default 1): denoise_loop_kv / chunk compute the time
+ * MLP and all adaRMS modulations of all steps as one M=num_steps GEMM. */
+#define MLCV_OPT_USE_GRAPH 1
+#define MLCV_OPT_HOIST_MODULATION 2
+int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
+
+/* prefill -- Pi0Model.prefill (pi0_model.py:128-140).
+ *   prefix_embs [1, P, vlm_width] f16, prefix_mask [1,1,1,P] f32 (0 / -1e9)
+ *   -> keys [depth, 1, kv, P, head_dim] f32 (post-RoPE), values [..] f16 */
+int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
+                 void* stream);
+
+/* denoise_step_kv -- Pi0Model.denoise_step_kv (pi0_model.py:142-163).
+ *   keys f32 / values f16 as produced by prefill, x_t [1,T,A] f16,
+ *   time_emb [1, ae_width] f16, suffix_cos / suffix_sin [1,T,1,hd/2] f32,
+ *   prefix_mask [1,1,1,P] f32  ->  v_out [1,T,A] f32 */
+int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, const void* x_t, const void* time_emb,
+                         const float* suffix_cos, const float* suffix_sin, const float* prefix_mask, float* v_out,
+                         void* stream);
+
+/* denoise_loop_kv -- Pi0Model.denoise_loop_kv (pi0_model.py:165-194).
+ *   x0 [1,T,A] f32, time_embs [num_steps, ae_width] f16 -> x_out [1,T,A] f32 */
+int mlcv_denoise_loop_kv(mlcv_ctx* ctx, const float* keys, const void* values, const float* x0,
+                         const void* time_embs, const float* suffix_cos, const float* suffix_sin,
+                         const float* prefix_mask, float* x_out, void* stream);
+
+/* One action chunk: prefill followed by denoise_loop_kv, as one graph
+ * (PiZeroRunner.sample_graph, sample.py:165-187, without the host helpers).
+ * keys/values are kept in the context. */
+int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, const float* x0,
+               const void* time_embs, const float* suffix_cos, const float* suffix_sin, float* x_out, void* stream);
+
+/* ---- kernel-level entry points (used by tests and the benchmark) ---------- */
+
+/* Isolated joint attention (gemma_dual.py:97-122 as called from
+ * attn_decode_e1 :255-275): q [Tq, H*hd] f16 already roped and scaled,
+ * prefix K [KV, Sp, hd] (f32 if k_f32 else f16) / V [KV, Sp, hd] f16,
+ * mask [Sp] f32 or NULL, suffix k/v [Ts, KV*hd] f16 already roped
+ * -> out [Tq, H*hd] f16. */
+int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32_t hd, const void* kp,
+                         int32_t k_f32, const void* vp, int32_t Sp, const float* mask, const void* ks,
+                         const void* vs, int32_t Ts, void* out, void* stream);
+
+/* Group quantization q4f16_1 (quant.py:217-266 + pack_weight :65-86):
+ * w [N,K] f16 -> q_weight [N, K/8] u32, q_scale [N, K/32] f16. */
+int mlcv_q4_quantize(const void* w, uint32_t* q_weight, void* q_scale, int32_t N, int32_t K, void* stream);
+
+/* Dequantization (quant.py:176-193): -> w [N,K] f16. */
+int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, int32_t N, int32_t K, void* stream);
+
+/* Linear y[M,N] = x[M,K] . W[N,K]^T (+ bias) in f16 with f32 accumulation, W
+ * either f16 (w) or q4f16_1 (q_weight, q_scale) -- nn.Linear / GroupQuantizeLinear
+ * (quant.py:301-325).  Runs the skinny MFMA GEMM of the denoise step. */
+int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,
+                const void* bias, void* y, int32_t N, void* stream);
+
+/* Enqueue `iters` launches of one operation of denoise_step_kv on `stream`, on the
+ * context's current buffers (benchmarking / profiling only; no counterpart in the
+ * reference).  `layer` selects the decoder layer; `keys` / `values` are needed for
+ * MLCV_OP_ATTENTION.  The results are the op's normal outputs. */
+#define MLCV_OP_TIME_MOD 0   /* time MLP (2 GEMVs) + all 2*depth+1 adaRMS modulations */
+#define MLCV_OP_MODULATION 1 /* the modulation GEMV alone (3*ae_width x (2*depth+1) rows) */
+#define MLCV_OP_QKV 2        /* adaRMS + q/k/v projections */
+#define MLCV_OP_ATTENTION 3  /* joint attention (+ split combine) */
+#define MLCV_OP_OPROJ 4      /* o_proj + gated residual */
+#define MLCV_OP_GATEUP 5     /* adaRMS + gate_up + GeGLU */
+#define MLCV_OP_DOWN 6       /* down + gated residual */
+#define MLCV_OP_HEAD 7       /* final adaRMS + action_out_proj */
+int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLCVLA_H_ */

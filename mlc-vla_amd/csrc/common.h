@@ -1,0 +1,99 @@
+// Shared device/host helpers for the gfx950 pi0.5 denoise library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <string>
+
+namespace mlcv {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ---- error reporting (host) ------------------------------------------------
+void set_error(const std::string& msg);
+const char* get_error();
+
+#define MLCV_HIP(expr)                                                               \
+  do {                                                                               \
+    hipError_t _e = (expr);                                                          \
+    if (_e != hipSuccess) {                                                          \
+      ::mlcv::set_error(std::string(#expr) + " failed: " + hipGetErrorString(_e) +   \
+                        " (" __FILE__ ":" + std::to_string(__LINE__) + ")");         \
+      return -1;                                                                     \
+    }                                                                                \
+  } while (0)
+
+#define MLCV_REQUIRE(cond, msg)                                                      \
+  do {                                                                               \
+    if (!(cond)) {                                                                   \
+      ::mlcv::set_error(std::string("invalid argument: ") + (msg));                  \
+      return -2;                                                                     \
+    }                                                                                \
+  } while (0)
+
+#define MLCV_TRY(expr)                                                               \
+  do {                                                                               \
+    int _r = (expr);                                                                 \
+    if (_r != 0) return _r;                                                          \
+  } while (0)
+
+// ---- device numerics helpers ----------------------------------------------
+// fp16 <-> fp32 with IEEE round-to-nearest-even (v_cvt_f16_f32 / v_cvt_f32_f16).
+__device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }
+__device__ __forceinline__ _Float16 f2h(float f) { return (_Float16)f; }
+
+// model-dtype (fp16) arithmetic: one rounding per operation.
+__device__ __forceinline__ _Float16 hadd(_Float16 a, _Float16 b) { return f2h(h2f(a) + h2f(b)); }
+__device__ __forceinline__ _Float16 hmul(_Float16 a, _Float16 b) { return f2h(h2f(a) * h2f(b)); }
+
+// x + dt * v with two roundings (product, then sum), never contracted into an fma:
+// the same arithmetic as the float32 host Euler update.
+__device__ __forceinline__ float euler_update(float x, float dt, float v) {
+#pragma clang fp contract(off)
+  const float p = dt * v;
+  return x + p;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;  // sqrt(2/pi)
+  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// wave-level reductions over lanes l, l^16, l^32 (the 4 row groups of a 16x16 MFMA tile)
+__device__ __forceinline__ float xor_max_16_32(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float xor_sum_16_32(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Split an fp32 value into fp16 hi + lo with hi + lo ~= x to ~2^-22 relative
+// (absolute floor: fp16 subnormal spacing 2^-24 on the lo part).
+__device__ __forceinline__ void split_f32(float x, _Float16& hi, _Float16& lo) {
+  hi = f2h(x);
+  lo = f2h(x - h2f(hi));
+}
+
+}  // namespace mlcv

@@ -1,0 +1,916 @@
+// Engine: parameter binding, activation buffers, the ordered kernel sequences of
+// prefill / denoise_step_kv / denoise_loop_kv / chunk, hipGraph capture, and the
+// exported C ABI (include/mlcvla.h).
+#include "kernels.h"
+#include "../../include/mlcvla.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <vector>
+
+namespace mlcv {
+
+static thread_local std::string g_err;
+void set_error(const std::string& m) { g_err = m; }
+const char* get_error() { return g_err.c_str(); }
+
+namespace {
+
+struct Lin {
+  const _Float16* w = nullptr;
+  const uint32_t* qw = nullptr;
+  const _Float16* qs = nullptr;
+  const _Float16* b = nullptr;
+  int N = 0, K = 0;
+};
+
+struct Layer {
+  Lin q[2], k[2], v[2], o[2], gu[2], dn[2], mod_in, mod_post;
+  const _Float16* ln_in0 = nullptr;
+  const _Float16* ln_post0 = nullptr;
+};
+
+struct OpDesc {
+  int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0;
+  bool q4 = false;
+};
+
+struct Graph {
+  hipGraphExec_t exec = nullptr;
+  std::vector<const void*> key;
+};
+
+template <typename T>
+int dalloc(T** p, size_t count, std::vector<void*>& owned) {
+  void* q = nullptr;
+  if (count == 0) count = 1;
+  MLCV_HIP(hipMalloc(&q, count * sizeof(T)));
+  owned.push_back(q);
+  *p = reinterpret_cast<T*>(q);
+  return 0;
+}
+
+}  // namespace
+
+struct Ctx {
+  mlcv_config cfg{};
+  bool q4 = false;
+  int dev = 0;
+  int W0, F0, W1, F1, D, H, KV, HD, P, T, A, NS, NM;
+  bool bound = false;
+  bool use_graph = true, hoist = true;
+
+  std::vector<Layer> layers;
+  Lin final_mod, ain, aout, tin, tout;
+
+  std::vector<void*> owned;       // buffers allocated at create
+  std::vector<void*> bind_owned;  // buffers allocated at bind (q4 -> fp16 prefill weights)
+
+  // suffix path
+  _Float16 *x16, *q, *k, *v, *attn, *h, *cond, *tmp, *mod, *te, *xin16;
+  float *x32, *x0, *vout, *cos, *sin, *mask;
+  // prefill path
+  _Float16 *px, *pxn, *pqkv, *pctx, *ph, *pvalues;
+  float *pcos, *psin, *pkeys;
+  // workspaces
+  float* skws = nullptr;
+  size_t skws_floats = 0;
+  unsigned* counters = nullptr;
+  size_t ncounters = 0;
+  float* attn_ws = nullptr;
+  size_t attn_ws_floats_n = 0;
+  int st_nsplit = 1, st_kps = 32, pf_nsplit = 1, pf_kps = 32;
+
+  SkSeg* d_segs = nullptr;
+  std::vector<SkSeg> h_segs;
+  std::vector<OpDesc> layer_ops;  // 4 per layer: qkv, o, gate_up, down
+  OpDesc op_tin, op_tout, op_mod, op_ain, op_aout;
+
+  hipStream_t cap = nullptr;
+  Graph g_step, g_loop, g_prefill, g_chunk;
+
+  void drop_graphs() {
+    for (Graph* g : {&g_step, &g_loop, &g_prefill, &g_chunk}) {
+      if (g->exec) (void)hipGraphExecDestroy(g->exec);
+      g->exec = nullptr;
+      g->key.clear();
+    }
+  }
+  ~Ctx() {
+    drop_graphs();
+    for (void* p : bind_owned) (void)hipFree(p);
+    for (void* p : owned) (void)hipFree(p);
+    if (cap) (void)hipStreamDestroy(cap);
+    if (d_segs) (void)hipFree(d_segs);
+  }
+};
+
+namespace {
+
+size_t kv_slice(const Ctx& c) { return (size_t)c.KV * c.P * c.HD; }
+
+SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
+  SkOp op{};
+  op.x = x;
+  op.ldx = ldx;
+  op.M = M;
+  op.K = d.K;
+  op.eps = c.cfg.rms_norm_eps;
+  op.epi = d.epi;
+  op.segs = c.d_segs + d.seg_off;
+  op.nseg = d.nseg;
+  op.ntiles = d.ntiles;
+  const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64);
+  op.splitk = p.splitk;
+  op.kper = p.kper;
+  op.ws = c.skws;
+  op.counters = c.counters;
+  return op;
+}
+
+int run_op(const Ctx& c, const OpDesc& d, SkOp op, hipStream_t st) { return sk_launch(op, d.q4, st); }
+
+// ---- time MLP + all adaRMS modulations for M steps --------------------------
+int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st) {
+  MLCV_TRY(run_op(c, c.op_tin, make_op(c, c.op_tin, te, c.W1, M), st));
+  MLCV_TRY(run_op(c, c.op_tout, make_op(c, c.op_tout, c.tmp, c.W1, M), st));
+  MLCV_TRY(run_op(c, c.op_mod, make_op(c, c.op_mod, c.cond, c.W1, M), st));
+  return 0;
+}
+
+// ---- the ops of one decoder layer of the suffix path (modulations in modp) ------
+const _Float16* mod_of(const Ctx& c, const _Float16* modp, int idx) { return modp + (size_t)idx * 3 * c.W1; }
+
+int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRMS (input) + q/k/v
+  const _Float16* m_in = mod_of(c, modp, 2 * L);
+  SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.x16, c.W1, c.T);
+  op.scale = m_in;
+  op.shift = m_in + c.W1;
+  return run_op(c, c.layer_ops[4 * L + 0], op, st);
+}
+
+int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipStream_t st) {
+  AttnArgs a{};
+  a.q = c.q;
+  a.q_ld = c.H * c.HD;
+  a.cos = c.cos;
+  a.sin = c.sin;
+  a.q_scale = 1.0f / std::sqrt((float)c.HD);
+  a.Tq = c.T;
+  a.H = c.H;
+  a.KV = c.KV;
+  a.hd = c.HD;
+  a.kp = keys + L * kv_slice(c);
+  a.kp_f32 = 1;
+  a.vp = values + L * kv_slice(c);
+  a.Sp = c.P;
+  a.mask = c.mask;
+  a.ks = c.k;
+  a.ks_ld = c.KV * c.HD;
+  a.vs = c.v;
+  a.vs_ld = c.KV * c.HD;
+  a.Ts = c.T;
+  a.ks_roped = 0;
+  a.out = c.attn;
+  a.out_ld = c.H * c.HD;
+  a.nsplit = c.st_nsplit;
+  a.kps = c.st_kps;
+  a.rows = c.T * (c.H / c.KV);
+  a.rpad = ((a.rows + 63) / 64) * 64;
+  a.part_o = c.attn_ws;
+  a.part_ml = c.attn_ws + (size_t)c.KV * a.nsplit * a.rpad * c.HD;
+  return attn_launch(a, st);
+}
+
+int enqueue_oproj(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // o_proj + gated residual
+  SkOp op = make_op(c, c.layer_ops[4 * L + 1], c.attn, c.H * c.HD, c.T);
+  op.gate = mod_of(c, modp, 2 * L) + 2 * c.W1;
+  return run_op(c, c.layer_ops[4 * L + 1], op, st);
+}
+
+int enqueue_gateup(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRMS (post) + gate_up + GeGLU
+  const _Float16* m_post = mod_of(c, modp, 2 * L + 1);
+  SkOp op = make_op(c, c.layer_ops[4 * L + 2], c.x16, c.W1, c.T);
+  op.scale = m_post;
+  op.shift = m_post + c.W1;
+  op.geglu_F = c.F1;
+  return run_op(c, c.layer_ops[4 * L + 2], op, st);
+}
+
+int enqueue_down(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // down + gated residual
+  SkOp op = make_op(c, c.layer_ops[4 * L + 3], c.h, c.F1, c.T);
+  op.gate = mod_of(c, modp, 2 * L + 1) + 2 * c.W1;
+  return run_op(c, c.layer_ops[4 * L + 3], op, st);
+}
+
+int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  // final adaRMS + action_out
+  const _Float16* m_fin = mod_of(c, modp, 2 * c.D);
+  SkOp op = make_op(c, c.op_aout, c.x16, c.W1, c.T);
+  op.scale = m_fin;
+  op.shift = m_fin + c.W1;
+  if (euler) {
+    op.epi = EPI_EULER;
+    op.dt = (float)(-1.0 / c.NS);
+    op.x32 = c.x32;
+    op.x16 = c.xin16;
+  }
+  return run_op(c, c.op_aout, op, st);
+}
+
+// ---- one suffix-only velocity evaluation (modulations already in modp) -------
+int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
+                 hipStream_t st) {
+  MLCV_TRY(run_op(c, c.op_ain, make_op(c, c.op_ain, c.xin16, c.A, c.T), st));
+  for (int L = 0; L < c.D; ++L) {
+    MLCV_TRY(enqueue_qkv(c, L, modp, st));
+    MLCV_TRY(enqueue_attn(c, L, keys, values, st));
+    MLCV_TRY(enqueue_oproj(c, L, modp, st));
+    MLCV_TRY(enqueue_gateup(c, L, modp, st));
+    MLCV_TRY(enqueue_down(c, L, modp, st));
+  }
+  return enqueue_head(c, modp, euler, st);
+}
+
+// ---- prefill: expert-0 over the prefix, K/V written per layer ----------------
+int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
+  const int W0 = c.W0, P = c.P, HD = c.HD;
+  const int nq = c.H * HD, nkv = c.KV * HD, nqkv = nq + 2 * nkv;
+  for (int L = 0; L < c.D; ++L) {
+    const Layer& ly = c.layers[L];
+    float* kL = keys + L * kv_slice(c);
+    _Float16* vL = values + L * kv_slice(c);
+    MLCV_TRY(rmsnorm_launch(c.px, ly.ln_in0, c.pxn, P, W0, c.cfg.rms_norm_eps, st));
+    TgArgs g{};
+    g.a = c.pxn;
+    g.lda = W0;
+    g.b0 = ly.q[0].w;
+    g.b1 = ly.k[0].w;
+    g.b2 = ly.v[0].w;
+    g.n1 = nq;
+    g.n2 = nq + nkv;
+    g.ldb = W0;
+    g.c = c.pqkv;
+    g.ldc = nqkv;
+    g.M = P;
+    g.N = nqkv;
+    g.K = W0;
+    g.epi = TG_STORE;
+    MLCV_TRY(tg_launch(g, st));
+    MLCV_TRY(kv_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.KV, HD, kL, vL, st));
+    if (L == c.D - 1) break;  // the last layer's attention / MLP feed no output
+    AttnArgs a{};
+    a.q = c.pqkv;
+    a.q_ld = nqkv;
+    a.cos = c.pcos;
+    a.sin = c.psin;
+    a.q_scale = 1.0f / std::sqrt((float)HD);
+    a.Tq = P;
+    a.H = c.H;
+    a.KV = c.KV;
+    a.hd = HD;
+    a.kp = kL;
+    a.kp_f32 = 1;
+    a.vp = vL;
+    a.Sp = P;
+    a.mask = c.mask;
+    a.Ts = 0;
+    a.out = c.pctx;
+    a.out_ld = nq;
+    a.nsplit = c.pf_nsplit;
+    a.kps = c.pf_kps;
+    a.rows = P * (c.H / c.KV);
+    a.rpad = ((a.rows + 63) / 64) * 64;
+    a.part_o = c.attn_ws;
+    a.part_ml = c.attn_ws + (size_t)c.KV * a.nsplit * a.rpad * HD;
+    MLCV_TRY(attn_launch(a, st));
+    TgArgs o{};
+    o.a = c.pctx;
+    o.lda = nq;
+    o.b0 = o.b1 = o.b2 = ly.o[0].w;
+    o.n1 = o.n2 = W0;
+    o.ldb = nq;
+    o.c = c.px;
+    o.ldc = W0;
+    o.M = P;
+    o.N = W0;
+    o.K = nq;
+    o.epi = TG_RESIDUAL;
+    MLCV_TRY(tg_launch(o, st));
+    MLCV_TRY(rmsnorm_launch(c.px, ly.ln_post0, c.pxn, P, W0, c.cfg.rms_norm_eps, st));
+    TgArgs gu{};
+    gu.a = c.pxn;
+    gu.lda = W0;
+    gu.b0 = gu.b1 = gu.b2 = ly.gu[0].w;
+    gu.n1 = gu.n2 = 2 * c.F0;
+    gu.ldb = W0;
+    gu.c = c.ph;
+    gu.ldc = c.F0;
+    gu.M = P;
+    gu.N = c.F0;
+    gu.K = W0;
+    gu.epi = TG_GEGLU;
+    gu.F = c.F0;
+    MLCV_TRY(tg_launch(gu, st));
+    TgArgs dn{};
+    dn.a = c.ph;
+    dn.lda = c.F0;
+    dn.b0 = dn.b1 = dn.b2 = ly.dn[0].w;
+    dn.n1 = dn.n2 = W0;
+    dn.ldb = c.F0;
+    dn.c = c.px;
+    dn.ldc = W0;
+    dn.M = P;
+    dn.N = W0;
+    dn.K = c.F0;
+    dn.epi = TG_RESIDUAL;
+    MLCV_TRY(tg_launch(dn, st));
+  }
+  return 0;
+}
+
+int enqueue_loop(Ctx& c, const float* keys, const _Float16* values, hipStream_t st) {
+  const size_t modstep = (size_t)c.NM * 3 * c.W1;
+  MLCV_TRY(euler_init_launch(c.x0, c.x32, c.xin16, c.T * c.A, st));
+  if (c.hoist) MLCV_TRY(enqueue_time_mod(c, c.te, c.NS, st));
+  for (int i = 0; i < c.NS; ++i) {
+    if (c.hoist) {
+      MLCV_TRY(enqueue_step(c, keys, values, c.mod + i * modstep, true, st));
+    } else {
+      MLCV_TRY(enqueue_time_mod(c, c.te + (size_t)i * c.W1, 1, st));
+      MLCV_TRY(enqueue_step(c, keys, values, c.mod, true, st));
+    }
+  }
+  return 0;
+}
+
+int run_graph(Ctx& c, Graph& g, const std::vector<const void*>& key, const std::function<int(hipStream_t)>& body,
+              hipStream_t user) {
+  if (!c.use_graph) return body(user);
+  if (!g.exec || g.key != key) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    g.exec = nullptr;
+    MLCV_HIP(hipStreamBeginCapture(c.cap, hipStreamCaptureModeThreadLocal));
+    const int r = body(c.cap);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(c.cap, &graph);
+    if (r != 0) {
+      if (e == hipSuccess && graph) (void)hipGraphDestroy(graph);
+      return r;
+    }
+    MLCV_HIP(e);
+    const hipError_t ie = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    MLCV_HIP(ie);
+    g.key = key;
+  }
+  MLCV_HIP(hipGraphLaunch(g.exec, user));
+  return 0;
+}
+
+int seg_ops(Ctx& c, OpDesc& d, const std::vector<SkSeg>& segs, int K, int epi, bool q4, int tile_rows) {
+  d.seg_off = (int)c.h_segs.size();
+  d.nseg = (int)segs.size();
+  d.K = K;
+  d.epi = epi;
+  d.q4 = q4;
+  int t = 0;
+  for (SkSeg s : segs) {
+    s.tile0 = t;
+    t += (s.n + tile_rows - 1) / tile_rows;
+    c.h_segs.push_back(s);
+  }
+  d.ntiles = t;
+  return 0;
+}
+
+SkSeg seg_of(const Lin& l, void* out, int n, int ldo) {
+  SkSeg s{};
+  s.w = l.w;
+  s.qw = l.qw;
+  s.qs = l.qs;
+  s.bias = l.b;
+  s.out = out;
+  s.n = n;
+  s.ldo = ldo;
+  return s;
+}
+
+}  // namespace
+}  // namespace mlcv
+
+using namespace mlcv;
+
+struct mlcv_ctx {
+  Ctx c;
+};
+
+extern "C" {
+
+const char* mlcv_last_error(void) { return get_error(); }
+
+int mlcv_param_count(const mlcv_config* cfg, int32_t* count) {
+  MLCV_REQUIRE(cfg && count, "null argument");
+  const int per_layer_lin = 12 + 2;  // 8 attn + 4 mlp + 2 modulation linears
+  const int n_fp = 18 * cfg->depth + 11;
+  const int n_lin = per_layer_lin * cfg->depth + 1 + 4;  // + final modulation + 4 head linears
+  *count = cfg->quant == MLCV_QUANT_Q4F16_1 ? n_fp + n_lin : n_fp;
+  return 0;
+}
+
+int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
+  MLCV_REQUIRE(cfg && out, "null argument");
+  MLCV_REQUIRE(cfg->dtype == MLCV_DTYPE_F16, "only float16 models are supported on gfx950 in this build");
+  MLCV_REQUIRE(cfg->quant == MLCV_QUANT_NONE || cfg->quant == MLCV_QUANT_Q4F16_1, "unknown quantization");
+  const int hd = cfg->head_dim;
+  MLCV_REQUIRE(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256, "head_dim must be 16/32/64/128/256");
+  MLCV_REQUIRE(cfg->num_kv_heads == 1 || cfg->num_kv_heads == cfg->num_heads, "num_kv_heads must be 1 or num_heads");
+  MLCV_REQUIRE(cfg->vlm_width % 32 == 0 && cfg->ae_width % 32 == 0, "widths must be multiples of 32");
+  MLCV_REQUIRE(cfg->ae_mlp % 32 == 0 && cfg->vlm_mlp % 64 == 0, "mlp dims: ae % 32, vlm % 64");
+  MLCV_REQUIRE(cfg->action_dim % 32 == 0, "action_dim must be a multiple of 32");
+  MLCV_REQUIRE((cfg->num_heads * hd) % 32 == 0, "num_heads * head_dim must be a multiple of 32");
+  MLCV_REQUIRE(cfg->depth >= 1 && cfg->prefix_len >= 1 && cfg->suffix_len >= 1 && cfg->num_steps >= 1,
+               "depth / lengths / steps must be positive");
+  MLCV_REQUIRE(cfg->num_steps <= 64, "num_steps must be <= 64");
+
+  auto* h = new (std::nothrow) mlcv_ctx();
+  if (!h) {
+    set_error("out of host memory");
+    return -1;
+  }
+  Ctx& c = h->c;
+  c.cfg = *cfg;
+  c.q4 = cfg->quant == MLCV_QUANT_Q4F16_1;
+  c.W0 = cfg->vlm_width;
+  c.F0 = cfg->vlm_mlp;
+  c.W1 = cfg->ae_width;
+  c.F1 = cfg->ae_mlp;
+  c.D = cfg->depth;
+  c.H = cfg->num_heads;
+  c.KV = cfg->num_kv_heads;
+  c.HD = hd;
+  c.P = cfg->prefix_len;
+  c.T = cfg->suffix_len;
+  c.A = cfg->action_dim;
+  c.NS = cfg->num_steps;
+  c.NM = 2 * c.D + 1;
+
+  auto fail = [&](int r) {
+    delete h;
+    return r;
+  };
+  if (hipGetDevice(&c.dev) != hipSuccess) {
+    set_error("no HIP device");
+    return fail(-1);
+  }
+  const int T = c.T, W1 = c.W1, nq = c.H * hd, nkv = c.KV * hd;
+  std::vector<void*>& o = c.owned;
+  int r = 0;
+#define ALLOC(ptr, n) \
+  if ((r = dalloc(&(ptr), (size_t)(n), o)) != 0) return fail(r)
+  ALLOC(c.x16, T * W1);
+  ALLOC(c.q, T * nq);
+  ALLOC(c.k, T * nkv);
+  ALLOC(c.v, T * nkv);
+  ALLOC(c.attn, T * nq);
+  ALLOC(c.h, (size_t)T * c.F1);
+  ALLOC(c.cond, c.NS * W1);
+  ALLOC(c.tmp, c.NS * W1);
+  ALLOC(c.mod, (size_t)c.NS * c.NM * 3 * W1);
+  ALLOC(c.te, c.NS * W1);
+  ALLOC(c.xin16, T * c.A);
+  ALLOC(c.x32, T * c.A);
+  ALLOC(c.x0, T * c.A);
+  ALLOC(c.vout, T * c.A);
+  ALLOC(c.cos, T * hd / 2);
+  ALLOC(c.sin, T * hd / 2);
+  ALLOC(c.mask, c.P);
+  const size_t P = c.P;
+  ALLOC(c.px, P * c.W0);
+  ALLOC(c.pxn, P * c.W0);
+  ALLOC(c.pqkv, P * (nq + 2 * nkv));
+  ALLOC(c.pctx, P * nq);
+  ALLOC(c.ph, P * c.F0);
+  ALLOC(c.pcos, P * hd / 2);
+  ALLOC(c.psin, P * hd / 2);
+  ALLOC(c.pkeys, (size_t)c.D * kv_slice(c));
+  ALLOC(c.pvalues, (size_t)c.D * kv_slice(c));
+
+  // prefix RoPE tables: radians = pos / theta^((2/hd) i) in float64, cast to float32
+  {
+    std::vector<float> hc(P * hd / 2), hs(P * hd / 2);
+    for (size_t p = 0; p < P; ++p)
+      for (int i = 0; i < hd / 2; ++i) {
+        const double ts = std::pow((double)cfg->rope_theta, (2.0 / hd) * i);
+        const double rad = (double)p / ts;
+        hc[p * (hd / 2) + i] = (float)std::cos(rad);
+        hs[p * (hd / 2) + i] = (float)std::sin(rad);
+      }
+    if (hipMemcpy(c.pcos, hc.data(), hc.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c.psin, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("copy of rope tables failed");
+      return fail(-1);
+    }
+  }
+  // attention split plans and workspace
+  const int st_rows = T * (c.H / c.KV), pf_rows = c.P * (c.H / c.KV);
+  attn_plan(st_rows, c.P + T, 256, &c.st_nsplit, &c.st_kps);
+  attn_plan(pf_rows, c.P, 256, &c.pf_nsplit, &c.pf_kps);
+  c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
+                                attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
+  ALLOC(c.attn_ws, c.attn_ws_floats_n);
+
+  // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
+  const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
+  struct Shape {
+    int ntiles, K, mb;
+  };
+  std::vector<Shape> shapes = {
+      {(nq + 63) / 64 + 2 * ((nkv + 63) / 64), W1, mb_t},  // qkv
+      {(W1 + 63) / 64, nq, mb_t},                         // o
+      {c.F1 / 32, W1, mb_t},                              // gate_up
+      {(W1 + 63) / 64, c.F1, mb_t},                       // down
+      {(W1 + 63) / 64, W1, mb_s},                         // time mlp
+      {c.NM * ((3 * W1 + 63) / 64), W1, mb_s},            // modulation
+      {(W1 + 63) / 64, c.A, mb_t},                        // action_in
+      {(c.A + 63) / 64, W1, mb_t},                        // action_out
+  };
+  for (const Shape& s : shapes) {
+    const SkPlan p = sk_plan(s.ntiles, s.K, s.mb);
+    c.skws_floats = std::max(c.skws_floats, sk_ws_floats(s.ntiles, s.mb, p));
+    c.ncounters = std::max(c.ncounters, (size_t)s.ntiles * s.mb);
+  }
+  ALLOC(c.skws, c.skws_floats);
+  ALLOC(c.counters, c.ncounters);
+#undef ALLOC
+  if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
+      hipStreamCreateWithFlags(&c.cap, hipStreamNonBlocking) != hipSuccess) {
+    set_error("context setup failed");
+    return fail(-1);
+  }
+  if (hipDeviceSynchronize() != hipSuccess) {
+    set_error("context setup sync failed");
+    return fail(-1);
+  }
+  *out = h;
+  return 0;
+}
+
+int mlcv_destroy(mlcv_ctx* ctx) {
+  if (!ctx) return 0;
+  (void)hipDeviceSynchronize();
+  delete ctx;
+  return 0;
+}
+
+int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
+  MLCV_REQUIRE(ctx, "null context");
+  Ctx& c = ctx->c;
+  if (key == MLCV_OPT_USE_GRAPH) c.use_graph = value != 0;
+  else if (key == MLCV_OPT_HOIST_MODULATION) c.hoist = value != 0;
+  else MLCV_REQUIRE(false, "unknown option");
+  c.drop_graphs();
+  return 0;
+}
+
+int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void* stream) {
+  MLCV_REQUIRE(ctx && ptrs, "null argument");
+  Ctx& c = ctx->c;
+  int32_t want = 0;
+  MLCV_TRY(mlcv_param_count(&c.cfg, &want));
+  MLCV_REQUIRE(count == want, "parameter count mismatch (expected " + std::to_string(want) + ")");
+  for (int i = 0; i < count; ++i) MLCV_REQUIRE(ptrs[i] != nullptr, "null parameter pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  c.drop_graphs();
+  MLCV_HIP(hipStreamSynchronize(st));
+  for (void* p : c.bind_owned) (void)hipFree(p);
+  c.bind_owned.clear();
+
+  int idx = 0;
+  auto half_ptr = [&]() { return reinterpret_cast<const _Float16*>(ptrs[idx++]); };
+  auto lin = [&](Lin& l, int N, int K, bool bias) {
+    l = Lin{};
+    l.N = N;
+    l.K = K;
+    if (c.q4) {
+      l.qw = reinterpret_cast<const uint32_t*>(ptrs[idx++]);
+      l.qs = half_ptr();
+    } else {
+      l.w = half_ptr();
+    }
+    if (bias) l.b = half_ptr();
+  };
+  const int nq = c.H * c.HD, nkv = c.KV * c.HD;
+  const int widths[2] = {c.W0, c.W1}, mlps[2] = {c.F0, c.F1};
+  c.layers.assign(c.D, Layer{});
+  for (int L = 0; L < c.D; ++L) {
+    Layer& ly = c.layers[L];
+    for (int e = 0; e < 2; ++e) {
+      lin(ly.q[e], nq, widths[e], false);
+      lin(ly.k[e], nkv, widths[e], false);
+      lin(ly.v[e], nkv, widths[e], false);
+      lin(ly.o[e], widths[e], nq, false);
+    }
+    for (int e = 0; e < 2; ++e) {
+      lin(ly.gu[e], 2 * mlps[e], widths[e], false);
+      lin(ly.dn[e], widths[e], mlps[e], false);
+    }
+    ly.ln_in0 = half_ptr();
+    lin(ly.mod_in, 3 * c.W1, c.W1, true);
+    ly.ln_post0 = half_ptr();
+    lin(ly.mod_post, 3 * c.W1, c.W1, true);
+  }
+  idx++;  // backbone.final_norm.0.weight (unused on the M1 path)
+  lin(c.final_mod, 3 * c.W1, c.W1, true);
+  lin(c.ain, c.W1, c.A, true);
+  lin(c.aout, c.A, c.W1, true);
+  lin(c.tin, c.W1, c.W1, true);
+  lin(c.tout, c.W1, c.W1, true);
+  MLCV_REQUIRE(idx == count, "internal: parameter walk mismatch");
+
+  // q4: expert-0 (prefill, compute-bound) runs on an fp16 copy dequantized once
+  if (c.q4) {
+    for (int L = 0; L < c.D; ++L) {
+      Layer& ly = c.layers[L];
+      Lin* ls[6] = {&ly.q[0], &ly.k[0], &ly.v[0], &ly.o[0], &ly.gu[0], &ly.dn[0]};
+      for (Lin* l : ls) {
+        _Float16* w = nullptr;
+        MLCV_TRY(dalloc(&w, (size_t)l->N * l->K, c.bind_owned));
+        MLCV_TRY(q4_dequant_launch(l->qw, l->qs, w, l->N, l->K, st));
+        l->w = w;
+      }
+    }
+  }
+
+  // skinny op tables
+  c.h_segs.clear();
+  c.layer_ops.assign(4 * c.D, OpDesc{});
+  const int W1 = c.W1;
+  for (int L = 0; L < c.D; ++L) {
+    Layer& ly = c.layers[L];
+    OpDesc* ops = &c.layer_ops[4 * L];
+    seg_ops(c, ops[0],
+            {seg_of(ly.q[1], c.q, nq, nq), seg_of(ly.k[1], c.k, nkv, nkv), seg_of(ly.v[1], c.v, nkv, nkv)}, W1,
+            EPI_STORE, c.q4, 64);
+    seg_ops(c, ops[1], {seg_of(ly.o[1], c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, 64);
+    seg_ops(c, ops[2], {seg_of(ly.gu[1], c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, 32);
+    seg_ops(c, ops[3], {seg_of(ly.dn[1], c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, 64);
+  }
+  seg_ops(c, c.op_tin, {seg_of(c.tin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64);
+  seg_ops(c, c.op_tout, {seg_of(c.tout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64);
+  {
+    std::vector<SkSeg> ms;
+    const int ldo = c.NM * 3 * W1;
+    for (int L = 0; L < c.D; ++L) {
+      ms.push_back(seg_of(c.layers[L].mod_in, c.mod + (size_t)(2 * L) * 3 * W1, 3 * W1, ldo));
+      ms.push_back(seg_of(c.layers[L].mod_post, c.mod + (size_t)(2 * L + 1) * 3 * W1, 3 * W1, ldo));
+    }
+    ms.push_back(seg_of(c.final_mod, c.mod + (size_t)(2 * c.D) * 3 * W1, 3 * W1, ldo));
+    seg_ops(c, c.op_mod, ms, W1, EPI_STORE, c.q4, 64);
+  }
+  seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, 64);
+  seg_ops(c, c.op_aout, {seg_of(c.aout, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, 64);
+
+  if (c.d_segs) {
+    (void)hipFree(c.d_segs);
+    c.d_segs = nullptr;
+  }
+  MLCV_HIP(hipMalloc(&c.d_segs, c.h_segs.size() * sizeof(SkSeg)));
+  MLCV_HIP(hipMemcpy(c.d_segs, c.h_segs.data(), c.h_segs.size() * sizeof(SkSeg), hipMemcpyHostToDevice));
+  MLCV_HIP(hipStreamSynchronize(st));
+  c.bound = true;
+  return 0;
+}
+
+int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
+                 void* stream) {
+  MLCV_REQUIRE(ctx && prefix_embs && prefix_mask && keys && values, "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  MLCV_HIP(hipMemcpyAsync(c.px, prefix_embs, (size_t)c.P * c.W0 * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.mask, prefix_mask, (size_t)c.P * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_TRY(run_graph(c, c.g_prefill, {}, [&](hipStream_t s) { return enqueue_prefill(c, c.pkeys, c.pvalues, s); },
+                     st));
+  const size_t n = (size_t)c.D * kv_slice(c);
+  MLCV_HIP(hipMemcpyAsync(keys, c.pkeys, n * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(values, c.pvalues, n * 2, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+static int copy_suffix_inputs(Ctx& c, const float* cos, const float* sin, const float* mask, hipStream_t st) {
+  const size_t half = c.HD / 2;
+  MLCV_HIP(hipMemcpyAsync(c.cos, cos, (size_t)c.T * half * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.sin, sin, (size_t)c.T * half * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.mask, mask, (size_t)c.P * 4, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, const void* x_t, const void* time_emb,
+                         const float* suffix_cos, const float* suffix_sin, const float* prefix_mask, float* v_out,
+                         void* stream) {
+  MLCV_REQUIRE(ctx && keys && values && x_t && time_emb && suffix_cos && suffix_sin && prefix_mask && v_out,
+               "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  MLCV_HIP(hipMemcpyAsync(c.xin16, x_t, (size_t)c.T * c.A * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.te, time_emb, (size_t)c.W1 * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  const _Float16* vals = reinterpret_cast<const _Float16*>(values);
+  MLCV_TRY(run_graph(c, c.g_step, {keys, values},
+                     [&](hipStream_t s) {
+                       MLCV_TRY(enqueue_time_mod(c, c.te, 1, s));
+                       return enqueue_step(c, keys, vals, c.mod, false, s);
+                     },
+                     st));
+  MLCV_HIP(hipMemcpyAsync(v_out, c.vout, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int mlcv_denoise_loop_kv(mlcv_ctx* ctx, const float* keys, const void* values, const float* x0,
+                         const void* time_embs, const float* suffix_cos, const float* suffix_sin,
+                         const float* prefix_mask, float* x_out, void* stream) {
+  MLCV_REQUIRE(ctx && keys && values && x0 && time_embs && suffix_cos && suffix_sin && prefix_mask && x_out,
+               "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  MLCV_HIP(hipMemcpyAsync(c.x0, x0, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.te, time_embs, (size_t)c.NS * c.W1 * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  const _Float16* vals = reinterpret_cast<const _Float16*>(values);
+  MLCV_TRY(run_graph(c, c.g_loop, {keys, values}, [&](hipStream_t s) { return enqueue_loop(c, keys, vals, s); },
+                     st));
+  MLCV_HIP(hipMemcpyAsync(x_out, c.x32, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, const float* x0,
+               const void* time_embs, const float* suffix_cos, const float* suffix_sin, float* x_out, void* stream) {
+  MLCV_REQUIRE(ctx && prefix_embs && prefix_mask && x0 && time_embs && suffix_cos && suffix_sin && x_out,
+               "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  MLCV_HIP(hipMemcpyAsync(c.px, prefix_embs, (size_t)c.P * c.W0 * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.x0, x0, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipMemcpyAsync(c.te, time_embs, (size_t)c.NS * c.W1 * 2, hipMemcpyDeviceToDevice, st));
+  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  MLCV_TRY(run_graph(c, c.g_chunk, {},
+                     [&](hipStream_t s) {
+                       MLCV_TRY(enqueue_prefill(c, c.pkeys, c.pvalues, s));
+                       return enqueue_loop(c, c.pkeys, c.pvalues, s);
+                     },
+                     st));
+  MLCV_HIP(hipMemcpyAsync(x_out, c.x32, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
+                  void* stream) {
+  MLCV_REQUIRE(ctx && iters >= 0, "bad argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  MLCV_REQUIRE(layer >= 0 && layer < c.D, "layer out of range");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const _Float16* vals = reinterpret_cast<const _Float16*>(values);
+  if (op == MLCV_OP_ATTENTION) MLCV_REQUIRE(keys && values, "attention needs keys and values");
+  for (int i = 0; i < iters; ++i) {
+    switch (op) {
+      case MLCV_OP_TIME_MOD: MLCV_TRY(enqueue_time_mod(c, c.te, 1, st)); break;
+      case MLCV_OP_MODULATION: MLCV_TRY(run_op(c, c.op_mod, make_op(c, c.op_mod, c.cond, c.W1, 1), st)); break;
+      case MLCV_OP_QKV: MLCV_TRY(enqueue_qkv(c, layer, c.mod, st)); break;
+      case MLCV_OP_ATTENTION: MLCV_TRY(enqueue_attn(c, layer, keys, vals, st)); break;
+      case MLCV_OP_OPROJ: MLCV_TRY(enqueue_oproj(c, layer, c.mod, st)); break;
+      case MLCV_OP_GATEUP: MLCV_TRY(enqueue_gateup(c, layer, c.mod, st)); break;
+      case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;
+      case MLCV_OP_HEAD: MLCV_TRY(enqueue_head(c, c.mod, false, st)); break;
+      default: MLCV_REQUIRE(false, "unknown op");
+    }
+  }
+  return 0;
+}
+
+// ---- kernel-level entry points ------------------------------------------------
+
+namespace {
+struct Scratch {
+  std::mutex mu;
+  float* ws = nullptr;
+  size_t ws_n = 0;
+  unsigned* counters = nullptr;
+  size_t counters_n = 0;
+  SkSeg* seg = nullptr;
+};
+Scratch g_scratch;
+
+int scratch_reserve(size_t ws_n, size_t counters_n) {
+  if (!g_scratch.seg) MLCV_HIP(hipMalloc(&g_scratch.seg, sizeof(SkSeg)));
+  if (ws_n > g_scratch.ws_n) {
+    if (g_scratch.ws) MLCV_HIP(hipFree(g_scratch.ws));
+    MLCV_HIP(hipMalloc(&g_scratch.ws, ws_n * sizeof(float)));
+    g_scratch.ws_n = ws_n;
+  }
+  if (counters_n > g_scratch.counters_n) {
+    if (g_scratch.counters) MLCV_HIP(hipFree(g_scratch.counters));
+    MLCV_HIP(hipMalloc(&g_scratch.counters, counters_n * sizeof(unsigned)));
+    MLCV_HIP(hipMemset(g_scratch.counters, 0, counters_n * sizeof(unsigned)));
+    g_scratch.counters_n = counters_n;
+  }
+  return 0;
+}
+}  // namespace
+
+int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32_t hd, const void* kp,
+                         int32_t k_f32, const void* vp, int32_t Sp, const float* mask, const void* ks,
+                         const void* vs, int32_t Ts, void* out, void* stream) {
+  MLCV_REQUIRE(q && kp && vp && out && Tq > 0 && H > 0 && KV > 0 && Sp >= 0 && Ts >= 0, "bad argument");
+  MLCV_REQUIRE(Ts == 0 || (ks && vs), "suffix k/v missing");
+  MLCV_REQUIRE(Sp + Ts > 0, "no keys");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  AttnArgs a{};
+  a.q = reinterpret_cast<const _Float16*>(q);
+  a.q_ld = H * hd;
+  a.q_scale = 1.0f;
+  a.Tq = Tq;
+  a.H = H;
+  a.KV = KV;
+  a.hd = hd;
+  a.kp = kp;
+  a.kp_f32 = k_f32;
+  a.vp = reinterpret_cast<const _Float16*>(vp);
+  a.Sp = Sp;
+  a.mask = mask;
+  a.ks = reinterpret_cast<const _Float16*>(ks);
+  a.ks_ld = KV * hd;
+  a.vs = reinterpret_cast<const _Float16*>(vs);
+  a.vs_ld = KV * hd;
+  a.Ts = Ts;
+  a.ks_roped = 1;
+  a.out = reinterpret_cast<_Float16*>(out);
+  a.out_ld = H * hd;
+  a.rows = Tq * (H / KV);
+  a.rpad = ((a.rows + 63) / 64) * 64;
+  attn_plan(a.rows, Sp + Ts, 256, &a.nsplit, &a.kps);
+  std::lock_guard<std::mutex> lk(g_scratch.mu);
+  const size_t need = attn_ws_floats(KV, a.rows, hd, a.nsplit);
+  MLCV_TRY(scratch_reserve(need, 1));
+  a.part_o = g_scratch.ws;
+  a.part_ml = g_scratch.ws + (size_t)KV * a.nsplit * a.rpad * hd;
+  return attn_launch(a, st);
+}
+
+int mlcv_q4_quantize(const void* w, uint32_t* q_weight, void* q_scale, int32_t N, int32_t K, void* stream) {
+  MLCV_REQUIRE(w && q_weight && q_scale && N > 0 && K > 0, "bad argument");
+  return q4_quantize_launch(reinterpret_cast<const _Float16*>(w), q_weight, reinterpret_cast<_Float16*>(q_scale), N,
+                            K, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, int32_t N, int32_t K, void* stream) {
+  MLCV_REQUIRE(w && q_weight && q_scale && N > 0 && K > 0, "bad argument");
+  return q4_dequant_launch(q_weight, reinterpret_cast<const _Float16*>(q_scale), reinterpret_cast<_Float16*>(w), N,
+                           K, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,
+                const void* bias, void* y, int32_t N, void* stream) {
+  MLCV_REQUIRE(x && y && M > 0 && K > 0 && N > 0, "bad argument");
+  MLCV_REQUIRE((w != nullptr) != (q_weight != nullptr && q_scale != nullptr), "pass either w or q_weight+q_scale");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  SkSeg s{};
+  s.w = reinterpret_cast<const _Float16*>(w);
+  s.qw = q_weight;
+  s.qs = reinterpret_cast<const _Float16*>(q_scale);
+  s.bias = reinterpret_cast<const _Float16*>(bias);
+  s.out = y;
+  s.n = N;
+  s.ldo = N;
+  s.tile0 = 0;
+  const int ntiles = (N + 63) / 64, mb = (M + 63) / 64;
+  const SkPlan p = sk_plan(ntiles, K, mb);
+  std::lock_guard<std::mutex> lk(g_scratch.mu);
+  MLCV_TRY(scratch_reserve(sk_ws_floats(ntiles, mb, p), (size_t)ntiles * mb));
+  MLCV_HIP(hipStreamSynchronize(st));
+  MLCV_HIP(hipMemcpy(g_scratch.seg, &s, sizeof(SkSeg), hipMemcpyHostToDevice));
+  SkOp op{};
+  op.x = reinterpret_cast<const _Float16*>(x);
+  op.ldx = K;
+  op.M = M;
+  op.K = K;
+  op.epi = EPI_STORE;
+  op.segs = g_scratch.seg;
+  op.nseg = 1;
+  op.ntiles = ntiles;
+  op.splitk = p.splitk;
+  op.kper = p.kper;
+  op.ws = g_scratch.ws;
+  op.counters = g_scratch.counters;
+  MLCV_TRY(sk_launch(op, q_weight != nullptr, st));
+  MLCV_HIP(hipStreamSynchronize(st));
+  return 0;
+}
+
+}  // extern "C"

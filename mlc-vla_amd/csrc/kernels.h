@@ -1,0 +1,126 @@
+// Kernel launch interfaces shared by the engine (host side).
+#pragma once
+
+#include "common.h"
+
+namespace mlcv {
+
+// ---------------------------------------------------------------------------
+// skinny GEMM: Y[M, N] = X[M, K] . W[N, K]^T for M <= 64 per m-block, fp16 or
+// q4f16_1 weights, fp32 accumulation on MFMA 16x16x32, fused prologue/epilogue.
+// ---------------------------------------------------------------------------
+enum SkEpi : int {
+  EPI_STORE = 0,       // out = fp16(acc) [+ fp16 bias]
+  EPI_STORE_SILU = 1,  // out = fp16(silu(fp16(acc) + bias))
+  EPI_GATED_RES = 2,   // x = fp16(x + fp16(fp16(acc) * gate))      (in place)
+  EPI_GEGLU = 3,       // h = fp16(fp16(gelu(fp16(acc_gate))) * fp16(acc_up))
+  EPI_VOUT = 4,        // v = f32(fp16(fp16(acc) + bias))
+  EPI_EULER = 5,       // x32 += dt * f32(fp16(fp16(acc) + bias)); x16 = fp16(x32)
+};
+
+// One weight matrix (segment) of a skinny GEMM launch; tiles of 64 output rows.
+struct SkSeg {
+  const _Float16* w;     // [n][K] fp16 row-major (null for q4)
+  const uint32_t* qw;    // [n][K/8] packed nibbles (q4)
+  const _Float16* qs;    // [n][K/32] fp16 group scales (q4)
+  const _Float16* bias;  // [n] or null
+  void* out;             // output base (element type depends on the epilogue)
+  int n;                 // output rows of this segment
+  int tile0;             // first tile id of this segment
+  int ldo;               // output stride between m rows (elements)
+  int m_stride_out;      // unused, reserved
+};
+
+struct SkOp {
+  const _Float16* x;     // X [M][ldx]
+  int ldx, M, K;
+  int mx_stride;         // per m-block stride of the modulation (0 = shared)
+  // adaRMS prologue: xn = fp16((x / sqrt(mean(x^2)+eps)) * (1 + scale) + shift)
+  const _Float16* scale; // [K] or null (no prologue)
+  const _Float16* shift; // [K]
+  float eps;
+  int epi;
+  const _Float16* gate;  // [N] (EPI_GATED_RES)
+  int geglu_F;           // EPI_GEGLU: rows [0,F) gate, [F,2F) up
+  const SkSeg* segs;     // device table
+  int nseg, ntiles;
+  int splitk, kper;
+  float* ws;             // split-K partials
+  unsigned* counters;    // per (tile, m-block), zero between launches
+  float dt;              // EPI_EULER
+  float* x32;            // EPI_EULER state [M][ldo]
+  _Float16* x16;         // EPI_EULER fp16 copy
+};
+
+struct SkPlan {
+  int splitk, kper;
+};
+SkPlan sk_plan(int ntiles, int K, int mblocks);
+size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p);
+int sk_launch(const SkOp& op, bool q4, hipStream_t st);
+
+// q4f16_1 helpers
+int q4_quantize_launch(const _Float16* w, uint32_t* qw, _Float16* qs, int N, int K, hipStream_t st);
+int q4_dequant_launch(const uint32_t* qw, const _Float16* qs, _Float16* out, int N, int K, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// joint attention (suffix-over-cached-prefix, MQA/GQA broadcast), split-KV
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+  const _Float16* q;     // raw q [Tq][q_ld], head h at h*hd
+  int q_ld;
+  const float* cos;      // [Tq][hd/2] rope for q (and suffix k); null = already roped
+  const float* sin;
+  float q_scale;         // applied after rope
+  int Tq, H, KV, hd;
+  const void* kp;        // prefix K [KV][Sp][hd], roped; fp32 (kp_f32) or fp16
+  int kp_f32;
+  const _Float16* vp;    // prefix V [KV][Sp][hd]
+  int Sp;
+  const float* mask;     // [Sp] additive, or null
+  const _Float16* ks;    // suffix k raw [Ts][ks_ld] (head kvh at kvh*hd), or null
+  int ks_ld;
+  const _Float16* vs;    // suffix v [Ts][vs_ld]
+  int vs_ld;
+  int Ts;
+  int ks_roped;          // suffix k already roped
+  _Float16* out;         // [Tq][out_ld], head h at h*hd
+  int out_ld;
+  float* part_o;         // [KV][nsplit][Rpad][hd]
+  float* part_ml;        // [KV][nsplit][Rpad][2]
+  int nsplit, kps;       // splits and keys per split (multiple of 32)
+  int rows, rpad;        // rows per kv head (Tq*H/KV) and padded
+};
+void attn_plan(int rows, int keys, int target_blocks, int* nsplit, int* kps);
+size_t attn_ws_floats(int KV, int rows, int hd, int nsplit);
+int attn_launch(const AttnArgs& a, hipStream_t st);
+
+// prefill helpers
+int rmsnorm_launch(const _Float16* x, const _Float16* w, _Float16* out, int rows, int dim, float eps,
+                   hipStream_t st);
+int kv_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin,
+                     int P, int KV, int hd, float* keys, _Float16* values, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// tiled GEMM for prefill: C[M,N] = A[M,K] . B[N,K]^T, MFMA 32x32x16
+// ---------------------------------------------------------------------------
+enum TgEpi : int {
+  TG_STORE = 0,     // C fp16
+  TG_RESIDUAL = 1,  // C = fp16(C + fp16(acc))
+  TG_GEGLU = 2,     // B rows interleaved gate/up per 32-col block; C = h [M][F]
+};
+struct TgArgs {
+  const _Float16* a; int lda;
+  const _Float16* b0; const _Float16* b1; const _Float16* b2;  // up to 3 stacked weight segments
+  int n1, n2;            // segment boundaries in N (b1 rows start at n1, b2 at n2)
+  int ldb;
+  _Float16* c; int ldc;
+  int M, N, K;
+  int epi;
+  int F;                 // TG_GEGLU: up rows offset in b0
+};
+int tg_launch(const TgArgs& a, hipStream_t st);
+
+int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStream_t st);
+
+}  // namespace mlcv

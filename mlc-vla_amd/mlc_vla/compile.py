@@ -1,0 +1,65 @@
+"""Build entry (drop-in for mlc_vla.compile).
+
+In the reference, ``compile_model`` lowers the TVM graph and JIT-compiles the
+kernels (python/mlc_vla/compile.py:99-133).  Here the kernels are prebuilt for
+gfx950 (``libmlcvla_hip.so``); ``compile_model`` validates the configuration and
+returns the executable description plus the ``named_params`` list.
+"""
+
+from __future__ import annotations
+
+import warnings
+
+from .model.pi0.pi0_model import KV_FUNCS, named_params
+from .runtime import Device, Executable, device
+
+GPU_TARGETS = ("rocm", "hip", "cuda", "gfx950")
+
+
+def _target_kind(target: str) -> str:
+    kind = str(target).split()[0].split("-")[0].lower()
+    if kind in GPU_TARGETS:
+        return "rocm"
+    raise NotImplementedError(
+        f"target {target!r}: this build runs on MI355X (gfx950) only; there is no CPU backend")
+
+
+def cublas_available() -> bool:
+    """The cuBLAS BYOC path of the reference does not exist on ROCm."""
+    return False
+
+
+def resolve_cublas(cublas, target_kind: str) -> bool:
+    """Tri-state cuBLAS switch of the reference (compile.py:55-76); always False here."""
+    if cublas:
+        warnings.warn("cublas=True has no effect: GEMMs run in the gfx950 HIP kernels", RuntimeWarning,
+                      stacklevel=2)
+    return False
+
+
+def check_config(config) -> None:
+    if config.dtype != "float16":
+        raise NotImplementedError(
+            f"dtype {config.dtype!r}: the gfx950 kernels compute the float16 model "
+            "(construct Pi0Config(dtype='float16'))")
+    if config.attn_logits_dtype != "float32":
+        raise NotImplementedError("attn_logits_dtype must be 'float32' in this build")
+
+
+def compile_model(config, target: str = "rocm", functions=None, cuda_graph: bool = False, cublas=None,
+                  hoist_modulation: bool = True):
+    """Return ``(executable, named_params)`` for the M1 functions (compile.py:99-133)."""
+    _target_kind(target)
+    check_config(config)
+    resolve_cublas(cublas, "rocm")
+    funcs = tuple(functions) if functions is not None else KV_FUNCS
+    unknown = [f for f in funcs if f not in KV_FUNCS]
+    if unknown:
+        raise NotImplementedError(f"functions {unknown} are not built on gfx950 (available: {KV_FUNCS})")
+    npar = named_params(config, funcs)
+    return Executable(config, funcs, npar, None, cuda_graph, hoist_modulation), npar
+
+
+def _device_for(target: str) -> Device:
+    _target_kind(target)
+    return device("rocm", 0)

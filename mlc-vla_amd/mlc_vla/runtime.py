@@ -1,0 +1,249 @@
+"""Device tensors and the VM-style entry points of the M1 functions.
+
+Mirrors the reference's runtime boundary: ``tvm.runtime.tensor(np, dev)`` builds
+device tensors and ``relax.VirtualMachine(ex, dev)["<fn>"](*tensors, params)``
+runs an exported function (python/mlc_vla/sample.py:95-105,128,158-160,184-186).
+Here device memory and the current stream come from PyTorch-ROCm; every function
+body is one call into ``libmlcvla_hip.so``.
+
+Behaviour kept from the reference boundary:
+  - arguments are checked against the exported signature (shape and dtype must
+    match exactly, like Relax struct-info matching) before anything runs;
+  - ``params`` is the last argument, a list in ``named_params`` order;
+  - outputs are freshly allocated device tensors; ``prefill`` returns a 2-tuple.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .model.pi0.pi0_model import get_default_spec
+
+_TORCH = {"float16": torch.float16, "float32": torch.float32, "int32": torch.int32, "uint32": torch.int32}
+
+
+class Device:
+    """A HIP device (``tvm.device("rocm", i)``)."""
+
+    def __init__(self, kind: str = "rocm", index: int = 0):
+        self.kind = kind
+        self.index = index
+
+    @property
+    def torch(self) -> torch.device:
+        return torch.device("cuda", self.index)
+
+    def sync(self) -> None:
+        torch.cuda.synchronize(self.index)
+
+    def __repr__(self) -> str:
+        return f"{self.kind}({self.index})"
+
+
+def device(kind: str = "rocm", index: int = 0) -> Device:
+    if not torch.cuda.is_available():
+        raise N.MlcvError("no HIP device visible: the gfx950 kernels are the only compute path")
+    return Device(kind, index)
+
+
+class Tensor:
+    """Device tensor with a logical dtype string (uint32 is stored as int32 bits)."""
+
+    __slots__ = ("torch", "dtype")
+
+    def __init__(self, t: torch.Tensor, dtype: str):
+        self.torch = t
+        self.dtype = dtype
+
+    @property
+    def shape(self):
+        return tuple(self.torch.shape)
+
+    def numpy(self) -> np.ndarray:
+        a = self.torch.detach().cpu().numpy()
+        return a.view(np.uint32) if self.dtype == "uint32" else a
+
+    def data_ptr(self) -> int:
+        return self.torch.data_ptr()
+
+    def __repr__(self) -> str:
+        return f"Tensor(shape={self.shape}, dtype={self.dtype})"
+
+
+def tensor(arr, dev: Optional[Device] = None) -> Tensor:
+    """Copy a numpy array to the device (``tvm.runtime.tensor``)."""
+    dev = dev or device()
+    a = np.ascontiguousarray(arr)
+    dt = str(a.dtype)
+    if dt not in _TORCH:
+        raise TypeError(f"unsupported dtype {dt}")
+    if dt == "uint32":
+        a = a.view(np.int32)
+    return Tensor(torch.from_numpy(a).to(dev.torch), dt)
+
+
+def empty(shape, dtype: str, dev: Optional[Device] = None) -> Tensor:
+    dev = dev or device()
+    return Tensor(torch.empty(tuple(shape), dtype=_TORCH[dtype], device=dev.torch), dtype)
+
+
+def as_tensor(x) -> Tensor:
+    if isinstance(x, Tensor):
+        return x
+    if isinstance(x, torch.Tensor):
+        inv = {torch.float16: "float16", torch.float32: "float32", torch.int32: "int32"}
+        if x.dtype not in inv:
+            raise TypeError(f"unsupported tensor dtype {x.dtype}")
+        return Tensor(x, inv[x.dtype])
+    raise TypeError(f"expected a device tensor, got {type(x).__name__}")
+
+
+def _ptr(t: Tensor) -> ctypes.c_void_p:
+    if not t.torch.is_cuda:
+        raise ValueError("tensor is not on the HIP device")
+    if not t.torch.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return ctypes.c_void_p(t.torch.data_ptr())
+
+
+def _check(name: str, arg: str, t: Tensor, shape, dtype) -> None:
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+        raise ValueError(f"{name}: argument {arg} expects {tuple(shape)} {dtype}, got {t.shape} {t.dtype}")
+
+
+class Executable:
+    """What ``compile_model`` returns: the configuration the kernels are planned for."""
+
+    def __init__(self, config, functions: Sequence[str], named_params, quant: Optional[str] = None,
+                 cuda_graph: bool = False, hoist_modulation: bool = True):
+        self.config = config
+        self.functions = tuple(functions)
+        self.named_params = list(named_params)
+        self.quant = quant
+        self.cuda_graph = cuda_graph
+        self.hoist_modulation = hoist_modulation
+
+    def c_config(self) -> N.Config:
+        c = self.config
+        vlm, ae = c.vlm, c.action_expert
+        return N.Config(
+            vlm_width=vlm.width, vlm_mlp=vlm.mlp_dim, ae_width=ae.width, ae_mlp=ae.mlp_dim,
+            depth=vlm.depth, num_heads=vlm.num_heads, num_kv_heads=vlm.num_kv_heads, head_dim=vlm.head_dim,
+            prefix_len=c.prefix_len, suffix_len=c.suffix_len, action_dim=c.action_dim,
+            num_steps=c.num_denoise_steps, rms_norm_eps=c.rms_norm_eps, rope_theta=c.rope_theta,
+            dtype=N.MLCV_DTYPE_F16,
+            quant=N.MLCV_QUANT_Q4F16_1 if self.quant == "q4f16_1" else N.MLCV_QUANT_NONE,
+        )
+
+
+class VirtualMachine:
+    """``vm["prefill" | "denoise_step_kv" | "denoise_loop_kv" | "chunk"](*tensors, params)``."""
+
+    def __init__(self, ex: Executable, dev: Optional[Device] = None):
+        self.ex = ex
+        self.dev = dev or device()
+        self._spec = get_default_spec(ex.config)
+        cfg = ex.c_config()
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.dev.index):
+            N.call("mlcv_create", ctypes.byref(cfg), ctypes.byref(h))
+        self._ctx = h
+        self._bound = None
+        self.set_graph(ex.cuda_graph)
+        self.set_hoist(ex.hoist_modulation)
+
+    def __del__(self):
+        h = getattr(self, "_ctx", None)
+        if h is not None and h.value:
+            try:
+                N.load().mlcv_destroy(h)
+            except Exception:  # noqa: BLE001 -- interpreter shutdown
+                pass
+            self._ctx = None
+
+    # options ---------------------------------------------------------------
+    def set_graph(self, on: bool) -> None:
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_USE_GRAPH, int(bool(on)))
+
+    def set_hoist(self, on: bool) -> None:
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_HOIST_MODULATION, int(bool(on)))
+
+    # plumbing --------------------------------------------------------------
+    def _stream(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(self.dev.index).cuda_stream)
+
+    def _bind(self, params: Sequence) -> None:
+        specs = self.ex.named_params
+        if len(params) != len(specs):
+            raise ValueError(f"expected {len(specs)} params, got {len(params)}")
+        ts: List[Tensor] = [as_tensor(p) for p in params]
+        for (name, sp), t in zip(specs, ts):
+            want = "int32" if sp.dtype == "uint32" and t.dtype == "int32" else sp.dtype
+            _check("params", name, t, sp.shape, want)
+        key = tuple(t.torch.data_ptr() for t in ts)
+        if key == self._bound:
+            return
+        arr = (ctypes.c_void_p * len(ts))(*[ctypes.c_void_p(k) for k in key])
+        N.call("mlcv_bind_params", self._ctx, arr, len(ts), self._stream())
+        self._bound = key
+        self._keep = ts  # the caller owns them; kept alive while bound
+
+    def _args(self, fn: str, tensors) -> List[Tensor]:
+        spec = self._spec[fn]
+        if len(tensors) != len(spec):
+            raise ValueError(f"{fn}: expected {len(spec)} tensors, got {len(tensors)}")
+        out = []
+        for (arg, sp), x in zip(spec.items(), tensors):
+            t = as_tensor(x)
+            _check(fn, arg, t, sp.shape, sp.dtype)
+            out.append(t)
+        return out
+
+    def __getitem__(self, name: str):
+        fns = {"prefill": self.prefill, "denoise_step_kv": self.denoise_step_kv,
+               "denoise_loop_kv": self.denoise_loop_kv, "chunk": self.chunk}
+        if name not in fns:
+            raise KeyError(f"function {name!r} is not built (available: {sorted(fns)})")
+        return fns[name]
+
+    # exported functions ------------------------------------------------------
+    def prefill(self, prefix_embs, prefix_mask, params):
+        self._bind(params)
+        pe, pm = self._args("prefill", (prefix_embs, prefix_mask))
+        kvs = self._spec["denoise_step_kv"]["keys"].shape
+        keys = empty(kvs, "float32", self.dev)
+        values = empty(kvs, self.ex.config.dtype, self.dev)
+        N.call("mlcv_prefill", self._ctx, _ptr(pe), _ptr(pm), _ptr(keys), _ptr(values), self._stream())
+        return keys, values
+
+    def denoise_step_kv(self, keys, values, x_t, time_emb, suffix_cos, suffix_sin, prefix_mask, params):
+        self._bind(params)
+        a = self._args("denoise_step_kv", (keys, values, x_t, time_emb, suffix_cos, suffix_sin, prefix_mask))
+        v = empty(a[2].shape, "float32", self.dev)
+        N.call("mlcv_denoise_step_kv", self._ctx, *[_ptr(t) for t in a], _ptr(v), self._stream())
+        return v
+
+    def denoise_loop_kv(self, keys, values, x0, time_embs, suffix_cos, suffix_sin, prefix_mask, params):
+        self._bind(params)
+        a = self._args("denoise_loop_kv", (keys, values, x0, time_embs, suffix_cos, suffix_sin, prefix_mask))
+        x = empty(a[2].shape, "float32", self.dev)
+        N.call("mlcv_denoise_loop_kv", self._ctx, *[_ptr(t) for t in a], _ptr(x), self._stream())
+        return x
+
+    def chunk(self, prefix_embs, prefix_mask, x0, time_embs, suffix_cos, suffix_sin, params):
+        """prefill + denoise_loop_kv as one graph; returns the final actions [1,T,A] f32."""
+        self._bind(params)
+        pe, pm = self._args("prefill", (prefix_embs, prefix_mask))
+        lk = self._spec["denoise_loop_kv"]
+        x0t, te, c, s = (as_tensor(t) for t in (x0, time_embs, suffix_cos, suffix_sin))
+        for arg, t in (("x0", x0t), ("time_embs", te), ("suffix_cos", c), ("suffix_sin", s)):
+            _check("chunk", arg, t, lk[arg].shape, lk[arg].dtype)
+        x = empty(x0t.shape, "float32", self.dev)
+        N.call("mlcv_chunk", self._ctx, _ptr(pe), _ptr(pm), _ptr(x0t), _ptr(te), _ptr(c), _ptr(s), _ptr(x),
+               self._stream())
+        return x

@@ -1,0 +1,182 @@
+"""Kernel-level parity on the GPU, through the C ABI: q4f16_1 quantize / dequantize
+bit-exact, the skinny GEMM (fp16 and q4 weights) and the joint attention against
+the oracle."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import cosine, max_abs
+from mlc_vla import _native as N
+from oracle import pi0_oracle as O
+from oracle import q4_oracle as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _st():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).cuda()
+
+
+def _p(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _host(t: torch.Tensor, dtype=None) -> np.ndarray:
+    torch.cuda.synchronize()
+    a = t.cpu().numpy()
+    return a.view(dtype) if dtype is not None else a
+
+
+def _ulp16(x: np.ndarray) -> np.ndarray:
+    x = np.abs(np.asarray(x, np.float16))
+    return (np.nextafter(x, np.float16(np.inf)) - x).astype(np.float64)
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (256, 1024), (1024, 4096), (50, 96)])
+def test_q4_quantize_bitexact(n, k):
+    print(f"q4 quantize N={n} K={k}", flush=True)
+    rng = np.random.default_rng(n + k)
+    w = (0.02 * rng.standard_normal((n, k))).astype(np.float16)
+    w[0, :8] = [0.7, -0.7, 0.35, -0.35, 0.1, 0.05, 0.0, 0.2]  # half-even ties (known answer)
+    if n > 1:
+        w[1, :32] = 0.0  # zero group
+    qw_ref, qs_ref = Q.quantize(w)
+    wd = _dev(w)
+    qw = torch.zeros((n, k // 8), dtype=torch.int32, device="cuda")
+    qs = torch.zeros((n, k // 32), dtype=torch.float16, device="cuda")
+    N.call("mlcv_q4_quantize", _p(wd), _p(qw), _p(qs), n, k, _st())
+    np.testing.assert_array_equal(_host(qw, np.uint32), qw_ref)
+    np.testing.assert_array_equal(_host(qs).view(np.uint16), qs_ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(7, 32), (3072, 1024), (64, 4096)])
+def test_q4_dequant_bitexact(n, k):
+    print(f"q4 dequant N={n} K={k}", flush=True)
+    rng = np.random.default_rng(k)
+    qw = rng.integers(0, 2 ** 32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)  # every nibble 0..15
+    qs = ((rng.random((n, k // 32)) + 0.01) * 0.02).astype(np.float16)
+    out = torch.empty((n, k), dtype=torch.float16, device="cuda")
+    qwd, qsd = _dev(qw), _dev(qs)
+    N.call("mlcv_q4_dequantize", _p(qwd), _p(qsd), _p(out), n, k, _st())
+    np.testing.assert_array_equal(_host(out).view(np.uint16), Q.dequantize(qw, qs).view(np.uint16))
+
+
+LIN_SHAPES = [(1, 1024, 3072), (50, 1024, 2560), (50, 2048, 1024), (50, 4096, 1024), (8, 32, 128), (50, 1024, 32),
+              (100, 256, 64), (4, 64, 16)]
+
+
+@pytest.mark.parametrize("m,k,n", LIN_SHAPES)
+@pytest.mark.parametrize("q4", [False, True], ids=["f16", "q4"])
+def test_linear_vs_oracle(m, k, n, q4):
+    print(f"linear M={m} K={k} N={n} q4={q4}", flush=True)
+    rng = np.random.default_rng(m * 7 + k + n)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    w = (0.02 * rng.standard_normal((n, k))).astype(np.float16)
+    b = (0.02 * rng.standard_normal(n)).astype(np.float16)
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    xd, bd = _dev(x), _dev(b)
+    if q4:
+        qw, qs = Q.quantize(w)
+        ref = Q.linear_q4(x, qw, qs, b)
+        w_eff = Q.dequantize(qw, qs)
+        qwd, qsd = _dev(qw), _dev(qs)
+        N.call("mlcv_linear", _p(xd), m, k, None, _p(qwd), _p(qsd), _p(bd), _p(y), n, _st())
+    else:
+        ref = O.linear(x, {"l.weight": w, "l.bias": b}, "l", O.Prec("f16"), bias=True)
+        w_eff = w
+        wd = _dev(w)
+        N.call("mlcv_linear", _p(xd), m, k, _p(wd), None, None, _p(bd), _p(y), n, _st())
+    got = _host(y).astype(np.float64)
+    # against the exact product: one rounding of the fp32 product to fp16, one of the fp16
+    # bias add (half an ulp each), plus fp32 accumulation slack
+    exact = x.astype(np.float64) @ w_eff.astype(np.float64).T
+    pre16 = exact.astype(np.float16)
+    bound = 0.5 * (_ulp16(pre16) + _ulp16(ref)) + 1e-6 * (1.0 + np.abs(exact))
+    err = np.abs(got - (exact + b.astype(np.float64)))
+    assert np.all(err <= bound + 0.5 * _ulp16(pre16)), float((err / bound).max())
+    assert cosine(got, ref) > 0.99999
+
+
+def _attn_case(tq, h, kv, hd, sp, ts, valid, k_f32, seed):
+    rng = np.random.default_rng(seed)
+    s = 1.0 / np.sqrt(hd)
+    q = (rng.standard_normal((tq, h * hd)) * s).astype(np.float16)
+    kp = (rng.standard_normal((kv, sp, hd)) * s).astype(np.float16)
+    vp = (rng.standard_normal((kv, sp, hd)) * s).astype(np.float16)
+    ks = (rng.standard_normal((ts, kv * hd)) * s).astype(np.float16)
+    vs = (rng.standard_normal((ts, kv * hd)) * s).astype(np.float16)
+    mask = np.where(np.arange(sp) < valid, 0.0, -1e9).astype(np.float32)
+    # oracle in float64 on the same (fp16-representable) values
+    qo = q.astype(np.float64).reshape(tq, h, hd)
+    ko = np.concatenate([kp.astype(np.float64).transpose(1, 0, 2), ks.astype(np.float64).reshape(ts, kv, hd)], 0)
+    vo = np.concatenate([vp.astype(np.float64).transpose(1, 0, 2), vs.astype(np.float64).reshape(ts, kv, hd)], 0)
+    full = np.concatenate([mask, np.zeros(ts, np.float32)]).astype(np.float64)
+    ref = O.sdpa(qo, ko, vo, full, O.Prec("f64"))
+    out = torch.empty((tq, h * hd), dtype=torch.float16, device="cuda")
+    qd, vpd = _dev(q), _dev(vp)
+    kpd = _dev(kp.astype(np.float32)) if k_f32 else _dev(kp)
+    md = _dev(mask)
+    ksd, vsd = (_dev(ks), _dev(vs)) if ts else (None, None)
+    N.call("mlcv_joint_attention", _p(qd), tq, h, kv, hd, _p(kpd), int(k_f32), _p(vpd), sp, _p(md),
+           _p(ksd) if ts else None, _p(vsd) if ts else None, ts, _p(out), _st())
+    return _host(out), ref
+
+
+@pytest.mark.parametrize(
+    "tq,h,kv,hd,sp,ts,valid,k_f32",
+    [
+        (50, 8, 1, 256, 968, 50, 900, True),    # isolated joint attention at the full pi0.5 shape
+        (50, 8, 1, 256, 968, 50, 900, False),   # same with an fp16 prefix cache
+        (8, 2, 1, 64, 32, 8, 32, True),         # 2-layer CPU-sized model
+        (4, 8, 1, 16, 776, 4, 700, True),       # the reference's dummy test model
+        (10, 4, 4, 32, 100, 10, 60, True),      # kv heads == q heads
+        (37, 2, 1, 128, 300, 0, 250, True),     # no suffix block (prefill form)
+        (50, 8, 1, 256, 968, 50, 40, True),     # most of the prefix padded: whole splits masked
+    ],
+)
+def test_joint_attention_vs_oracle(tq, h, kv, hd, sp, ts, valid, k_f32):
+    print(f"attention Tq={tq} H={h} KV={kv} hd={hd} Sp={sp} Ts={ts} valid={valid} kf32={k_f32}", flush=True)
+    got, ref = _attn_case(tq, h, kv, hd, sp, ts, valid, k_f32, seed=tq + sp + hd)
+    assert np.all(np.isfinite(got))
+    scale = float(np.abs(ref).max())
+    assert max_abs(got, ref) <= 2e-3 * scale + 2e-4, (max_abs(got, ref), scale)
+    assert cosine(got, ref) > 0.99999
+
+
+def test_joint_attention_logits_are_fp32_accurate():
+    """Large-magnitude logits from a float32 K cache: the kernel's hi/lo split QK^T
+    stays within the error the fp16 probabilities alone allow, while logits from
+    fp16-rounded K (a plain fp16 QK^T) exceed that bound."""
+    rng = np.random.default_rng(11)
+    tq, h, hd, sp = 16, 2, 256, 128
+    q = (rng.standard_normal((tq, h * hd)) * 0.3).astype(np.float16)
+    kp32 = rng.standard_normal((1, sp, hd)).astype(np.float32) * 6.0  # not fp16-representable
+    vp = rng.standard_normal((1, sp, hd)).astype(np.float16)
+    q64 = q.astype(np.float64).reshape(tq, h, hd)
+    v64 = vp.astype(np.float64).transpose(1, 0, 2)
+    k64 = kp32.astype(np.float64).transpose(1, 0, 2)
+    ref = O.sdpa(q64, k64, v64, None, O.Prec("f64"))
+    # sum_j p_j |v_j|: scale of the error from rounding each probability to fp16
+    absref = O.sdpa(q64, k64, np.abs(v64), None, O.Prec("f64"))
+    bound = 2 * _ulp16(ref) + 2.0 ** -10 * absref + 1e-6
+    out = torch.empty((tq, h * hd), dtype=torch.float16, device="cuda")
+    qd, kd, vd = _dev(q), _dev(kp32), _dev(vp)
+    N.call("mlcv_joint_attention", _p(qd), tq, h, 1, hd, _p(kd), 1, _p(vd), sp, None, None, None, 0, _p(out), _st())
+    got = _host(out)
+    diff = np.abs(got.astype(np.float64) - ref)
+    assert np.all(diff <= bound), float((diff / bound).max())
+    k16 = kp32.astype(np.float16).astype(np.float64).transpose(1, 0, 2)
+    ref16 = O.sdpa(q64, k16, v64, None, O.Prec("f64"))
+    assert np.any(np.abs(ref16 - ref) > bound)
