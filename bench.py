@@ -1,0 +1,317 @@
+#!/usr/bin/env python
+"""Benchmark of the pi0.5 M1 denoise path on one MI355X.
+
+Headline: ``denoise_step_kv`` microseconds per step at the full pi0.5 shape
+(18 action-expert layers of width 1024 / MLP 4096, 8 query heads / 1 KV head /
+head_dim 256, frozen prefix K/V of 968 tokens, horizon 50, action_dim 32, fp16
+weights and activations, fp32 logits / statistics), plus the 10-step action chunk
+(prefill of the 18-layer Gemma-2B-shaped prefix expert over 968 tokens with 800
+valid, then the in-graph Euler loop, one hipGraph) in milliseconds, each as a
+fraction of the 8 TB/s HBM roofline.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Prints one JSON line.  Weights are random N(0, 0.02) (no checkpoint), inputs
+synthetic and resident in HBM before the timed region.  The CPU baseline is the
+numpy float32 oracle of the same step on the host cores (not the reference's TVM
+build, which is not installable here).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mlc-vla_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "denoise_step_kv µs/step + 10-step chunk ms @prefix 968; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed denoise_step_kv calls")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--chunk-iters", type=int, default=20)
+    ap.add_argument("--op-iters", type=int, default=100)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-q4", action="store_true")
+    return ap.parse_args()
+
+
+def step_bytes(cfg, weight_bytes_per_param=2.0, q4=False):
+    """Algorithmic HBM bytes of one denoise_step_kv: every weight it reads once, the prefix
+    K (fp32) and V (fp16) cache once, and the step's inputs / output."""
+    from oracle import pi0_oracle as O  # shape bookkeeping only
+
+    d = O.dims_from_config(cfg)
+    nbytes = 0.0
+    for name, shape in O.param_specs(d):
+        if ".experts.0." in name or ".mlp.0." in name or name.endswith("layernorm.0.weight") or \
+                name == "backbone.final_norm.0.weight":
+            continue  # expert-0 weights are not read by the suffix step
+        n = 1
+        for s in shape:
+            n *= s
+        if q4 and name.endswith(".weight") and len(shape) == 2:
+            nbytes += n * 0.5 + (n / 32) * 2  # packed nibbles + fp16 group scales
+        else:
+            nbytes += n * weight_bytes_per_param
+    kv = d.depth * d.num_kv_heads * d.prefix_len * d.head_dim
+    nbytes += kv * (4 + 2)
+    T, A, hd = d.suffix_len, d.action_dim, d.head_dim
+    nbytes += T * A * 2 + d.ae_width * 2 + 2 * T * hd // 2 * 4 + d.prefix_len * 4 + T * A * 4
+    return nbytes
+
+
+def step_flops(cfg):
+    from oracle import pi0_oracle as O
+
+    d = O.dims_from_config(cfg)
+    T, W, F, H, hd, KV = d.suffix_len, d.ae_width, d.ae_mlp, d.num_heads, d.head_dim, d.num_kv_heads
+    per_layer = 2 * T * W * (H * hd + 2 * KV * hd) + 2 * T * H * hd * W + 2 * T * W * 2 * F + 2 * T * F * W
+    keys = d.prefix_len + T
+    per_layer += 2 * 2 * H * T * keys * hd
+    mod = 2 * (2 * d.depth + 1) * 3 * W * W + 2 * 2 * W * W
+    return d.depth * per_layer + mod + 2 * T * d.action_dim * W * 2
+
+
+def op_bytes_flops(cfg, op):
+    """Algorithmic bytes / flops of one launch of an op of the step (layer 0)."""
+    v, a = cfg.vlm, cfg.action_expert
+    T, W, F, H, hd, KV, P = cfg.suffix_len, a.width, a.mlp_dim, v.num_heads, v.head_dim, v.num_kv_heads, cfg.prefix_len
+    nq, nkv = H * hd, KV * hd
+    if op == "modulation":
+        nm = 2 * v.depth + 1
+        return nm * (3 * W * W + 3 * W) * 2 + W * 2 + nm * 3 * W * 2, 2 * nm * 3 * W * W
+    if op == "qkv":
+        return (nq + 2 * nkv) * W * 2 + T * W * 2 + 2 * W * 2 + T * (nq + 2 * nkv) * 2, 2 * T * W * (nq + 2 * nkv)
+    if op == "attention":
+        return (KV * P * hd * 6 + T * nq * 2 + 2 * T * nkv * 2 + T * nq * 2 + P * 4 + T * hd * 4,
+                4 * H * T * (P + T) * hd)
+    if op == "o_proj":
+        return W * nq * 2 + T * nq * 2 + 2 * T * W * 2 + W * 2, 2 * T * nq * W
+    if op == "gate_up":
+        return 2 * F * W * 2 + T * W * 2 + 2 * W * 2 + T * F * 2, 2 * T * W * 2 * F
+    if op == "down":
+        return W * F * 2 + T * F * 2 + 2 * T * W * 2 + W * 2, 2 * T * F * W
+    if op == "head":
+        return cfg.action_dim * W * 2 + T * W * 2 + T * cfg.action_dim * 4, 2 * T * W * cfg.action_dim
+    raise KeyError(op)
+
+
+OPS_PER_STEP = {"modulation": 1, "qkv": 18, "attention": 18, "o_proj": 18, "gate_up": 18, "down": 18, "head": 1}
+
+
+def cpu_baseline(cfg, seconds):
+    """The numpy float32 oracle of one denoise_step_kv on the host cores (bounded sample)."""
+    import numpy as np
+
+    from oracle import pi0_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = [t for t in threadpool_info() if t.get("user_api") == "blas"]
+        if blas:
+            threads = max(t["num_threads"] for t in blas)
+    except Exception:  # noqa: BLE001
+        pass
+    d = O.dims_from_config(cfg)
+    keep = lambda n: not (".experts.0." in n or ".mlp.0." in n)  # noqa: E731
+    params = O.make_params([(n, s) for n, s in O.param_specs(d) if keep(n)], 0, "float32")
+    rng = np.random.default_rng(5)
+    keys = rng.standard_normal((d.depth, 1, d.num_kv_heads, d.prefix_len, d.head_dim)).astype(np.float32)
+    values = rng.standard_normal(keys.shape).astype(np.float32)
+    x_t = rng.standard_normal((1, d.suffix_len, d.action_dim)).astype(np.float32)
+    te = O.sinusoidal_time_emb(1.0, d.ae_width)
+    cos, sin = O.make_rope_np(d.suffix_len, d.head_dim, d.theta, offset=d.prefix_len)
+    pm = O.make_prefix_mask_np(d.prefix_len)
+    P = O.Prec("f32")
+    O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 50:
+            break
+    return {"value": round(el / n * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"{n} float32 denoise_step_kv at the full pi0.5 shape (18 layers, P=968, T=50) "
+                      f"with the numpy oracle after 1 warm-up ({el:.1f} s)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the M1 denoise path is a single-request, single-device path and "
+              f"this build has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from mlc_vla import _native as N
+    from mlc_vla import runtime
+    from mlc_vla.compile import compile_model
+    from mlc_vla.compile_quant import compile_model_quant
+    from mlc_vla.model.pi0 import Pi0Config
+    from mlc_vla.sample import make_prefix_mask_np, make_rope_np, make_time_embs
+
+    torch.cuda.set_device(0)
+    dev = runtime.device()
+    cfg = Pi0Config(dtype="float16", action_horizon=50)  # prefix_len 968, 18 layers
+    ex, npar = compile_model(cfg, "rocm", cuda_graph=True)
+    vm = runtime.VirtualMachine(ex, dev)
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    params = []
+    for _, p in npar:
+        t = torch.randn(p.shape, generator=gen, device="cuda", dtype=torch.float32).mul_(0.02).to(torch.float16)
+        params.append(runtime.Tensor(t, "float16"))
+    gen.manual_seed(3)
+    prefix = runtime.Tensor(torch.randn((1, 968, 2048), generator=gen, device="cuda").to(torch.float16), "float16")
+    rng = np.random.default_rng(0)
+    noise = rng.standard_normal((1, 50, 32)).astype(np.float32)
+    tes = make_time_embs(10, 1024)
+    d = lambda a: runtime.tensor(a, dev)  # noqa: E731
+    # config 3: all-valid prefix, suffix rope offset 968; config 5: 800 valid tokens
+    pm_all, pm_800 = d(make_prefix_mask_np(968)), d(make_prefix_mask_np(968, num_valid=800))
+    c968, s968 = (d(a) for a in make_rope_np(50, 256, 10_000.0, offset=968))
+    c800, s800 = (d(a) for a in make_rope_np(50, 256, 10_000.0, offset=800))
+    x_t = d(noise.astype(np.float16))
+    te = d(tes[0].astype(np.float16))
+    te_all = d(np.concatenate(tes, 0).astype(np.float16))
+    x0 = d(noise)
+    keys, values = vm["prefill"](prefix, pm_all, params)
+    torch.cuda.synchronize()
+
+    def timed(fn, iters, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters, (time.perf_counter() - w0) * 1e3 / iters
+
+    # ---- headline: denoise_step_kv ---------------------------------------------
+    step = lambda: vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)  # noqa: E731
+    step_ms, step_wall_ms = timed(step, args.steps, args.warmup)
+    # ---- chunk: prefill + 10-step loop as one graph -----------------------------
+    chunk = lambda: vm["chunk"](prefix, pm_800, x0, te_all, c800, s800, params)  # noqa: E731
+    chunk_ms, _ = timed(chunk, args.chunk_iters, 3)
+    prefill_ms, _ = timed(lambda: vm["prefill"](prefix, pm_800, params), args.chunk_iters, 3)
+    loop_ms, _ = timed(lambda: vm["denoise_loop_kv"](keys, values, x0, te_all, c800, s800, pm_800, params),
+                       args.chunk_iters, 3)
+    vm.set_hoist(False)
+    chunk_nh_ms, _ = timed(chunk, args.chunk_iters, 3)
+    vm.set_hoist(True)
+
+    # ---- per-op launch times (the step's kernels one op at a time) ------------
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    per_op = {}
+    for name, cnt in OPS_PER_STEP.items():
+        op = N.OPS[name]
+        run = lambda: N.call("mlcv_bench_op", vm._ctx, op, 0, args.op_iters, runtime._ptr(keys),  # noqa: E731
+                             runtime._ptr(values), stream())
+        ms, _ = timed(run, 1, 1)
+        us = ms * 1e3 / args.op_iters
+        b, f = op_bytes_flops(cfg, name)
+        per_op[name] = {"us": round(us, 2), "per_step": cnt, "us_per_step": round(us * cnt, 1),
+                        "GBps": round(b / (us * 1e-6) / 1e9, 1), "bytes": int(b), "flops": int(f)}
+    dom = max(per_op, key=lambda k: per_op[k]["us_per_step"])
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom)
+
+    sbytes = step_bytes(cfg)
+    step_us = step_ms * 1e3
+    out = {
+        "metric": METRIC,
+        "value": round(step_us, 1),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "pi05_denoise_step_kv_fp16_P968_T50", "layers": 18, "ae_width": 1024,
+                   "ae_mlp": 4096, "heads": 8, "kv_heads": 1, "head_dim": 256, "prefix_len": 968,
+                   "horizon": 50, "action_dim": 32, "chunk_steps": 10, "chunk_valid_prefix": 800},
+        "step_wall_us": round(step_wall_ms * 1e3, 1),
+        "chunk_ms": round(chunk_ms, 3),
+        "chunk_ms_per_step_modulation": round(chunk_nh_ms, 3),
+        "prefill_ms": round(prefill_ms, 3),
+        "loop_ms": round(loop_ms, 3),
+        "step_roofline": {"bound": "hbm", "achieved": round(sbytes / (step_us * 1e-6) / 1e9, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(sbytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "bytes_per_step": int(sbytes), "flops_per_step": int(step_flops(cfg))},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": per_op[dom]["bytes"], "avg_launch_us": per_op[dom]["us"]},
+        "per_op": per_op,
+    }
+    pf_flops = 2 * 968 * 2048 * (2560 + 2048 + 2 * 16384) * 18 + 2 * 968 * 16384 * 2048 * 17 + \
+        4 * 8 * 968 * 968 * 256 * 17
+    out["prefill_mfma"] = {"tflops": round(pf_flops / (prefill_ms * 1e-3) / 1e12, 1),
+                           "frac": round(pf_flops / (prefill_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+    if not args.no_q4:
+        exq, qnp, qmap, quant = compile_model_quant(cfg, "rocm", None, "q4f16_1", cuda_graph=True)
+        vmq = runtime.VirtualMachine(exq, dev)
+        by_name = {n: t for (n, _), t in zip(npar, params)}
+        qparams = []
+        cache = {}
+        for n, p in qnp:
+            if n.endswith(".q_weight") or n.endswith(".q_scale"):
+                base = n.rsplit(".", 1)[0]
+                if base not in cache:
+                    cache[base] = quant.quantize_weight(by_name[base + ".weight"])
+                qparams.append(cache[base][0 if n.endswith(".q_weight") else 1])
+            else:
+                qparams.append(by_name[n])
+        del cache
+        vq = vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams)
+        q_ms, _ = timed(lambda: vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams),
+                        args.steps, args.warmup)
+        qbytes = step_bytes(cfg, q4=True)
+        v16 = step().numpy()
+        cosq = float(np.dot(vq.numpy().ravel(), v16.ravel()) / (np.linalg.norm(vq.numpy()) * np.linalg.norm(v16)))
+        out["q4f16_1_step"] = {"us": round(q_ms * 1e3, 1), "bytes_per_step": int(qbytes),
+                               "frac": round(qbytes / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                               "cos_vs_fp16": round(cosq, 5)}
+        del vmq, qparams
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

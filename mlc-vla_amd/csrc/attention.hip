@@ -38,12 +38,101 @@ __device__ __forceinline__ void rope8(const _Float16* x, int d0, int half, const
   const int dc = first ? d0 : d0 - half;
   const h8 a = *reinterpret_cast<const h8*>(x + d0);
   const h8 b = *reinterpret_cast<const h8*>(x + dp);
+  const f4 c0 = *reinterpret_cast<const f4*>(cs + dc), c1 = *reinterpret_cast<const f4*>(cs + dc + 4);
+  const f4 s0 = *reinterpret_cast<const f4*>(sn + dc), s1 = *reinterpret_cast<const f4*>(sn + dc + 4);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float c = cs[dc + e], s = sn[dc + e];
+    const float c = e < 4 ? c0[e] : c1[e - 4], sv = e < 4 ? s0[e] : s1[e - 4];
     const float xa = h2f(a[e]), xb = h2f(b[e]);
-    out[e] = first ? (xa * c - xb * s) : (xa * c + xb * s);
+    out[e] = first ? (xa * c - xb * sv) : (xa * c + xb * sv);
   }
+}
+
+// one key chunk of K (fp32, roped) and V (fp16) held in registers between the
+// global loads and the LDS stores, so the next chunk's loads overlap this chunk's math
+template <int HD>
+struct KvRegs {
+  static constexpr int NIT = (KCH * (HD / 8) + 255) / 256;
+  float k[NIT][8];
+  h8 v[NIT];
+  float msk;
+};
+
+template <int HD>
+__device__ __forceinline__ void kv_gload(KvRegs<HD>& r, const AttnArgs& a, int c0, int kend, int kvh, int tid) {
+  constexpr int HALF = HD / 2;
+  const float* kp32 = reinterpret_cast<const float*>(a.kp) + (size_t)kvh * a.Sp * HD;
+  const _Float16* kp16 = reinterpret_cast<const _Float16*>(a.kp) + (size_t)kvh * a.Sp * HD;
+  const _Float16* vpb = a.vp + (size_t)kvh * a.Sp * HD;
+#pragma unroll
+  for (int it = 0; it < KvRegs<HD>::NIT; ++it) {
+    const int item = tid + 256 * it;
+    const int jl = item / (HD / 8);
+    const int d0 = (item % (HD / 8)) * 8;
+    const int kj = c0 + jl;
+    r.v[it] = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.k[it][e] = 0.f;
+    if (item >= KCH * (HD / 8) || kj >= kend) continue;
+    if (kj < a.Sp) {
+      if (a.kp_f32) {
+        const f4 x0 = *reinterpret_cast<const f4*>(kp32 + (size_t)kj * HD + d0);
+        const f4 x1 = *reinterpret_cast<const f4*>(kp32 + (size_t)kj * HD + d0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          r.k[it][e] = x0[e];
+          r.k[it][e + 4] = x1[e];
+        }
+      } else {
+        const h8 x = *reinterpret_cast<const h8*>(kp16 + (size_t)kj * HD + d0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.k[it][e] = h2f(x[e]);
+      }
+      r.v[it] = *reinterpret_cast<const h8*>(vpb + (size_t)kj * HD + d0);
+    } else {
+      const int ts = kj - a.Sp;
+      const _Float16* kr = a.ks + (size_t)ts * a.ks_ld + (size_t)kvh * HD;
+      if (!a.ks_roped && a.cos) {
+        rope8(kr, d0, HALF, a.cos + (size_t)ts * HALF, a.sin + (size_t)ts * HALF, r.k[it]);
+      } else {
+        const h8 x = *reinterpret_cast<const h8*>(kr + d0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.k[it][e] = h2f(x[e]);
+      }
+      r.v[it] = *reinterpret_cast<const h8*>(a.vs + (size_t)ts * a.vs_ld + (size_t)kvh * HD + d0);
+    }
+  }
+  r.msk = 0.f;
+  if (tid < KCH) {
+    const int kj = c0 + tid;
+    if (kj >= kend) r.msk = -INFINITY;
+    else if (kj < a.Sp) r.msk = a.mask ? a.mask[kj] : 0.f;
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void kv_sstore(const KvRegs<HD>& r, AttnSmem<HD>& sm, int tid) {
+  constexpr int KLD = AttnSmem<HD>::KLD, VLD = AttnSmem<HD>::VLD;
+#pragma unroll
+  for (int it = 0; it < KvRegs<HD>::NIT; ++it) {
+    const int item = tid + 256 * it;
+    if (item >= KCH * (HD / 8)) continue;
+    const int jl = item / (HD / 8);
+    const int d0 = (item % (HD / 8)) * 8;
+    h8 hi8, lo8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      _Float16 hi, lo;
+      split_f32(r.k[it][e], hi, lo);
+      hi8[e] = hi;
+      lo8[e] = lo;
+    }
+    *reinterpret_cast<h8*>(&sm.kh[jl * KLD + d0]) = hi8;
+    *reinterpret_cast<h8*>(&sm.kl[jl * KLD + d0]) = lo8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm.vt[(d0 + e) * VLD + jl] = r.v[it][e];
+  }
+  if (tid < KCH) sm.msk[tid] = r.msk;
 }
 
 template <int HD>
@@ -102,66 +191,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const int S = a.Sp + a.Ts;
   const int kbeg = split * a.kps;
   const int kend = min(S, kbeg + a.kps);
-  const float* kp32 = reinterpret_cast<const float*>(a.kp) + (size_t)kvh * a.Sp * HD;
-  const _Float16* kp16 = reinterpret_cast<const _Float16*>(a.kp) + (size_t)kvh * a.Sp * HD;
-  const _Float16* vpb = a.vp + (size_t)kvh * a.Sp * HD;
+  KvRegs<HD> regs;
+  if (kbeg < kend) kv_gload<HD>(regs, a, kbeg, kend, kvh, tid);
 
   for (int c0 = kbeg; c0 < kend; c0 += KCH) {
-    // ---- stage K (hi/lo), V^T and the mask for keys [c0, c0+32) ------------
-    for (int item = tid; item < KCH * (HD / 8); item += 256) {
-      const int jl = item / (HD / 8);
-      const int d0 = (item % (HD / 8)) * 8;
-      const int kj = c0 + jl;
-      float kv8[8];
-      h8 vv = (h8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (kj < kend && kj < a.Sp) {
-        if (a.kp_f32) {
-          const f4 x0 = *reinterpret_cast<const f4*>(kp32 + (size_t)kj * HD + d0);
-          const f4 x1 = *reinterpret_cast<const f4*>(kp32 + (size_t)kj * HD + d0 + 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { kv8[e] = x0[e]; kv8[e + 4] = x1[e]; }
-        } else {
-          const h8 x = *reinterpret_cast<const h8*>(kp16 + (size_t)kj * HD + d0);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kv8[e] = h2f(x[e]);
-        }
-        vv = *reinterpret_cast<const h8*>(vpb + (size_t)kj * HD + d0);
-      } else if (kj < kend) {
-        const int ts = kj - a.Sp;
-        const _Float16* kr = a.ks + (size_t)ts * a.ks_ld + (size_t)kvh * HD;
-        if (!a.ks_roped && a.cos) {
-          rope8(kr, d0, HALF, a.cos + (size_t)ts * HALF, a.sin + (size_t)ts * HALF, kv8);
-        } else {
-          const h8 x = *reinterpret_cast<const h8*>(kr + d0);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kv8[e] = h2f(x[e]);
-        }
-        vv = *reinterpret_cast<const h8*>(a.vs + (size_t)ts * a.vs_ld + (size_t)kvh * HD + d0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kv8[e] = 0.f;
-      }
-      h8 hi8, lo8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        _Float16 hi, lo;
-        split_f32(kv8[e], hi, lo);
-        hi8[e] = hi;
-        lo8[e] = lo;
-      }
-      *reinterpret_cast<h8*>(&sm.kh[jl * KLD + d0]) = hi8;
-      *reinterpret_cast<h8*>(&sm.kl[jl * KLD + d0]) = lo8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.vt[(d0 + e) * VLD + jl] = vv[e];
-    }
-    if (tid < KCH) {
-      const int kj = c0 + tid;
-      float mv;
-      if (kj >= kend) mv = -INFINITY;
-      else if (kj < a.Sp) mv = a.mask ? a.mask[kj] : 0.f;
-      else mv = 0.f;
-      sm.msk[tid] = mv;
-    }
+    kv_sstore<HD>(regs, sm, tid);
+    if (c0 + KCH < kend) kv_gload<HD>(regs, a, c0 + KCH, kend, kvh, tid);
     __syncthreads();
 
     // ---- logits S^T for 2 key tiles of 16 --------------------------------
@@ -249,25 +284,38 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   const int hd = a.hd;
   const int grp = a.H / a.KV;
   const int hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
-  float mmax = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const size_t pr = ((size_t)kvh * a.nsplit + s) * a.rpad + row;
-    mmax = fmaxf(mmax, a.part_ml[pr * 2]);
+  const size_t pr0 = (size_t)kvh * a.nsplit * a.rpad + row;
+  // split weights w_s = exp(m_s - max) / sum_s l_s exp(m_s - max), lane s holds split s
+  float m = -INFINITY, l = 0.f;
+  if (lane < a.nsplit) {
+    m = a.part_ml[(pr0 + (size_t)lane * a.rpad) * 2];
+    l = a.part_ml[(pr0 + (size_t)lane * a.rpad) * 2 + 1];
   }
-  float lsum = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const size_t pr = ((size_t)kvh * a.nsplit + s) * a.rpad + row;
-    lsum += a.part_ml[pr * 2 + 1] * expf(a.part_ml[pr * 2] - mmax);
-  }
-  const float inv = 1.0f / lsum;
+  float mmax = m;
+  for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o));
+  const float e = lane < a.nsplit ? expf(m - mmax) : 0.f;
+  const float lsum = wave_sum(l * e);
+  const float wgt = e / lsum;
+  float wv[16];  // all lanes take part in the shuffles (nsplit <= 16)
+#pragma unroll
+  for (int s = 0; s < 16; ++s) wv[s] = __shfl(wgt, s);
   _Float16* orow = a.out + (size_t)t * a.out_ld + (size_t)h * hd;
-  for (int d = lane; d < hd; d += 64) {
-    float acc = 0.f;
-    for (int s = 0; s < a.nsplit; ++s) {
-      const size_t pr = ((size_t)kvh * a.nsplit + s) * a.rpad + row;
-      acc += a.part_o[pr * hd + d] * expf(a.part_ml[pr * 2] - mmax);
+  for (int d = lane * 4; d < hd; d += 256) {
+    f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      if (s >= a.nsplit) break;
+      const float ws = wv[s];
+      const f4 o = *reinterpret_cast<const f4*>(a.part_o + (pr0 + (size_t)s * a.rpad) * hd + d);
+      acc[0] += ws * o[0];
+      acc[1] += ws * o[1];
+      acc[2] += ws * o[2];
+      acc[3] += ws * o[3];
     }
-    orow[d] = f2h(acc * inv);
+    h4 o4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o4[i] = f2h(acc[i]);
+    *reinterpret_cast<h4*>(orow + d) = o4;
   }
 }
 
@@ -328,7 +376,7 @@ void attn_plan(int rows, int keys, int target_blocks, int* nsplit, int* kps) {
   const int rb = (rows + ROWS - 1) / ROWS;
   const int chunks = (keys + KCH - 1) / KCH;
   int ns = (target_blocks + rb - 1) / rb;
-  if (ns > 8) ns = 8;
+  if (ns > 16) ns = 16;
   if (ns > chunks) ns = chunks;
   if (ns < 1) ns = 1;
   const int cps = (chunks + ns - 1) / ns;
@@ -347,6 +395,7 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.kps % KCH == 0 && a.nsplit >= 1, "attention split plan");
   MLCV_REQUIRE((long)a.nsplit * a.kps >= (long)(a.Sp + a.Ts), "attention splits do not cover the keys");
   MLCV_REQUIRE(a.nsplit == 1 || (a.part_o && a.part_ml), "attention workspace missing");
+  MLCV_REQUIRE(a.nsplit <= 16, "at most 16 key splits");
   dim3 grid((a.rows + ROWS - 1) / ROWS, a.nsplit, a.KV);
   switch (a.hd) {
     case 16: attn_kernel<16><<<grid, 256, 0, st>>>(a); break;

@@ -89,6 +89,27 @@ __device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Cross-workgroup hand-off without cache maintenance: data written with agent-scope
+// stores (write-through to the coherent memory side), a full s_waitcnt before the
+// agent-scope counter RMW, and agent-scope loads on the reading side.  This avoids the
+// L2 writeback + invalidate that a device-scope fence costs on a multi-XCD part.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+// agent-scope acquire: invalidate possibly stale cached lines before plain loads of data
+// another workgroup wrote through with store_coherent (no writeback of this XCD's L2)
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ unsigned counter_add(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(unsigned* p) {
+  __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Split an fp32 value into fp16 hi + lo with hi + lo ~= x to ~2^-22 relative
 // (absolute floor: fp16 subnormal spacing 2^-24 on the lo part).
 __device__ __forceinline__ void split_f32(float x, _Float16& hi, _Float16& lo) {

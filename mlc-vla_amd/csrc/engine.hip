@@ -71,7 +71,8 @@ struct Ctx {
 
   // suffix path
   _Float16 *x16, *q, *k, *v, *attn, *h, *cond, *tmp, *mod, *te, *xin16;
-  float *x32, *x0, *vout, *cos, *sin, *mask;
+  float *x32, *x0, *vout, *cos, *sin, *mask, *rowss;
+  int rss_tiles = 1;
   // prefill path
   _Float16 *px, *pxn, *pqkv, *pctx, *ph, *pvalues;
   float *pcos, *psin, *pkeys;
@@ -122,12 +123,15 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   op.epi = d.epi;
   op.segs = c.d_segs + d.seg_off;
   op.nseg = d.nseg;
+  for (int i = 0; i < d.nseg && i < 3; ++i) op.inl[i] = c.h_segs[d.seg_off + i];
   op.ntiles = d.ntiles;
   const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64);
   op.splitk = p.splitk;
   op.kper = p.kper;
   op.ws = c.skws;
   op.counters = c.counters;
+  op.rowss_ld = c.T;
+  op.rowss_tiles = c.rss_tiles;
   return op;
 }
 
@@ -149,6 +153,7 @@ int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRM
   SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.x16, c.W1, c.T);
   op.scale = m_in;
   op.shift = m_in + c.W1;
+  op.rowss_in = c.rowss;
   return run_op(c, c.layer_ops[4 * L + 0], op, st);
 }
 
@@ -188,6 +193,7 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
 int enqueue_oproj(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // o_proj + gated residual
   SkOp op = make_op(c, c.layer_ops[4 * L + 1], c.attn, c.H * c.HD, c.T);
   op.gate = mod_of(c, modp, 2 * L) + 2 * c.W1;
+  op.rowss_out = c.rowss;
   return run_op(c, c.layer_ops[4 * L + 1], op, st);
 }
 
@@ -196,6 +202,7 @@ int enqueue_gateup(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // ad
   SkOp op = make_op(c, c.layer_ops[4 * L + 2], c.x16, c.W1, c.T);
   op.scale = m_post;
   op.shift = m_post + c.W1;
+  op.rowss_in = c.rowss;
   op.geglu_F = c.F1;
   return run_op(c, c.layer_ops[4 * L + 2], op, st);
 }
@@ -203,6 +210,7 @@ int enqueue_gateup(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // ad
 int enqueue_down(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // down + gated residual
   SkOp op = make_op(c, c.layer_ops[4 * L + 3], c.h, c.F1, c.T);
   op.gate = mod_of(c, modp, 2 * L + 1) + 2 * c.W1;
+  op.rowss_out = c.rowss;
   return run_op(c, c.layer_ops[4 * L + 3], op, st);
 }
 
@@ -211,6 +219,7 @@ int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  //
   SkOp op = make_op(c, c.op_aout, c.x16, c.W1, c.T);
   op.scale = m_fin;
   op.shift = m_fin + c.W1;
+  op.rowss_in = c.rowss;
   if (euler) {
     op.epi = EPI_EULER;
     op.dt = (float)(-1.0 / c.NS);
@@ -223,7 +232,9 @@ int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  //
 // ---- one suffix-only velocity evaluation (modulations already in modp) -------
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
                  hipStream_t st) {
-  MLCV_TRY(run_op(c, c.op_ain, make_op(c, c.op_ain, c.xin16, c.A, c.T), st));
+  SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
+  ain.rowss_out = c.rowss;
+  MLCV_TRY(run_op(c, c.op_ain, ain, st));
   for (int L = 0; L < c.D; ++L) {
     MLCV_TRY(enqueue_qkv(c, L, modp, st));
     MLCV_TRY(enqueue_attn(c, L, keys, values, st));
@@ -487,6 +498,9 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.cos, T * hd / 2);
   ALLOC(c.sin, T * hd / 2);
   ALLOC(c.mask, c.P);
+  c.rss_tiles = (W1 + 63) / 64;
+  MLCV_REQUIRE(c.rss_tiles <= 64, "ae_width must be <= 4096");
+  ALLOC(c.rowss, (size_t)c.rss_tiles * T);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
   ALLOC(c.pxn, P * c.W0);
@@ -903,6 +917,7 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
   op.epi = EPI_STORE;
   op.segs = g_scratch.seg;
   op.nseg = 1;
+  op.inl[0] = s;
   op.ntiles = ntiles;
   op.splitk = p.splitk;
   op.kper = p.kper;

@@ -34,15 +34,21 @@ struct SkSeg {
 struct SkOp {
   const _Float16* x;     // X [M][ldx]
   int ldx, M, K;
-  int mx_stride;         // per m-block stride of the modulation (0 = shared)
   // adaRMS prologue: xn = fp16((x / sqrt(mean(x^2)+eps)) * (1 + scale) + shift)
   const _Float16* scale; // [K] or null (no prologue)
   const _Float16* shift; // [K]
   float eps;
+  // row sums of squares of the residual stream, one partial per 64-column tile:
+  // read by the prologue (rowss_in, rowss_tiles partials) and written by epilogues
+  // that produce x (rowss_out); element [tile * rowss_ld + m]
+  const float* rowss_in;
+  float* rowss_out;
+  int rowss_ld, rowss_tiles;
   int epi;
   const _Float16* gate;  // [N] (EPI_GATED_RES)
   int geglu_F;           // EPI_GEGLU: rows [0,F) gate, [F,2F) up
-  const SkSeg* segs;     // device table
+  SkSeg inl[3];          // segments passed by value (nseg <= 3)
+  const SkSeg* segs;     // device table when nseg > 3
   int nseg, ntiles;
   int splitk, kper;
   float* ws;             // split-K partials

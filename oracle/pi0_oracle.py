@@ -335,15 +335,19 @@ def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: Optional[np.ndarray]
     kv = k.shape[1]
     if kv not in (1, n):
         raise ValueError("kv heads must broadcast to q heads")
+    g = n // kv  # head h reads kv head h // g (broadcast_to semantics for kv in {1, n})
     ldt = P.hi if logits_dtype == "float32" or P.mode == "f64" else np.float16
-    qh = q.astype(ldt).astype(P.acc).transpose(1, 0, 2)            # [n, Tq, hd]
-    kh = np.broadcast_to(k.astype(ldt).astype(P.acc).transpose(1, 0, 2), (n, k.shape[0], hd))
-    logits = np.matmul(qh, kh.transpose(0, 2, 1)).astype(P.hi)     # [n, Tq, Ts] f32
-    if mask is not None:
-        logits = logits + mask.astype(P.hi)
-    probs = softmax(logits).astype(v.dtype)
-    vh = np.broadcast_to(v.transpose(1, 0, 2), (n, v.shape[0], hd))
-    enc = np.matmul(probs.astype(P.acc), vh.astype(P.acc)).astype(v.dtype)  # [n, Tq, hd]
+    qh = q.astype(ldt).astype(P.acc).transpose(1, 0, 2)             # [n, Tq, hd]
+    enc = np.empty((n, tq, hd), v.dtype)
+    for j in range(kv):
+        hs = slice(j * g, (j + 1) * g)
+        kj = np.ascontiguousarray(k[:, j, :].astype(ldt).astype(P.acc))  # [Ts, hd]
+        logits = np.matmul(qh[hs], kj.T).astype(P.hi)                 # [g, Tq, Ts] f32
+        if mask is not None:
+            logits = logits + mask.astype(P.hi)
+        probs = softmax(logits).astype(v.dtype)
+        vj = np.ascontiguousarray(v[:, j, :]).astype(P.acc)            # [Ts, hd]
+        enc[hs] = np.matmul(probs.astype(P.acc), vj).astype(v.dtype)
     return enc.transpose(1, 0, 2).reshape(tq, n * hd)
 
 
