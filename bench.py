@@ -46,17 +46,45 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-q4", action="store_true")
+    ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
+                    help="print a per-kernel, per-launch-shape table of a rocprofv3 --kernel-trace CSV and exit")
     return ap.parse_args()
+
+
+def summarize_trace(path):
+    """Markdown table of a rocprofv3 kernel trace grouped by (kernel, grid, workgroup)."""
+    import csv
+
+    groups = {}
+    total = 0
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            name = name.split("(")[0].replace("mlcv::(anonymous namespace)::", "")
+            grid = "x".join(r[f"Grid_Size_{a}"] for a in "XYZ")
+            key = (name, grid, int(r["Workgroup_Size_X"]), int(r["LDS_Block_Size"]),
+                   int(r["VGPR_Count"]) + int(r["Accum_VGPR_Count"]))
+            dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            g = groups.setdefault(key, [])
+            g.append(dur)
+            total += dur
+    print("| kernel | grid (threads) | workgroup | LDS B | VGPR+AGPR | calls | avg us | median us | min us | "
+          "max us | share |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    for key, d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        d.sort()
+        print(f"| {key[0][:48]} | {key[1]} | {key[2]} | {key[3]} | {key[4]} | {len(d)} | {sum(d) / len(d) / 1e3:.2f} | "
+              f"{d[len(d) // 2] / 1e3:.2f} | {d[0] / 1e3:.2f} | {d[-1] / 1e3:.2f} | {sum(d) / total:.1%} |")
 
 
 def step_bytes(cfg, weight_bytes_per_param=2.0, q4=False):
     """Algorithmic HBM bytes of one denoise_step_kv: every weight it reads once, the prefix
     K (fp32) and V (fp16) cache once, and the step's inputs / output."""
-    from oracle import pi0_oracle as O  # shape bookkeeping only
+    from mlc_vla.model.pi0.pi0_model import KV_FUNCS, named_params
 
-    d = O.dims_from_config(cfg)
     nbytes = 0.0
-    for name, shape in O.param_specs(d):
+    for name, prm in named_params(cfg, KV_FUNCS):
+        shape = prm.shape
         if ".experts.0." in name or ".mlp.0." in name or name.endswith("layernorm.0.weight") or \
                 name == "backbone.final_norm.0.weight":
             continue  # expert-0 weights are not read by the suffix step
@@ -67,23 +95,22 @@ def step_bytes(cfg, weight_bytes_per_param=2.0, q4=False):
             nbytes += n * 0.5 + (n / 32) * 2  # packed nibbles + fp16 group scales
         else:
             nbytes += n * weight_bytes_per_param
-    kv = d.depth * d.num_kv_heads * d.prefix_len * d.head_dim
+    v = cfg.vlm
+    kv = v.depth * v.num_kv_heads * cfg.prefix_len * v.head_dim
     nbytes += kv * (4 + 2)
-    T, A, hd = d.suffix_len, d.action_dim, d.head_dim
-    nbytes += T * A * 2 + d.ae_width * 2 + 2 * T * hd // 2 * 4 + d.prefix_len * 4 + T * A * 4
+    T, A, hd = cfg.suffix_len, cfg.action_dim, v.head_dim
+    nbytes += T * A * 2 + cfg.action_expert.width * 2 + 2 * T * hd // 2 * 4 + cfg.prefix_len * 4 + T * A * 4
     return nbytes
 
 
 def step_flops(cfg):
-    from oracle import pi0_oracle as O
-
-    d = O.dims_from_config(cfg)
-    T, W, F, H, hd, KV = d.suffix_len, d.ae_width, d.ae_mlp, d.num_heads, d.head_dim, d.num_kv_heads
+    v, a = cfg.vlm, cfg.action_expert
+    T, W, F, H, hd, KV = cfg.suffix_len, a.width, a.mlp_dim, v.num_heads, v.head_dim, v.num_kv_heads
     per_layer = 2 * T * W * (H * hd + 2 * KV * hd) + 2 * T * H * hd * W + 2 * T * W * 2 * F + 2 * T * F * W
-    keys = d.prefix_len + T
+    keys = cfg.prefix_len + T
     per_layer += 2 * 2 * H * T * keys * hd
-    mod = 2 * (2 * d.depth + 1) * 3 * W * W + 2 * 2 * W * W
-    return d.depth * per_layer + mod + 2 * T * d.action_dim * W * 2
+    mod = 2 * (2 * v.depth + 1) * 3 * W * W + 2 * 2 * W * W
+    return v.depth * per_layer + mod + 2 * T * cfg.action_dim * W * 2
 
 
 def op_bytes_flops(cfg, op):
@@ -145,7 +172,7 @@ def cpu_baseline(cfg, seconds):
         O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 50:
+        if el >= seconds or n >= 5000:
             break
     return {"value": round(el / n * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n} float32 denoise_step_kv at the full pi0.5 shape (18 layers, P=968, T=50) "
@@ -154,6 +181,9 @@ def cpu_baseline(cfg, seconds):
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize_trace(args.summarize)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the M1 denoise path is a single-request, single-device path and "
               f"this build has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)

@@ -44,6 +44,14 @@ const char* get_error();
   } while (0)
 
 // ---- device numerics helpers ----------------------------------------------
+// Load through a global-address-space pointer: a pointer the compiler cannot trace to
+// global memory becomes a flat load, which forces a full vmcnt(0) wait at its first use.
+template <class T>
+__device__ __forceinline__ T load_global(const T* p) {
+  typedef const __attribute__((address_space(1))) T gT;
+  return *(gT*)p;
+}
+
 // fp16 <-> fp32 with IEEE round-to-nearest-even (v_cvt_f16_f32 / v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }
 __device__ __forceinline__ _Float16 f2h(float f) { return (_Float16)f; }
@@ -65,6 +73,16 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// The same two functions from the hardware exp2 / reciprocal (about 2 ulp of float32,
+// far below the fp16 rounding their results get): 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u))
+// and x / (1 + e^(-x)).  Saturate correctly: e^(+big) = inf gives x * 0, e^(-big) = 0 gives x.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float gelu_tanh_hw(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  return x * __builtin_amdgcn_rcpf(1.0f + exp_hw(-2.0f * u));
+}
+__device__ __forceinline__ float silu_hw(float x) { return x * __builtin_amdgcn_rcpf(1.0f + exp_hw(-x)); }
 
 // wave-level reductions over lanes l, l^16, l^32 (the 4 row groups of a 16x16 MFMA tile)
 __device__ __forceinline__ float xor_max_16_32(float v) {

@@ -34,7 +34,7 @@ struct Layer {
 };
 
 struct OpDesc {
-  int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0;
+  int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0, seg_tiles = 0;
   bool q4 = false;
 };
 
@@ -79,6 +79,7 @@ struct Ctx {
   // workspaces
   float* skws = nullptr;
   size_t skws_floats = 0;
+  float* zero = nullptr;  // 64*64 zero floats, never written
   unsigned* counters = nullptr;
   size_t ncounters = 0;
   float* attn_ws = nullptr;
@@ -123,12 +124,14 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   op.epi = d.epi;
   op.segs = c.d_segs + d.seg_off;
   op.nseg = d.nseg;
+  op.seg_tiles = d.seg_tiles;
   for (int i = 0; i < d.nseg && i < 3; ++i) op.inl[i] = c.h_segs[d.seg_off + i];
   op.ntiles = d.ntiles;
   const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64);
   op.splitk = p.splitk;
   op.kper = p.kper;
   op.ws = c.skws;
+  op.zero = c.zero;
   op.counters = c.counters;
   op.rowss_ld = c.T;
   op.rowss_tiles = c.rss_tiles;
@@ -388,9 +391,12 @@ int seg_ops(Ctx& c, OpDesc& d, const std::vector<SkSeg>& segs, int K, int epi, b
   d.epi = epi;
   d.q4 = q4;
   int t = 0;
+  d.seg_tiles = segs.empty() ? 0 : (segs[0].n + tile_rows - 1) / tile_rows;
   for (SkSeg s : segs) {
     s.tile0 = t;
-    t += (s.n + tile_rows - 1) / tile_rows;
+    const int nt = (s.n + tile_rows - 1) / tile_rows;
+    if (nt != d.seg_tiles) d.seg_tiles = 0;
+    t += nt;
     c.h_segs.push_back(s);
   }
   d.ntiles = t;
@@ -558,8 +564,10 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   }
   ALLOC(c.skws, c.skws_floats);
   ALLOC(c.counters, c.ncounters);
+  ALLOC(c.zero, 64 * 64);
 #undef ALLOC
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(c.zero, 0, 64 * 64 * sizeof(float)) != hipSuccess ||
       hipStreamCreateWithFlags(&c.cap, hipStreamNonBlocking) != hipSuccess) {
     set_error("context setup failed");
     return fail(-1);
@@ -818,11 +826,16 @@ struct Scratch {
   unsigned* counters = nullptr;
   size_t counters_n = 0;
   SkSeg* seg = nullptr;
+  float* zero = nullptr;
 };
 Scratch g_scratch;
 
 int scratch_reserve(size_t ws_n, size_t counters_n) {
   if (!g_scratch.seg) MLCV_HIP(hipMalloc(&g_scratch.seg, sizeof(SkSeg)));
+  if (!g_scratch.zero) {
+    MLCV_HIP(hipMalloc(&g_scratch.zero, 64 * 64 * sizeof(float)));
+    MLCV_HIP(hipMemset(g_scratch.zero, 0, 64 * 64 * sizeof(float)));
+  }
   if (ws_n > g_scratch.ws_n) {
     if (g_scratch.ws) MLCV_HIP(hipFree(g_scratch.ws));
     MLCV_HIP(hipMalloc(&g_scratch.ws, ws_n * sizeof(float)));
@@ -922,6 +935,7 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
   op.splitk = p.splitk;
   op.kper = p.kper;
   op.ws = g_scratch.ws;
+  op.zero = g_scratch.zero;
   op.counters = g_scratch.counters;
   MLCV_TRY(sk_launch(op, q_weight != nullptr, st));
   MLCV_HIP(hipStreamSynchronize(st));

@@ -4,33 +4,41 @@
 // dequantized in registers.
 //
 // Mapping: D[n][m] = sum_k W[n][k] * X[m][k]: the A operand is a 16-row slab of W
-// (lane l holds 32 contiguous k of row l%16 per 128-k chunk, so one wave reads
-// 16 rows x 256 contiguous bytes), the B operand is X^T read from LDS with the
-// same k permutation.  A workgroup (4 waves) owns 64 consecutive output rows
-// (for GeGLU: 32 gate rows + the matching 32 up rows) and one K slice, taken in
-// rounds of 512; K slices are reduced by the last-arriving workgroup of a tile in
-// a fixed order.
+// (lane l holds row l%16; per 128-k chunk one load instruction covers 64 contiguous
+// bytes of each of the wave's 16 rows), the B operand is X^T read from LDS with the
+// same k order.  A workgroup (4 waves) owns 64 output columns (for GeGLU: 32
+// columns, i.e. their 32 gate + 32 up weight rows) and one K slice of NC*128 per
+// round; K slices of one tile are reduced by the last-arriving workgroup in split
+// order.
 //
-// Latency structure (each kernel moves only 4-17 MB, so one HBM round trip is a
-// large part of its time): every memory phase is one batch of independent loads --
-// all W chunks of a round, then the X slice, then (split-K) all partials, then the
-// epilogue's operands -- never a loop of dependent loads.
+// Every result stays in the MFMA D layout until it is stored: lane (g, r) holds
+// columns n0..n0+3 (n0 = 4g within its wave's 16) of rows r, 16+r, 32+r, 48+r.
+//
+// The kernel is straight-line by construction: a workgroup always computes 4 m
+// tiles and NC chunks per round, loads use clamped (always valid) addresses, and K
+// positions past the slice are zeroed with selects on X.  Conditional MFMAs or
+// conditional loads would make the compiler shuttle the accumulators between
+// register files and split the code into exec-mask blocks, which costs more than
+// the work they skip: with one wave per SIMD every VALU instruction is latency.
 //
 // Row statistics of the adaRMS prologue are not recomputed from x: every epilogue
 // that writes the residual stream x also writes, per 64-column tile, the partial
 // sum of squares of each row (``rowss_out``); the consuming GEMM sums those partials
 // in tile order (``rowss_in``).
+//
+// Split-K partials: with gridDim.x a multiple of 8 the splits of a tile run on one
+// XCD (workgroups are dealt to the 8 XCDs round-robin by linear id), so partials go
+// through that XCD's L2 with plain stores; otherwise they are written through to
+// memory.  The last workgroup to increment the tile counter sums them.
 #include "kernels.h"
 
 namespace mlcv {
 
 namespace {
-constexpr int KC = 128;           // k per chunk (32 per lane group)
-constexpr int RK = 4 * KC;        // k per round (all of it loaded at once)
-constexpr int MB = 64;            // m rows per block
-constexpr int XLD = RK + 8;       // LDS row stride of the X slice (halfs)
-constexpr int TLD = 64 + 4;       // LDS row stride of the fp32 result tile (aliases the X slice)
-constexpr int MAX_SPLIT = 16;
+constexpr int KC = 128;           // k per chunk (4 MFMA k-steps of 32)
+constexpr int MB = 64;            // m rows per block (4 MFMA m tiles)
+constexpr int MAX_SPLIT = 8;
+constexpr int TILE_F = MB * 64;   // floats of one split-K partial tile
 
 // 8 nibbles of a word -> fp16 (q - 7) * s, ordered [n0,n4,n1,n5,n2,n6,n3,n7].
 __device__ __forceinline__ h8 dequant_word(uint32_t word, _Float16 s) {
@@ -66,30 +74,22 @@ struct WRaw<true> {
   _Float16 s;
 };
 
-// Weights of one 128-k chunk at kc for this lane (row `row`, lane group g):
+// Weights of one 128-k chunk at kc for this lane's row (lane group g), clamped into
+// the row so every load is valid (the matching X entries are zero past the slice):
 //   fp16: k-step j holds k = kc + 32j + 8g .. +7 (one load instruction covers 64
-//         contiguous bytes of each of the wave's 16 rows); a k-step at or past kend is 0.
-//   q4:   the 32 nibbles at kc + 32g .. +31 (16 B) and their group scale; the k-step j
+//         contiguous bytes of each of the wave's 16 rows);
+//   q4:   the 32 nibbles at kc + 32g .. +31 (16 B) and their group scale; k-step j
 //         takes dequantized elements 8j..8j+7 in the order [n0,n4,n1,n5,n2,n6,n3,n7].
-// kend is a multiple of 32, so every 32-k step is either fully valid or fully invalid.
 template <bool Q4>
-__device__ __forceinline__ void load_wraw(WRaw<Q4>& f, const SkSeg& seg, int row, bool row_ok, int kc, int g,
-                                          int kend, int K) {
+__device__ __forceinline__ void load_wraw(WRaw<Q4>& f, const SkSeg& seg, int row, int kc, int g, int K) {
   if constexpr (!Q4) {
-    const _Float16* p = seg.w + (size_t)row * K + kc + 8 * g;
+    const _Float16* p = seg.w + (size_t)row * K;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.v[j] = (row_ok && kc + 32 * j < kend) ? *reinterpret_cast<const h8*>(p + 32 * j)
-                                              : (h8){0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < 4; ++j) f.v[j] = load_global(reinterpret_cast<const h8*>(p + min(kc + 32 * j + 8 * g, K - 8)));
   } else {
-    const int k = kc + 32 * g;
-    if (!(row_ok && k < kend)) {
-      f.words = (u4){0x77777777u, 0x77777777u, 0x77777777u, 0x77777777u};  // q = 7 -> 0
-      f.s = (_Float16)0.0f;
-      return;
-    }
-    f.words = *reinterpret_cast<const u4*>(seg.qw + (size_t)row * (K / 8) + k / 8);
-    f.s = seg.qs[(size_t)row * (K / 32) + k / 32];
+    const int k = min(kc + 32 * g, K - 32);
+    f.words = load_global(reinterpret_cast<const u4*>(seg.qw + (size_t)row * (K / 8) + k / 8));
+    f.s = load_global(seg.qs + (size_t)row * (K / 32) + k / 32);
   }
 }
 
@@ -99,305 +99,293 @@ __device__ __forceinline__ h8 wfrag(const WRaw<Q4>& f, int j) {
   else return dequant_word(f.words[j], f.s);
 }
 
-__device__ __forceinline__ void load16h(const _Float16* p, float out[16]) {
-  const h8 a = reinterpret_cast<const h8*>(p)[0];
-  const h8 b = reinterpret_cast<const h8*>(p)[1];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    out[e] = h2f(a[e]);
-    out[8 + e] = h2f(b[e]);
-  }
-}
-
-template <bool Q4, bool NORM>
+template <bool Q4, bool NORM, int EPI, int NC, bool TABLE>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
+  constexpr int XK = NC * KC;      // k per round
+  constexpr int XLD = XK + 8;      // LDS row stride of the X slice (halfs)
+  constexpr int TPR = XK / 8;      // threads per X row
+  constexpr int RPP = 256 / TPR;   // X rows per load pass
+  constexpr int NXL = MB / RPP;    // X loads per thread
   __shared__ __attribute__((aligned(16))) _Float16 xs[MB * XLD];
-  __shared__ float denom[MB];  // 1 / sqrt(mean(x^2) + eps) per row
+  __shared__ float denom[4][MB];   // 1 / sqrt(mean(x^2) + eps) per row, one copy per wave
+  __shared__ float red[4][MB];     // per-wave row sums of squares (rowss_out)
   __shared__ int is_last;
-  float* tile = reinterpret_cast<float*>(xs);  // result tile [m][n_local], reuses the X slice
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int tile_id = blockIdx.x, s = blockIdx.y, mb = blockIdx.z;
+  const int S = gridDim.y;
   const int m0 = mb * MB;
+  const int mlast = op.M - 1;
   const int mrows = min(MB, op.M - m0);
-  const int MT = (mrows + 15) >> 4;
 
-  int si = 0;
+  // the segment: up to 3 from the kernel arguments, picked by selects (no branch on an
+  // argument value, so every argument load issues at once), or from a device table of
+  // equal-sized segments (one dependent load)
   SkSeg seg;
-  if (op.nseg <= 3) {  // kernel arguments: no dependent global load before the weight stream
-    if (op.nseg > 1 && op.inl[1].tile0 <= tile_id) si = 1;
-    if (op.nseg > 2 && op.inl[2].tile0 <= tile_id) si = 2;
-    seg = op.inl[si];
+  if constexpr (!TABLE) {
+    const SkSeg s0 = op.inl[0], s1 = op.inl[1], s2 = op.inl[2];
+    const bool u1 = op.nseg > 1 && tile_id >= s1.tile0;
+    const bool u2 = op.nseg > 2 && tile_id >= s2.tile0;
+    seg = u2 ? s2 : (u1 ? s1 : s0);
   } else {
-    while (si + 1 < op.nseg && op.segs[si + 1].tile0 <= tile_id) ++si;
-    seg = op.segs[si];
+    seg = op.segs[tile_id / op.seg_tiles];
   }
   const int lt = tile_id - seg.tile0;
-  const bool geglu = op.epi == EPI_GEGLU;
-  const int row = geglu ? ((w < 2) ? (32 * lt + 16 * w + r16) : (op.geglu_F + 32 * lt + 16 * (w - 2) + r16))
-                        : (64 * lt + 16 * w + r16);
-  const bool row_ok = geglu ? true : (row < seg.n);
-
   const int K = op.K;
   const int kbeg = s * op.kper;
   const int kend = min(K, kbeg + op.kper);
+  const int row = (EPI == EPI_GEGLU) ? (r16 < 8 ? 0 : op.geglu_F) + 32 * lt + 8 * w + (r16 & 7)
+                                     : min(64 * lt + 16 * w + r16, seg.n - 1);
+  // output columns n0..n0+3 of this lane (GeGLU: lanes g < 2 own the outputs)
+  const int n0 = (EPI == EPI_GEGLU) ? 32 * lt + 8 * w + 4 * (g & 1) : 64 * lt + 16 * w + 4 * g;
+  const int ncl = max(0, min(n0, seg.n - 4));
+  const bool nok = n0 < seg.n;
+  const size_t ldo = (size_t)seg.ldo;
+  const bool has_bias = seg.bias != nullptr;
 
-  // adaRMS row statistics: the producer's per-tile partial sums of squares, issued first
-  // and summed in tile order once the X / W loads of the first round are in flight
+  // ---- epilogue operands first: they do not depend on the product ---------------
+  h4 xo[4], gq = (h4){0, 0, 0, 0}, bq = (h4){0, 0, 0, 0};
+  f4 x32o[4];
+  const _Float16* zero_h = reinterpret_cast<const _Float16*>(op.zero);
+  if constexpr (EPI == EPI_GATED_RES) {
+    const _Float16* xb = reinterpret_cast<const _Float16*>(seg.out);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      xo[mt] = *reinterpret_cast<const h4*>(xb + (size_t)min(m0 + 16 * mt + r16, mlast) * ldo + ncl);
+    gq = *reinterpret_cast<const h4*>(op.gate + ncl);
+  }
+  if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU || EPI == EPI_VOUT || EPI == EPI_EULER) {
+    bq = load_global(reinterpret_cast<const h4*>(has_bias ? seg.bias + ncl : zero_h));
+  }
+  if constexpr (EPI == EPI_EULER) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      x32o[mt] = *reinterpret_cast<const f4*>(op.x32 + (size_t)min(m0 + 16 * mt + r16, mlast) * ldo + ncl);
+  }
+
+  // adaRMS row statistics: the producer's per-tile partial sums of squares, one row per
+  // lane; every wave loads them and keeps its own copy of the row scales (no barrier)
   float rss[16];
   if constexpr (NORM) {
+    const int m = min(m0 + lane, mlast);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      rss[i] = (tid < mrows && i < op.rowss_tiles) ? op.rowss_in[(size_t)i * op.rowss_ld + m0 + tid] : 0.f;
+    for (int t = 0; t < 16; ++t) rss[t] = op.rowss_in[(size_t)min(t, op.rowss_tiles - 1) * op.rowss_ld + m];
   }
 
   f4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  for (int kr = kbeg; kr < kend; kr += RK) {
-    // (1) the X slice [64 rows][512 k] first (L2-resident, and vmcnt retires in order):
-    //     thread -> 8 consecutive k (tid % 64) of rows tid/64 + 4i
-    const int kk = (tid & 63) * 8, mr = tid >> 6;
+  // one round: rounds after the first run in a loop, the first is peeled so that the
+  // prefetched loads above stay in flight (a loop header would wait for all of them)
+  const int kk = (tid % TPR) * 8, mr = tid / TPR;
+  auto round = [&](const int kr, const bool first) __attribute__((always_inline)) {
+    // (1) the X slice [64 rows][XK]: thread -> 8 consecutive k of rows mr + RPP*i (rows
+    //     past M repeat the last row; k past the slice is zeroed below)
     const int kg = kr + kk;
     const bool kok = kg < kend;
-    h8 v[16];
+    const int kgc = min(kg, K - 8);
+    h8 v[NXL];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = mr + 4 * i;
-      v[i] = (kok && m < mrows) ? *reinterpret_cast<const h8*>(op.x + (size_t)(m0 + m) * op.ldx + kg)
-                                : (h8){0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int i = 0; i < NXL; ++i)
+      v[i] = *reinterpret_cast<const h8*>(op.x + (size_t)min(m0 + mr + RPP * i, mlast) * op.ldx + kgc);
     h8 sc = (h8){0, 0, 0, 0, 0, 0, 0, 0}, sh = sc;
     if constexpr (NORM) {
-      if (kok) {
-        sc = *reinterpret_cast<const h8*>(op.scale + kg);
-        sh = *reinterpret_cast<const h8*>(op.shift + kg);
-      }
+      sc = *reinterpret_cast<const h8*>(op.scale + kgc);
+      sh = *reinterpret_cast<const h8*>(op.shift + kgc);
     }
     // (2) then every weight chunk of this round
-    WRaw<Q4> wr[4];
+    WRaw<Q4> wr[NC];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int kc = kr + c * KC;
-      load_wraw<Q4>(wr[c], seg, row, row_ok, kc, g, kend, K);
-    }
-    if (NORM && kr == kbeg) {
-      if (tid < mrows) {
+    for (int c = 0; c < NC; ++c) load_wraw<Q4>(wr[c], seg, row, kr + c * KC, g, K);
+    if constexpr (NORM) {
+      if (first) {
         float ssum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ssum += rss[i];
-        for (int grp = 16; grp < op.rowss_tiles; grp += 16)  // widths > 1024 only
-          for (int i = grp; i < min(grp + 16, op.rowss_tiles); ++i) ssum += op.rowss_in[(size_t)i * op.rowss_ld + m0 + tid];
-        denom[tid] = 1.0f / sqrtf(ssum / (float)K + op.eps);  // reciprocal of the rms
+        for (int t = 0; t < 16; ++t) ssum += t < op.rowss_tiles ? rss[t] : 0.f;
+        const int m = min(m0 + lane, mlast);
+        for (int t = 16; t < op.rowss_tiles; ++t) ssum += op.rowss_in[(size_t)t * op.rowss_ld + m];  // K > 1024
+        denom[w][lane] = 1.0f / sqrtf(ssum / (float)K + op.eps);  // read back by this wave only
       }
-      __syncthreads();
     }
-    // (3) normalize the X slice into LDS while the weights are in flight
-    {
+    // (3) normalize / mask the X slice into LDS while the weights are in flight
+    float a1[8], b1[8];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a1[e] = kok ? 1.0f + h2f(sc[e]) : 0.f;
+        b1[e] = kok ? h2f(sh[e]) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NXL; ++i) {
+      const int m = mr + RPP * i;
+      h8 o;
       if constexpr (NORM) {
-        float sc1[8], shf[8];
+        const float rinv = denom[w][m];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          sc1[e] = 1.0f + h2f(sc[e]);
-          shf[e] = h2f(sh[e]);
-        }
+        for (int e = 0; e < 8; ++e) o[e] = f2h(fmaf(h2f(v[i][e]) * rinv, a1[e], b1[e]));
+      } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int m = mr + 4 * i;
-          const float rinv = m < mrows ? denom[m] : 1.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float nrm = h2f(v[i][e]) * rinv;
-            v[i][e] = (m < mrows && kok) ? f2h(nrm * sc1[e] + shf[e]) : (_Float16)0.0f;
-          }
-        }
+        for (int e = 0; e < 8; ++e) o[e] = kok ? v[i][e] : (_Float16)0.0f;
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const h8 o = Q4 ? perm8(v[i]) : v[i];
-        *reinterpret_cast<h8*>(&xs[(mr + 4 * i) * XLD + kk]) = o;
-      }
+      if constexpr (Q4) o = perm8(o);
+      *reinterpret_cast<h8*>(&xs[m * XLD + kk]) = o;
     }
     __syncthreads();
     // (4) MFMA over the round
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (kr + c * KC < kend) {
+    for (int c = 0; c < NC; ++c) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h8 a = wfrag<Q4>(wr[c], j);
+      for (int j = 0; j < 4; ++j) {
+        const h8 a = wfrag<Q4>(wr[c], j);
+        const int ko = Q4 ? 32 * g + 8 * j : 32 * j + 8 * g;
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            if (mt < MT) {
-              const int ko = Q4 ? 32 * g + 8 * j : 32 * j + 8 * g;
-              const h8 b = *reinterpret_cast<const h8*>(&xs[(mt * 16 + r16) * XLD + c * KC + ko]);
-              acc[mt] = mfma16x16x32(a, b, acc[mt]);
-            }
-          }
+        for (int mt = 0; mt < 4; ++mt) {
+          const h8 b = *reinterpret_cast<const h8*>(&xs[(mt * 16 + r16) * XLD + c * KC + ko]);
+          acc[mt] = mfma16x16x32(a, b, acc[mt]);
         }
       }
     }
     __syncthreads();
-  }
+  };
+  round(kbeg, true);
+  for (int kr = kbeg + XK; kr < kend; kr += XK) round(kr, false);
 
-  // ---- result tile in LDS: tile[m][n_local] ---------------------------------
-  if (gridDim.y == 1) {
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      if (mt < MT) *reinterpret_cast<f4*>(&tile[(mt * 16 + r16) * TLD + 16 * w + 4 * g]) = acc[mt];
-    __syncthreads();
-  } else {
-    // partials through the coherent memory side, reduced by the last workgroup of the tile
+  // ---- split-K: partials of every split, summed by the last workgroup in split order ----
+  if (S > 1) {
     const int cidx = tile_id * gridDim.z + mb;
-    float* wsp = op.ws + ((size_t)cidx * gridDim.y + s) * (MB * 64);
+    float* wsp = op.ws + ((size_t)cidx * S + s) * TILE_F + (size_t)r16 * 64 + 16 * w + 4 * g;
+    if ((gridDim.x & 7) == 0) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int mm = mt * 16 + r16;
-      if (mt < MT && mm < mrows)
+      for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f4*>(wsp + mt * 16 * 64) = acc[mt];
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_coherent(&wsp[mm * 64 + 16 * w + 4 * g + i], acc[mt][i]);
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_coherent(wsp + mt * 16 * 64 + i, acc[mt][i]);
     }
     wait_all_memory();
     __syncthreads();
-    if (tid == 0) is_last = counter_add(&op.counters[cidx], 1u) == gridDim.y - 1;
+    if (tid == 0) is_last = counter_add(&op.counters[cidx], 1u) == (unsigned)(S - 1);
     __syncthreads();
     if (!is_last) return;
-    // every other split's partial has been written through before its counter add;
-    // drop any stale cached copies, then read them with plain vector loads
-    if (w == 0) acquire_agent();
-    __syncthreads();
-    const int mm = tid >> 2, cc = (tid & 3) * 16;
-    if (mm < mrows) {
-      const float* base = op.ws + (size_t)cidx * gridDim.y * (MB * 64) + mm * 64 + cc;
-      f4 sum[4];
+    // XCD-local: the partials are in this XCD's L2 and this CU's L1 has never held
+    // these lines in this kernel, so plain loads see them; otherwise drop stale copies
+    if ((gridDim.x & 7) != 0) acquire_agent();
+    const size_t lo = (size_t)r16 * 64 + 16 * w + 4 * g;
+    const float* base = op.ws + (size_t)cidx * S * TILE_F + lo;
+    f4 part[MAX_SPLIT][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sum[i] = (f4){0.f, 0.f, 0.f, 0.f};
-      const int S = gridDim.y;
+    for (int q = 0; q < MAX_SPLIT; ++q) {
+      const float* src = q < S ? base + (size_t)q * TILE_F : op.zero + lo;  // missing splits read zeros
 #pragma unroll
-      for (int grp = 0; grp < MAX_SPLIT; grp += 8) {
-        if (grp < S) {
-          f4 part[8][4];
+      for (int mt = 0; mt < 4; ++mt) part[q][mt] = *reinterpret_cast<const f4*>(src + mt * 16 * 64);
+    }
 #pragma unroll
-          for (int q = 0; q < 8; ++q)
+    for (int mt = 0; mt < 4; ++mt) {
+      f4 sum = part[0][mt];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              part[q][i] = (grp + q < S) ? reinterpret_cast<const f4*>(base + (size_t)(grp + q) * (MB * 64))[i]
-                                         : (f4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int q = 0; q < 8; ++q)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sum[i] += part[q][i];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<f4*>(&tile[mm * TLD + cc + 4 * i]) = sum[i];
+      for (int q = 1; q < MAX_SPLIT; ++q) sum += part[q][mt];
+      acc[mt] = sum;
     }
     if (tid == 0) counter_reset(&op.counters[cidx]);
-    __syncthreads();
   }
 
-  // ---- epilogue: thread -> row m, 16 consecutive output columns ----------------
-  const int m = tid >> 2, c0 = (tid & 3) * 16;
-  const int epi = op.epi;
-  const bool mok = m < mrows;
-  float a[16];
+  // ---- epilogue in the D layout: row m0 + 16mt + r16, columns n0..n0+3 ------------
+  bool mok[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) a[i] = mok ? tile[m * TLD + c0 + i] : 0.f;
-  const size_t mo = (size_t)(m0 + m) * seg.ldo;
-  if (epi == EPI_GEGLU) {
-    if (mok && c0 < 32) {
-      h8 o[2];
+  for (int mt = 0; mt < 4; ++mt) mok[mt] = 16 * mt + r16 < mrows;
+
+  if constexpr (EPI == EPI_GEGLU) {
+    // lanes g < 2 hold 4 gate columns, lane ^ 32 the matching 4 up columns: the pair
+    // swaps halves so that each lane finishes 2 columns (g < 2: the first two)
+    const bool lo = g < 2;
+    const int col = n0 + (lo ? 0 : 2);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const _Float16 gv = f2h(a[i]);
-        const _Float16 uv = f2h(tile[m * TLD + 32 + c0 + i]);
-        o[i >> 3][i & 7] = hmul(f2h(gelu_tanh(h2f(gv))), uv);
-      }
-      h8* dst = reinterpret_cast<h8*>(reinterpret_cast<_Float16*>(seg.out) + mo + 32 * lt + c0);
-      dst[0] = o[0];
-      dst[1] = o[1];
+    for (int mt = 0; mt < 4; ++mt) {
+      const float r0 = __shfl_xor(lo ? acc[mt][2] : acc[mt][0], 32);
+      const float r1 = __shfl_xor(lo ? acc[mt][3] : acc[mt][1], 32);
+      const float ga = lo ? acc[mt][0] : r0, gb = lo ? acc[mt][1] : r1;
+      const float ua = lo ? r0 : acc[mt][2], ub = lo ? r1 : acc[mt][3];
+      h2 o;
+      o[0] = hmul(f2h(gelu_tanh_hw(h2f(f2h(ga)))), f2h(ua));
+      o[1] = hmul(f2h(gelu_tanh_hw(h2f(f2h(gb)))), f2h(ub));
+      if (mok[mt] && nok)
+        *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(seg.out) + (size_t)(m0 + 16 * mt + r16) * ldo + col) = o;
     }
     return;
   }
-  const int n0 = 64 * lt + c0;
-  const bool full = mok && n0 + 16 <= seg.n;
-  float ss = 0.f;  // row sum of squares of the new x over these columns
-  if (epi == EPI_GATED_RES) {
-    if (full) {
-      _Float16* xo = reinterpret_cast<_Float16*>(seg.out) + mo + n0;
-      float xv[16], gv[16];
-      load16h(xo, xv);
-      load16h(op.gate + n0, gv);
-      h8 o[2];
+
+  float ss[4];  // row sums of squares of the stored x over this lane's 4 columns
+  if constexpr (EPI == EPI_GATED_RES) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const _Float16 r = hadd(f2h(xv[i]), hmul(f2h(a[i]), f2h(gv[i])));
-        o[i >> 3][i & 7] = r;
-        ss += h2f(r) * h2f(r);
+    for (int mt = 0; mt < 4; ++mt) {
+      h4 o;
+      float s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 r = hadd(xo[mt][i], hmul(f2h(acc[mt][i]), gq[i]));
+        o[i] = r;
+        s2 += h2f(r) * h2f(r);
       }
-      reinterpret_cast<h8*>(xo)[0] = o[0];
-      reinterpret_cast<h8*>(xo)[1] = o[1];
-    } else if (mok) {
-      for (int i = 0; i < 16 && n0 + i < seg.n; ++i) {
-        _Float16* xo = reinterpret_cast<_Float16*>(seg.out) + mo + n0 + i;
-        const _Float16 r = hadd(*xo, hmul(f2h(a[i]), op.gate[n0 + i]));
-        *xo = r;
-        ss += h2f(r) * h2f(r);
-      }
+      if (mok[mt] && nok)
+        *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + (size_t)(m0 + 16 * mt + r16) * ldo + n0) = o;
+      ss[mt] = nok ? s2 : 0.f;
     }
   } else {
-    float bv[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) bv[i] = 0.f;
-    if (seg.bias) {
-      if (full) {
-        load16h(seg.bias + n0, bv);
-      } else if (mok) {
-        for (int i = 0; i < 16 && n0 + i < seg.n; ++i) bv[i] = h2f(seg.bias[n0 + i]);
+    for (int mt = 0; mt < 4; ++mt) {
+      h4 y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        _Float16 t = f2h(acc[mt][i]);
+        if (has_bias) t = hadd(t, bq[i]);
+        if constexpr (EPI == EPI_STORE_SILU) t = f2h(silu_hw(h2f(t)));
+        y[i] = t;
       }
-    }
-    _Float16 y[16];
+      const size_t mo = (size_t)(m0 + 16 * mt + r16) * ldo + n0;
+      float s2 = 0.f;
+      if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU) {
+        if (mok[mt] && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = y;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      y[i] = f2h(a[i]);
-      if (seg.bias) y[i] = hadd(y[i], f2h(bv[i]));
-      if (epi == EPI_STORE_SILU) y[i] = f2h(silu(h2f(y[i])));
-    }
-    if (epi == EPI_STORE || epi == EPI_STORE_SILU) {
-      _Float16* o = reinterpret_cast<_Float16*>(seg.out) + mo + n0;
-      if (full) {
-        h8 v0, v1;
+        for (int i = 0; i < 4; ++i) s2 += h2f(y[i]) * h2f(y[i]);
+      } else if constexpr (EPI == EPI_VOUT) {
+        if (mok[mt] && nok)
+          *reinterpret_cast<f4*>(reinterpret_cast<float*>(seg.out) + mo) = (f4){h2f(y[0]), h2f(y[1]), h2f(y[2]), h2f(y[3])};
+      } else if constexpr (EPI == EPI_EULER) {
+        f4 nx;
+        h4 nh;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v0[i] = y[i];
-          v1[i] = y[8 + i];
+        for (int i = 0; i < 4; ++i) {
+          nx[i] = euler_update(x32o[mt][i], op.dt, h2f(y[i]));
+          nh[i] = f2h(nx[i]);
         }
-        reinterpret_cast<h8*>(o)[0] = v0;
-        reinterpret_cast<h8*>(o)[1] = v1;
-      } else if (mok) {
-        for (int i = 0; i < 16 && n0 + i < seg.n; ++i) o[i] = y[i];
+        if (mok[mt] && nok) {
+          *reinterpret_cast<f4*>(op.x32 + mo) = nx;
+          *reinterpret_cast<h4*>(op.x16 + mo) = nh;
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (mok && n0 + i < seg.n) ss += h2f(y[i]) * h2f(y[i]);
-    } else if (epi == EPI_VOUT) {
-      if (mok)
-        for (int i = 0; i < 16 && n0 + i < seg.n; ++i) reinterpret_cast<float*>(seg.out)[mo + n0 + i] = h2f(y[i]);
-    } else if (epi == EPI_EULER) {
-      if (mok)
-        for (int i = 0; i < 16 && n0 + i < seg.n; ++i) {
-          const float nx = euler_update(op.x32[mo + n0 + i], op.dt, h2f(y[i]));
-          op.x32[mo + n0 + i] = nx;
-          op.x16[mo + n0 + i] = f2h(nx);
-        }
+      ss[mt] = nok ? s2 : 0.f;
     }
   }
-  if (op.rowss_out) {
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    if ((tid & 3) == 0 && mok) op.rowss_out[(size_t)lt * op.rowss_ld + m0 + m] = ss;
+  if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
+    if (op.rowss_out) {
+      // over the wave's 16 columns (lanes g), then over the 4 waves in order
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        ss[mt] += __shfl_xor(ss[mt], 16);
+        ss[mt] += __shfl_xor(ss[mt], 32);
+      }
+      if (g == 0) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) red[w][16 * mt + r16] = ss[mt];
+      }
+      __syncthreads();
+      if (w == 0 && lane < mrows)
+        op.rowss_out[(size_t)lt * op.rowss_ld + m0 + lane] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    }
   }
 }
 
@@ -452,6 +440,42 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ qw, const _Float1
   }
 }
 
+template <bool Q4, bool NORM, int EPI, bool TABLE = false>
+int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
+  switch (nc) {
+    case 1: skinny_kernel<Q4, NORM, EPI, 1, TABLE><<<grid, 256, 0, st>>>(op); break;
+    case 2: skinny_kernel<Q4, NORM, EPI, 2, TABLE><<<grid, 256, 0, st>>>(op); break;
+    default: skinny_kernel<Q4, NORM, EPI, 4, TABLE><<<grid, 256, 0, st>>>(op); break;
+  }
+  return 0;
+}
+
+template <bool Q4>
+int launch_q(const SkOp& op, bool norm, int nc, dim3 grid, hipStream_t st) {
+  if (op.nseg > 3) {
+    MLCV_REQUIRE(!norm && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs,
+                 "more than 3 weight segments need equal sizes, a plain store and no prologue");
+    return launch_nc<Q4, false, EPI_STORE, true>(op, nc, grid, st);
+  }
+  if (norm) {
+    switch (op.epi) {
+      case EPI_STORE: return launch_nc<Q4, true, EPI_STORE>(op, nc, grid, st);
+      case EPI_GEGLU: return launch_nc<Q4, true, EPI_GEGLU>(op, nc, grid, st);
+      case EPI_VOUT: return launch_nc<Q4, true, EPI_VOUT>(op, nc, grid, st);
+      case EPI_EULER: return launch_nc<Q4, true, EPI_EULER>(op, nc, grid, st);
+      default: break;
+    }
+  } else {
+    switch (op.epi) {
+      case EPI_STORE: return launch_nc<Q4, false, EPI_STORE>(op, nc, grid, st);
+      case EPI_STORE_SILU: return launch_nc<Q4, false, EPI_STORE_SILU>(op, nc, grid, st);
+      case EPI_GATED_RES: return launch_nc<Q4, false, EPI_GATED_RES>(op, nc, grid, st);
+      default: break;
+    }
+  }
+  MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
+}
+
 }  // namespace
 
 SkPlan sk_plan(int ntiles, int K, int mblocks) {
@@ -460,7 +484,7 @@ SkPlan sk_plan(int ntiles, int K, int mblocks) {
   const int blocks = ntiles * mblocks;
   int want = (256 + blocks - 1) / blocks;
   if (want < 1) want = 1;
-  if (want > 8) want = 8;
+  if (want > MAX_SPLIT) want = MAX_SPLIT;
   if (want > chunks) want = chunks;
   const int cps = (chunks + want - 1) / want;
   SkPlan p;
@@ -470,25 +494,30 @@ SkPlan sk_plan(int ntiles, int K, int mblocks) {
 }
 
 size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p) {
-  return p.splitk > 1 ? (size_t)ntiles * mblocks * p.splitk * MB * 64 : 0;
+  return p.splitk > 1 ? (size_t)ntiles * mblocks * p.splitk * TILE_F : 0;
 }
 
 int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
-  MLCV_REQUIRE(op.K % 32 == 0, "skinny GEMM needs K % 32 == 0");
+  MLCV_REQUIRE(op.K % 32 == 0 && op.K >= 32, "skinny GEMM needs K % 32 == 0");
   MLCV_REQUIRE(op.M >= 1, "skinny GEMM needs M >= 1");
   MLCV_REQUIRE(op.splitk >= 1 && op.splitk <= MAX_SPLIT, "skinny GEMM split count");
+  MLCV_REQUIRE(op.kper % KC == 0 && (long)op.kper * op.splitk >= op.K, "skinny GEMM split plan");
+  MLCV_REQUIRE(op.zero != nullptr, "skinny GEMM needs the zero page");
+  MLCV_REQUIRE(op.splitk == 1 || (op.ws && op.counters), "skinny GEMM split-K workspace missing");
   MLCV_REQUIRE(op.scale == nullptr || (op.rowss_in && op.rowss_tiles >= 1),
                "adaRMS prologue needs the producer's row statistics");
+  MLCV_REQUIRE(op.ldx % 8 == 0, "skinny GEMM needs 16-byte aligned X rows");
+  MLCV_REQUIRE(op.nseg >= 1, "skinny GEMM needs a weight segment");
+  for (int i = 0; i < op.nseg && i < 3; ++i) {
+    MLCV_REQUIRE(op.inl[i].n % 4 == 0 && op.inl[i].ldo % 4 == 0, "skinny GEMM outputs need n % 4 == 0");
+  }
   const int mblocks = (op.M + MB - 1) / MB;
   dim3 grid(op.ntiles, op.splitk, mblocks);
   const bool norm = op.scale != nullptr;
-  if (q4) {
-    if (norm) skinny_kernel<true, true><<<grid, 256, 0, st>>>(op);
-    else skinny_kernel<true, false><<<grid, 256, 0, st>>>(op);
-  } else {
-    if (norm) skinny_kernel<false, true><<<grid, 256, 0, st>>>(op);
-    else skinny_kernel<false, false><<<grid, 256, 0, st>>>(op);
-  }
+  const int cps = op.kper / KC;
+  const int nc = cps >= 3 ? 4 : cps;
+  if (q4) MLCV_TRY(launch_q<true>(op, norm, nc, grid, st));
+  else MLCV_TRY(launch_q<false>(op, norm, nc, grid, st));
   MLCV_HIP(hipGetLastError());
   return 0;
 }

@@ -50,8 +50,10 @@ struct SkOp {
   SkSeg inl[3];          // segments passed by value (nseg <= 3)
   const SkSeg* segs;     // device table when nseg > 3
   int nseg, ntiles;
+  int seg_tiles;         // > 0: every segment has this many tiles (direct table index)
   int splitk, kper;
   float* ws;             // split-K partials
+  const float* zero;     // >= 64*64 zero floats, never written (missing splits, absent bias)
   unsigned* counters;    // per (tile, m-block), zero between launches
   float dt;              // EPI_EULER
   float* x32;            // EPI_EULER state [M][ldo]
