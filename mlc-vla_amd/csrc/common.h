@@ -103,6 +103,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+// 16x16x16 f16: lane l holds A[l%16][4(l/16)+i], B[4(l/16)+i][l%16], D[4(l/16)+i][l%16]
+__device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }

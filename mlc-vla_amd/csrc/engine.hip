@@ -536,8 +536,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   }
   // attention split plans and workspace
   const int st_rows = T * (c.H / c.KV), pf_rows = c.P * (c.H / c.KV);
-  attn_plan(st_rows, c.P + T, 256, &c.st_nsplit, &c.st_kps);
-  attn_plan(pf_rows, c.P, 256, &c.pf_nsplit, &c.pf_kps);
+  attn_plan(st_rows, c.P, T, 128, &c.st_nsplit, &c.st_kps);
+  attn_plan(pf_rows, c.P, 0, 256, &c.pf_nsplit, &c.pf_kps);
   c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
                                 attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
   ALLOC(c.attn_ws, c.attn_ws_floats_n);
@@ -881,7 +881,7 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
   a.out_ld = H * hd;
   a.rows = Tq * (H / KV);
   a.rpad = ((a.rows + 63) / 64) * 64;
-  attn_plan(a.rows, Sp + Ts, 256, &a.nsplit, &a.kps);
+  attn_plan(a.rows, Sp, Ts, 128, &a.nsplit, &a.kps);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
   const size_t need = attn_ws_floats(KV, a.rows, hd, a.nsplit);
   MLCV_TRY(scratch_reserve(need, 1));

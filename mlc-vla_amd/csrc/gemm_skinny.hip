@@ -99,6 +99,23 @@ __device__ __forceinline__ h8 wfrag(const WRaw<Q4>& f, int j) {
   else return dequant_word(f.words[j], f.s);
 }
 
+// acc[mt] = sum over the NS split partials of this lane's 4 columns, in split order
+template <int NS>
+__device__ __forceinline__ void sum_splits(const float* base, f4* acc) {
+  f4 part[NS][4];
+#pragma unroll
+  for (int q = 0; q < NS; ++q)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) part[q][mt] = *reinterpret_cast<const f4*>(base + (size_t)q * TILE_F + mt * 16 * 64);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    f4 sum = part[0][mt];
+#pragma unroll
+    for (int q = 1; q < NS; ++q) sum += part[q][mt];
+    acc[mt] = sum;
+  }
+}
+
 template <bool Q4, bool NORM, int EPI, int NC, bool TABLE>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   constexpr int XK = NC * KC;      // k per round
@@ -274,21 +291,15 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     // XCD-local: the partials are in this XCD's L2 and this CU's L1 has never held
     // these lines in this kernel, so plain loads see them; otherwise drop stale copies
     if ((gridDim.x & 7) != 0) acquire_agent();
-    const size_t lo = (size_t)r16 * 64 + 16 * w + 4 * g;
-    const float* base = op.ws + (size_t)cidx * S * TILE_F + lo;
-    f4 part[MAX_SPLIT][4];
-#pragma unroll
-    for (int q = 0; q < MAX_SPLIT; ++q) {
-      const float* src = q < S ? base + (size_t)q * TILE_F : op.zero + lo;  // missing splits read zeros
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) part[q][mt] = *reinterpret_cast<const f4*>(src + mt * 16 * 64);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      f4 sum = part[0][mt];
-#pragma unroll
-      for (int q = 1; q < MAX_SPLIT; ++q) sum += part[q][mt];
-      acc[mt] = sum;
+    const float* base = op.ws + (size_t)cidx * S * TILE_F + (size_t)r16 * 64 + 16 * w + 4 * g;
+    switch (S) {  // every partial of the tile in one batch of loads, summed in split order
+      case 2: sum_splits<2>(base, acc); break;
+      case 3: sum_splits<3>(base, acc); break;
+      case 4: sum_splits<4>(base, acc); break;
+      case 5: sum_splits<5>(base, acc); break;
+      case 6: sum_splits<6>(base, acc); break;
+      case 7: sum_splits<7>(base, acc); break;
+      default: sum_splits<8>(base, acc); break;
     }
     if (tid == 0) counter_reset(&op.counters[cidx]);
   }

@@ -53,7 +53,7 @@ struct SkOp {
   int seg_tiles;         // > 0: every segment has this many tiles (direct table index)
   int splitk, kper;
   float* ws;             // split-K partials
-  const float* zero;     // >= 64*64 zero floats, never written (missing splits, absent bias)
+  const float* zero;     // >= 64*64 zero floats, never written (absent bias)
   unsigned* counters;    // per (tile, m-block), zero between launches
   float dt;              // EPI_EULER
   float* x32;            // EPI_EULER state [M][ldo]
@@ -96,10 +96,11 @@ struct AttnArgs {
   int out_ld;
   float* part_o;         // [KV][nsplit][Rpad][hd]
   float* part_ml;        // [KV][nsplit][Rpad][2]
-  int nsplit, kps;       // splits and keys per split (multiple of 32)
+  int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
   int rows, rpad;        // rows per kv head (Tq*H/KV) and padded
 };
-void attn_plan(int rows, int keys, int target_blocks, int* nsplit, int* kps);
+// nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
+void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps);
 size_t attn_ws_floats(int KV, int rows, int hd, int nsplit);
 int attn_launch(const AttnArgs& a, hipStream_t st);
 
