@@ -48,7 +48,48 @@ def parse():
     ap.add_argument("--no-q4", action="store_true")
     ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
                     help="print a per-kernel, per-launch-shape table of a rocprofv3 --kernel-trace CSV and exit")
+    ap.add_argument("--summarize-pmc", metavar="COUNTER_CSV",
+                    help="print the mean of each counter per dispatch of a rocprofv3 --pmc CSV, by kernel and "
+                         "launch shape, and exit")
+    ap.add_argument("--only-op", choices=sorted(OPS_PER_STEP), default=None,
+                    help="after set-up, run --op-iters launches of one op of the step and exit (for --pmc runs)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="run --op-iters device copies of this many MiB and exit (counter calibration)")
     return ap.parse_args()
+
+
+def kernel_name(raw):
+    """Short kernel name: drop 'void ', the anonymous namespace and the parameter list."""
+    n = raw[5:] if raw.startswith("void ") else raw
+    n = n.replace("mlcv::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    if n.endswith(")"):
+        depth = 0
+        for i in range(len(n) - 1, -1, -1):
+            depth += n[i] == ")"
+            depth -= n[i] == "("
+            if depth == 0:
+                n = n[:i]
+                break
+    return n
+
+
+def summarize_pmc(path):
+    """Markdown table of a rocprofv3 --pmc counter CSV: mean per dispatch by (kernel, grid, workgroup)."""
+    import csv
+
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            key = (kernel_name(r["Kernel_Name"]), r["Grid_Size"], r["Workgroup_Size"])
+            d = per.setdefault(key, {}).setdefault(r["Counter_Name"], {})
+            d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    counters = sorted({c for v in per.values() for c in v})
+    print("| kernel | grid (threads) | workgroup | dispatches | " + " | ".join(f"{c} (mean)" for c in counters) + " |")
+    print("|---|---|---|---|" + "---|" * len(counters))
+    for key, cs in sorted(per.items(), key=lambda kv: -max(len(v) for v in kv[1].values())):
+        n = max(len(v) for v in cs.values())
+        vals = [f"{sum(cs[c].values()) / len(cs[c]):.1f}" if c in cs else "" for c in counters]
+        print(f"| {key[0][:48]} | {key[1]} | {key[2]} | {n} | " + " | ".join(vals) + " |")
 
 
 def summarize_trace(path):
@@ -59,8 +100,7 @@ def summarize_trace(path):
     total = 0
     with open(path) as f:
         for r in csv.DictReader(f):
-            name = r["Kernel_Name"]
-            name = name.split("(")[0].replace("mlcv::(anonymous namespace)::", "")
+            name = kernel_name(r["Kernel_Name"])
             grid = "x".join(r[f"Grid_Size_{a}"] for a in "XYZ")
             key = (name, grid, int(r["Workgroup_Size_X"]), int(r["LDS_Block_Size"]),
                    int(r["VGPR_Count"]) + int(r["Accum_VGPR_Count"]))
@@ -184,6 +224,9 @@ def main():
     if args.summarize:
         summarize_trace(args.summarize)
         return
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the M1 denoise path is a single-request, single-device path and "
               f"this build has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -200,6 +243,15 @@ def main():
     from mlc_vla.sample import make_prefix_mask_np, make_rope_np, make_time_embs
 
     torch.cuda.set_device(0)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.op_iters)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_mib": args.copy_mib, "iters": args.op_iters,
+                          "bytes_read_per_copy": src.numel() * 4, "bytes_written_per_copy": dst.numel() * 4}))
+        return
     dev = runtime.device()
     cfg = Pi0Config(dtype="float16", action_horizon=50)  # prefix_len 968, 18 layers
     ex, npar = compile_model(cfg, "rocm", cuda_graph=True)
@@ -241,6 +293,15 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / iters, (time.perf_counter() - w0) * 1e3 / iters
 
+    if args.only_op:
+        op = N.OPS[args.only_op]
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        N.call("mlcv_bench_op", vm._ctx, op, 0, args.op_iters, runtime._ptr(keys), runtime._ptr(values), st)
+        torch.cuda.synchronize()
+        b, f = op_bytes_flops(cfg, args.only_op)
+        print(json.dumps({"only_op": args.only_op, "launches": args.op_iters, "bytes_per_launch": int(b)}))
+        return
+
     # ---- headline: denoise_step_kv ---------------------------------------------
     step = lambda: vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)  # noqa: E731
     step_ms, step_wall_ms = timed(step, args.steps, args.warmup)
@@ -269,9 +330,10 @@ def main():
     dom = max(per_op, key=lambda k: per_op[k]["us_per_step"])
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath):  # calibrated PMC bytes per launch (see profiles/traffic_per_op_pmc.md)
         with open(tpath) as f:
-            traffic = json.load(f).get(dom)
+            rec = json.load(f).get(dom)
+        traffic = rec.get("traffic") if isinstance(rec, dict) else rec
 
     sbytes = step_bytes(cfg)
     step_us = step_ms * 1e3
