@@ -6,9 +6,11 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <mutex>
+#include <string>
 #include <vector>
 
 namespace mlcv {
@@ -35,8 +37,47 @@ struct Layer {
 
 struct OpDesc {
   int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0, seg_tiles = 0;
+  int tr = 64, splits = 0;  // weight rows per tile, K slices (0: planner's choice)
   bool q4 = false;
 };
+
+// Tiling of the step's GEMMs at M <= 64 (per-CU bytes through L1 are the first-order cost):
+// q/k/v and gate_up take the whole K per workgroup (no split-K exchange); o_proj and down
+// split K over 32-row tiles; everything else uses 64-row tiles and the planner's split.
+struct Tiling {
+  int tr, splits;
+};
+Tiling TILE_QKV = {16, 1}, TILE_O = {32, 4}, TILE_GU = {32, 1}, TILE_DOWN = {32, 8};
+constexpr int TR_AIN = 32, SPLIT_AIN = 1;
+
+// MLCV_TILING="qkv=TR:S,o=TR:S,gu=TR:S,down=TR:S" overrides the layer GEMM tilings for
+// tuning (read at context creation; TR in {16, 32, 64}, S = K slices, 0 = planner).
+void read_tiling_override() {
+  const char* e = std::getenv("MLCV_TILING");
+  if (!e) return;
+  std::string spec(e);
+  size_t pos = 0;
+  while (pos < spec.size()) {
+    size_t end = spec.find(',', pos);
+    if (end == std::string::npos) end = spec.size();
+    const std::string item = spec.substr(pos, end - pos);
+    const size_t eq = item.find('='), colon = item.find(':');
+    if (eq != std::string::npos && colon != std::string::npos && colon > eq) {
+      const std::string name = item.substr(0, eq);
+      const int tr = std::atoi(item.substr(eq + 1, colon - eq - 1).c_str());
+      const int sp = std::atoi(item.substr(colon + 1).c_str());
+      if (tr == 16 || tr == 32 || tr == 64) {
+        Tiling t{tr, sp};
+        if (name == "qkv") TILE_QKV = t;
+        else if (name == "o") TILE_O = t;
+        else if (name == "gu") TILE_GU = t;
+        else if (name == "down") TILE_DOWN = t;
+      }
+    }
+    pos = end + 1;
+  }
+}
+constexpr int RSS_COLS = 16;  // residual row statistics: one partial per 16 columns
 
 struct Graph {
   hipGraphExec_t exec = nullptr;
@@ -127,13 +168,14 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   op.seg_tiles = d.seg_tiles;
   for (int i = 0; i < d.nseg && i < 3; ++i) op.inl[i] = c.h_segs[d.seg_off + i];
   op.ntiles = d.ntiles;
-  const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64);
+  op.tr = d.tr;
+  const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64, d.splits);
   op.splitk = p.splitk;
   op.kper = p.kper;
   op.ws = c.skws;
   op.zero = c.zero;
   op.counters = c.counters;
-  op.rowss_ld = c.T;
+  op.rowss_ld = c.rss_tiles;
   op.rowss_tiles = c.rss_tiles;
   return op;
 }
@@ -384,12 +426,15 @@ int run_graph(Ctx& c, Graph& g, const std::vector<const void*>& key, const std::
   return 0;
 }
 
-int seg_ops(Ctx& c, OpDesc& d, const std::vector<SkSeg>& segs, int K, int epi, bool q4, int tile_rows) {
+int seg_ops(Ctx& c, OpDesc& d, const std::vector<SkSeg>& segs, int K, int epi, bool q4, int tr, int splits) {
+  const int tile_rows = epi == EPI_GEGLU ? tr / 2 : tr;  // output columns per tile
   d.seg_off = (int)c.h_segs.size();
   d.nseg = (int)segs.size();
   d.K = K;
   d.epi = epi;
   d.q4 = q4;
+  d.tr = tr;
+  d.splits = splits;
   int t = 0;
   d.seg_tiles = segs.empty() ? 0 : (segs[0].n + tile_rows - 1) / tile_rows;
   for (SkSeg s : segs) {
@@ -452,6 +497,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
                "depth / lengths / steps must be positive");
   MLCV_REQUIRE(cfg->num_steps <= 64, "num_steps must be <= 64");
 
+  static std::once_flag tiling_once;
+  std::call_once(tiling_once, read_tiling_override);
   auto* h = new (std::nothrow) mlcv_ctx();
   if (!h) {
     set_error("out of host memory");
@@ -504,9 +551,9 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.cos, T * hd / 2);
   ALLOC(c.sin, T * hd / 2);
   ALLOC(c.mask, c.P);
-  c.rss_tiles = (W1 + 63) / 64;
-  MLCV_REQUIRE(c.rss_tiles <= 64, "ae_width must be <= 4096");
-  ALLOC(c.rowss, (size_t)c.rss_tiles * T);
+  MLCV_REQUIRE(W1 % 64 == 0, "ae_width must be a multiple of 64");
+  c.rss_tiles = W1 / RSS_COLS;
+  ALLOC(c.rowss, (size_t)T * c.rss_tiles);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
   ALLOC(c.pxn, P * c.W0);
@@ -545,21 +592,22 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
   const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
   struct Shape {
-    int ntiles, K, mb;
+    int ntiles, K, mb, tr, splits;
   };
+  auto tiles = [](int n, int cols) { return (n + cols - 1) / cols; };
   std::vector<Shape> shapes = {
-      {(nq + 63) / 64 + 2 * ((nkv + 63) / 64), W1, mb_t},  // qkv
-      {(W1 + 63) / 64, nq, mb_t},                         // o
-      {c.F1 / 32, W1, mb_t},                              // gate_up
-      {(W1 + 63) / 64, c.F1, mb_t},                       // down
-      {(W1 + 63) / 64, W1, mb_s},                         // time mlp
-      {c.NM * ((3 * W1 + 63) / 64), W1, mb_s},            // modulation
-      {(W1 + 63) / 64, c.A, mb_t},                        // action_in
-      {(c.A + 63) / 64, W1, mb_t},                        // action_out
+      {tiles(nq, TILE_QKV.tr) + 2 * tiles(nkv, TILE_QKV.tr), W1, mb_t, TILE_QKV.tr, TILE_QKV.splits},  // qkv
+      {tiles(W1, TILE_O.tr), nq, mb_t, TILE_O.tr, TILE_O.splits},                                   // o
+      {tiles(c.F1, TILE_GU.tr / 2), W1, mb_t, TILE_GU.tr, TILE_GU.splits},                          // gate_up
+      {tiles(W1, TILE_DOWN.tr), c.F1, mb_t, TILE_DOWN.tr, TILE_DOWN.splits},                        // down
+      {tiles(W1, 64), W1, mb_s, 64, 0},                                          // time mlp
+      {c.NM * tiles(3 * W1, 64), W1, mb_s, 64, 1},                               // modulation
+      {tiles(W1, TR_AIN), c.A, mb_t, TR_AIN, SPLIT_AIN},                         // action_in
+      {tiles(c.A, 64), W1, mb_t, 64, 0},                                         // action_out
   };
   for (const Shape& s : shapes) {
-    const SkPlan p = sk_plan(s.ntiles, s.K, s.mb);
-    c.skws_floats = std::max(c.skws_floats, sk_ws_floats(s.ntiles, s.mb, p));
+    const SkPlan p = sk_plan(s.ntiles, s.K, s.mb, s.splits);
+    c.skws_floats = std::max(c.skws_floats, sk_ws_floats(s.ntiles, s.mb, p, s.tr));
     c.ncounters = std::max(c.ncounters, (size_t)s.ntiles * s.mb);
   }
   ALLOC(c.skws, c.skws_floats);
@@ -675,13 +723,13 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     OpDesc* ops = &c.layer_ops[4 * L];
     seg_ops(c, ops[0],
             {seg_of(ly.q[1], c.q, nq, nq), seg_of(ly.k[1], c.k, nkv, nkv), seg_of(ly.v[1], c.v, nkv, nkv)}, W1,
-            EPI_STORE, c.q4, 64);
-    seg_ops(c, ops[1], {seg_of(ly.o[1], c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, 64);
-    seg_ops(c, ops[2], {seg_of(ly.gu[1], c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, 32);
-    seg_ops(c, ops[3], {seg_of(ly.dn[1], c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, 64);
+            EPI_STORE, c.q4, TILE_QKV.tr, TILE_QKV.splits);
+    seg_ops(c, ops[1], {seg_of(ly.o[1], c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, TILE_O.tr, TILE_O.splits);
+    seg_ops(c, ops[2], {seg_of(ly.gu[1], c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, TILE_GU.tr, TILE_GU.splits);
+    seg_ops(c, ops[3], {seg_of(ly.dn[1], c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, TILE_DOWN.tr, TILE_DOWN.splits);
   }
-  seg_ops(c, c.op_tin, {seg_of(c.tin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64);
-  seg_ops(c, c.op_tout, {seg_of(c.tout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64);
+  seg_ops(c, c.op_tin, {seg_of(c.tin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
+  seg_ops(c, c.op_tout, {seg_of(c.tout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
   {
     std::vector<SkSeg> ms;
     const int ldo = c.NM * 3 * W1;
@@ -690,10 +738,10 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
       ms.push_back(seg_of(c.layers[L].mod_post, c.mod + (size_t)(2 * L + 1) * 3 * W1, 3 * W1, ldo));
     }
     ms.push_back(seg_of(c.final_mod, c.mod + (size_t)(2 * c.D) * 3 * W1, 3 * W1, ldo));
-    seg_ops(c, c.op_mod, ms, W1, EPI_STORE, c.q4, 64);
+    seg_ops(c, c.op_mod, ms, W1, EPI_STORE, c.q4, 64, 1);
   }
-  seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, 64);
-  seg_ops(c, c.op_aout, {seg_of(c.aout, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, 64);
+  seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, TR_AIN, SPLIT_AIN);
+  seg_ops(c, c.op_aout, {seg_of(c.aout, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, 64, 0);
 
   if (c.d_segs) {
     (void)hipFree(c.d_segs);
@@ -917,9 +965,9 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
   s.ldo = N;
   s.tile0 = 0;
   const int ntiles = (N + 63) / 64, mb = (M + 63) / 64;
-  const SkPlan p = sk_plan(ntiles, K, mb);
+  const SkPlan p = sk_plan(ntiles, K, mb, 0);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
-  MLCV_TRY(scratch_reserve(sk_ws_floats(ntiles, mb, p), (size_t)ntiles * mb));
+  MLCV_TRY(scratch_reserve(sk_ws_floats(ntiles, mb, p, 64), (size_t)ntiles * mb));
   MLCV_HIP(hipStreamSynchronize(st));
   MLCV_HIP(hipMemcpy(g_scratch.seg, &s, sizeof(SkSeg), hipMemcpyHostToDevice));
   SkOp op{};
@@ -932,6 +980,7 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
   op.nseg = 1;
   op.inl[0] = s;
   op.ntiles = ntiles;
+  op.tr = 64;
   op.splitk = p.splitk;
   op.kper = p.kper;
   op.ws = g_scratch.ws;

@@ -38,7 +38,6 @@ namespace {
 constexpr int KC = 128;           // k per chunk (4 MFMA k-steps of 32)
 constexpr int MB = 64;            // m rows per block (4 MFMA m tiles)
 constexpr int MAX_SPLIT = 8;
-constexpr int TILE_F = MB * 64;   // floats of one split-K partial tile
 
 // 8 nibbles of a word -> fp16 (q - 7) * s, ordered [n0,n4,n1,n5,n2,n6,n3,n7].
 __device__ __forceinline__ h8 dequant_word(uint32_t word, _Float16 s) {
@@ -99,37 +98,49 @@ __device__ __forceinline__ h8 wfrag(const WRaw<Q4>& f, int j) {
   else return dequant_word(f.words[j], f.s);
 }
 
-// acc[mt] = sum over the NS split partials of this lane's 4 columns, in split order
-template <int NS>
-__device__ __forceinline__ void sum_splits(const float* base, f4* acc) {
-  f4 part[NS][4];
+// acc[i] (this wave's owned m tiles) = sum over the NS split partials, in split order
+template <int NS, int NOWN>
+__device__ __forceinline__ void sum_splits(const float* base, size_t split_stride, const int* own_off, f4* acc) {
+  f4 part[NS][NOWN];
 #pragma unroll
   for (int q = 0; q < NS; ++q)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) part[q][mt] = *reinterpret_cast<const f4*>(base + (size_t)q * TILE_F + mt * 16 * 64);
+    for (int i = 0; i < NOWN; ++i) part[q][i] = *reinterpret_cast<const f4*>(base + q * split_stride + own_off[i]);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    f4 sum = part[0][mt];
+  for (int i = 0; i < NOWN; ++i) {
+    f4 sum = part[0][i];
 #pragma unroll
-    for (int q = 1; q < NS; ++q) sum += part[q][mt];
-    acc[mt] = sum;
+    for (int q = 1; q < NS; ++q) sum += part[q][i];
+    acc[i] = sum;
   }
 }
 
-template <bool Q4, bool NORM, int EPI, int NC, bool TABLE>
+// One output tile of TR weight rows (SLABS = TR/16 MFMA row slabs) over one K slice.
+// Wave w = (slab, kg): slab w % SLABS, k group w / SLABS takes chunks kg*CPW .. +CPW of
+// every round.  The k groups of a slab are summed through LDS in k-group order; after
+// that wave (slab, kg) owns m tiles kg, kg + KG, ... of its slab (split-K, epilogue).
+template <bool Q4, bool NORM, int EPI, int NC, bool TABLE, int TR>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
-  constexpr int XK = NC * KC;      // k per round
-  constexpr int XLD = XK + 8;      // LDS row stride of the X slice (halfs)
-  constexpr int TPR = XK / 8;      // threads per X row
-  constexpr int RPP = 256 / TPR;   // X rows per load pass
-  constexpr int NXL = MB / RPP;    // X loads per thread
+  constexpr int SLABS = TR / 16;
+  constexpr int KG = 4 / SLABS;      // waves per slab
+  constexpr int CPW = NC / KG;       // chunks per wave per round
+  constexpr int NOWN = 4 / KG;       // m tiles owned per wave after the k-group sum
+  static_assert(SLABS * KG == 4 && CPW * KG == NC && CPW >= 1, "tile / chunk configuration");
+  constexpr int XK = NC * KC;        // k per round
+  constexpr int XLD = XK + 8;        // LDS row stride of the X slice (halfs)
+  constexpr int TPR = XK / 8;        // threads per X row
+  constexpr int RPP = 256 / TPR;     // X rows per load pass
+  constexpr int NXL = MB / RPP;      // X loads per thread
+  constexpr int TILE_F = TR * 64;    // floats of one split-K partial tile
   __shared__ __attribute__((aligned(16))) _Float16 xs[MB * XLD];
-  __shared__ float denom[4][MB];   // 1 / sqrt(mean(x^2) + eps) per row, one copy per wave
-  __shared__ float red[4][MB];     // per-wave row sums of squares (rowss_out)
+  __shared__ float denom[4][MB];     // 1 / sqrt(mean(x^2) + eps) per row, one copy per wave
   __shared__ int is_last;
+  static_assert(KG == 1 || (size_t)KG * SLABS * 4 * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
+  f4* red = reinterpret_cast<f4*>(xs);  // [KG][SLABS][4 m tiles][64 lanes] after the last round
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
+  const int slab = w % SLABS, kg = w / SLABS;
   const int tile_id = blockIdx.x, s = blockIdx.y, mb = blockIdx.z;
   const int S = gridDim.y;
   const int m0 = mb * MB;
@@ -152,24 +163,25 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   const int K = op.K;
   const int kbeg = s * op.kper;
   const int kend = min(K, kbeg + op.kper);
-  const int row = (EPI == EPI_GEGLU) ? (r16 < 8 ? 0 : op.geglu_F) + 32 * lt + 8 * w + (r16 & 7)
-                                     : min(64 * lt + 16 * w + r16, seg.n - 1);
+  // GeGLU: a slab holds 8 gate + 8 up rows of 8 output columns (TR/2 outputs per tile)
+  const int row = (EPI == EPI_GEGLU) ? (r16 < 8 ? 0 : op.geglu_F) + (TR / 2) * lt + 8 * slab + (r16 & 7)
+                                     : min(TR * lt + 16 * slab + r16, seg.n - 1);
   // output columns n0..n0+3 of this lane (GeGLU: lanes g < 2 own the outputs)
-  const int n0 = (EPI == EPI_GEGLU) ? 32 * lt + 8 * w + 4 * (g & 1) : 64 * lt + 16 * w + 4 * g;
+  const int n0 = (EPI == EPI_GEGLU) ? (TR / 2) * lt + 8 * slab + 4 * (g & 1) : TR * lt + 16 * slab + 4 * g;
   const int ncl = max(0, min(n0, seg.n - 4));
   const bool nok = n0 < seg.n;
   const size_t ldo = (size_t)seg.ldo;
   const bool has_bias = seg.bias != nullptr;
 
-  // ---- epilogue operands first: they do not depend on the product ---------------
-  h4 xo[4], gq = (h4){0, 0, 0, 0}, bq = (h4){0, 0, 0, 0};
-  f4 x32o[4];
+  // ---- epilogue operands first (owned m tiles only): they do not depend on the product ----
+  h4 xo[NOWN], gq = (h4){0, 0, 0, 0}, bq = (h4){0, 0, 0, 0};
+  f4 x32o[NOWN];
   const _Float16* zero_h = reinterpret_cast<const _Float16*>(op.zero);
   if constexpr (EPI == EPI_GATED_RES) {
     const _Float16* xb = reinterpret_cast<const _Float16*>(seg.out);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      xo[mt] = *reinterpret_cast<const h4*>(xb + (size_t)min(m0 + 16 * mt + r16, mlast) * ldo + ncl);
+    for (int i = 0; i < NOWN; ++i)
+      xo[i] = *reinterpret_cast<const h4*>(xb + (size_t)min(m0 + 16 * (kg + i * KG) + r16, mlast) * ldo + ncl);
     gq = *reinterpret_cast<const h4*>(op.gate + ncl);
   }
   if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU || EPI == EPI_VOUT || EPI == EPI_EULER) {
@@ -177,17 +189,17 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   }
   if constexpr (EPI == EPI_EULER) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      x32o[mt] = *reinterpret_cast<const f4*>(op.x32 + (size_t)min(m0 + 16 * mt + r16, mlast) * ldo + ncl);
+    for (int i = 0; i < NOWN; ++i)
+      x32o[i] = *reinterpret_cast<const f4*>(op.x32 + (size_t)min(m0 + 16 * (kg + i * KG) + r16, mlast) * ldo + ncl);
   }
 
-  // adaRMS row statistics: the producer's per-tile partial sums of squares, one row per
-  // lane; every wave loads them and keeps its own copy of the row scales (no barrier)
-  float rss[16];
+  // adaRMS row statistics: the producer's partial sums of squares per 16-column group,
+  // stored [row][group]; one row per lane, every wave keeps its own copy of the row scales
+  f4 rss[16];
   if constexpr (NORM) {
-    const int m = min(m0 + lane, mlast);
+    const float* rr = op.rowss_in + (size_t)min(m0 + lane, mlast) * op.rowss_ld;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) rss[t] = op.rowss_in[(size_t)min(t, op.rowss_tiles - 1) * op.rowss_ld + m];
+    for (int q = 0; q < 16; ++q) rss[q] = *reinterpret_cast<const f4*>(rr + min(4 * q, op.rowss_tiles - 4));
   }
 
   f4 acc[4];
@@ -200,9 +212,9 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   auto round = [&](const int kr, const bool first) __attribute__((always_inline)) {
     // (1) the X slice [64 rows][XK]: thread -> 8 consecutive k of rows mr + RPP*i (rows
     //     past M repeat the last row; k past the slice is zeroed below)
-    const int kg = kr + kk;
-    const bool kok = kg < kend;
-    const int kgc = min(kg, K - 8);
+    const int kg8 = kr + kk;
+    const bool kok = kg8 < kend;
+    const int kgc = min(kg8, K - 8);
     h8 v[NXL];
 #pragma unroll
     for (int i = 0; i < NXL; ++i)
@@ -212,17 +224,19 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       sc = *reinterpret_cast<const h8*>(op.scale + kgc);
       sh = *reinterpret_cast<const h8*>(op.shift + kgc);
     }
-    // (2) then every weight chunk of this round
-    WRaw<Q4> wr[NC];
+    // (2) then this wave's weight chunks of the round
+    WRaw<Q4> wr[CPW];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) load_wraw<Q4>(wr[c], seg, row, kr + c * KC, g, K);
+    for (int c = 0; c < CPW; ++c) load_wraw<Q4>(wr[c], seg, row, kr + (kg * CPW + c) * KC, g, K);
     if constexpr (NORM) {
       if (first) {
         float ssum = 0.f;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) ssum += t < op.rowss_tiles ? rss[t] : 0.f;
-        const int m = min(m0 + lane, mlast);
-        for (int t = 16; t < op.rowss_tiles; ++t) ssum += op.rowss_in[(size_t)t * op.rowss_ld + m];  // K > 1024
+        for (int q = 0; q < 16; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ssum += 4 * q + e < op.rowss_tiles ? rss[q][e] : 0.f;
+        const float* rr = op.rowss_in + (size_t)min(m0 + lane, mlast) * op.rowss_ld;
+        for (int t = 64; t < op.rowss_tiles; ++t) ssum += rr[t];  // widths past 1024
         denom[w][lane] = 1.0f / sqrtf(ssum / (float)K + op.eps);  // read back by this wave only
       }
     }
@@ -251,16 +265,16 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       *reinterpret_cast<h8*>(&xs[m * XLD + kk]) = o;
     }
     __syncthreads();
-    // (4) MFMA over the round
+    // (4) MFMA over this wave's chunks of the round
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    for (int c = 0; c < CPW; ++c) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const h8 a = wfrag<Q4>(wr[c], j);
-        const int ko = Q4 ? 32 * g + 8 * j : 32 * j + 8 * g;
+        const int ko = (kg * CPW + c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          const h8 b = *reinterpret_cast<const h8*>(&xs[(mt * 16 + r16) * XLD + c * KC + ko]);
+          const h8 b = *reinterpret_cast<const h8*>(&xs[(mt * 16 + r16) * XLD + ko]);
           acc[mt] = mfma16x16x32(a, b, acc[mt]);
         }
       }
@@ -270,18 +284,41 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   round(kbeg, true);
   for (int kr = kbeg + XK; kr < kend; kr += XK) round(kr, false);
 
+  // ---- k groups of a slab summed in k-group order; wave keeps m tiles kg + i*KG ----------
+  f4 own[NOWN];
+  if constexpr (KG == 1) {
+#pragma unroll
+    for (int i = 0; i < NOWN; ++i) own[i] = acc[i];
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) red[((kg * SLABS + slab) * 4 + mt) * 64 + lane] = acc[mt];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NOWN; ++i) {
+      const int mt = kg + i * KG;
+      f4 sum = red[((0 * SLABS + slab) * 4 + mt) * 64 + lane];
+#pragma unroll
+      for (int q = 1; q < KG; ++q) sum += red[((q * SLABS + slab) * 4 + mt) * 64 + lane];
+      own[i] = sum;
+    }
+  }
+
   // ---- split-K: partials of every split, summed by the last workgroup in split order ----
+  // partial layout per tile: [slab][m tile][lane][4]
+  int own_off[NOWN];
+#pragma unroll
+  for (int i = 0; i < NOWN; ++i) own_off[i] = ((slab * 4 + kg + i * KG) * 64 + lane) * 4;
   if (S > 1) {
     const int cidx = tile_id * gridDim.z + mb;
-    float* wsp = op.ws + ((size_t)cidx * S + s) * TILE_F + (size_t)r16 * 64 + 16 * w + 4 * g;
+    float* wsp = op.ws + ((size_t)cidx * S + s) * TILE_F;
     if ((gridDim.x & 7) == 0) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f4*>(wsp + mt * 16 * 64) = acc[mt];
+      for (int i = 0; i < NOWN; ++i) *reinterpret_cast<f4*>(wsp + own_off[i]) = own[i];
     } else {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int i = 0; i < NOWN; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_coherent(wsp + mt * 16 * 64 + i, acc[mt][i]);
+        for (int e = 0; e < 4; ++e) store_coherent(wsp + own_off[i] + e, own[i][e]);
     }
     wait_all_memory();
     __syncthreads();
@@ -291,111 +328,102 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     // XCD-local: the partials are in this XCD's L2 and this CU's L1 has never held
     // these lines in this kernel, so plain loads see them; otherwise drop stale copies
     if ((gridDim.x & 7) != 0) acquire_agent();
-    const float* base = op.ws + (size_t)cidx * S * TILE_F + (size_t)r16 * 64 + 16 * w + 4 * g;
+    const float* base = op.ws + (size_t)cidx * S * TILE_F;
     switch (S) {  // every partial of the tile in one batch of loads, summed in split order
-      case 2: sum_splits<2>(base, acc); break;
-      case 3: sum_splits<3>(base, acc); break;
-      case 4: sum_splits<4>(base, acc); break;
-      case 5: sum_splits<5>(base, acc); break;
-      case 6: sum_splits<6>(base, acc); break;
-      case 7: sum_splits<7>(base, acc); break;
-      default: sum_splits<8>(base, acc); break;
+      case 2: sum_splits<2, NOWN>(base, TILE_F, own_off, own); break;
+      case 3: sum_splits<3, NOWN>(base, TILE_F, own_off, own); break;
+      case 4: sum_splits<4, NOWN>(base, TILE_F, own_off, own); break;
+      case 5: sum_splits<5, NOWN>(base, TILE_F, own_off, own); break;
+      case 6: sum_splits<6, NOWN>(base, TILE_F, own_off, own); break;
+      case 7: sum_splits<7, NOWN>(base, TILE_F, own_off, own); break;
+      default: sum_splits<8, NOWN>(base, TILE_F, own_off, own); break;
     }
     if (tid == 0) counter_reset(&op.counters[cidx]);
   }
 
-  // ---- epilogue in the D layout: row m0 + 16mt + r16, columns n0..n0+3 ------------
-  bool mok[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) mok[mt] = 16 * mt + r16 < mrows;
-
+  // ---- epilogue in the D layout: row m0 + 16mt + r16 (owned mt), columns n0..n0+3 --------
   if constexpr (EPI == EPI_GEGLU) {
     // lanes g < 2 hold 4 gate columns, lane ^ 32 the matching 4 up columns: the pair
     // swaps halves so that each lane finishes 2 columns (g < 2: the first two)
     const bool lo = g < 2;
     const int col = n0 + (lo ? 0 : 2);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const float r0 = __shfl_xor(lo ? acc[mt][2] : acc[mt][0], 32);
-      const float r1 = __shfl_xor(lo ? acc[mt][3] : acc[mt][1], 32);
-      const float ga = lo ? acc[mt][0] : r0, gb = lo ? acc[mt][1] : r1;
-      const float ua = lo ? r0 : acc[mt][2], ub = lo ? r1 : acc[mt][3];
+    for (int i = 0; i < NOWN; ++i) {
+      const int mt = kg + i * KG;
+      const float r0 = __shfl_xor(lo ? own[i][2] : own[i][0], 32);
+      const float r1 = __shfl_xor(lo ? own[i][3] : own[i][1], 32);
+      const float ga = lo ? own[i][0] : r0, gb = lo ? own[i][1] : r1;
+      const float ua = lo ? r0 : own[i][2], ub = lo ? r1 : own[i][3];
       h2 o;
       o[0] = hmul(f2h(gelu_tanh_hw(h2f(f2h(ga)))), f2h(ua));
       o[1] = hmul(f2h(gelu_tanh_hw(h2f(f2h(gb)))), f2h(ub));
-      if (mok[mt] && nok)
+      if (16 * mt + r16 < mrows && nok)
         *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(seg.out) + (size_t)(m0 + 16 * mt + r16) * ldo + col) = o;
     }
     return;
   }
 
-  float ss[4];  // row sums of squares of the stored x over this lane's 4 columns
-  if constexpr (EPI == EPI_GATED_RES) {
+  float ss[NOWN];  // row sums of squares of the stored x over this lane's 4 columns
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+  for (int i = 0; i < NOWN; ++i) {
+    const int mt = kg + i * KG;
+    const bool mok = 16 * mt + r16 < mrows;
+    const size_t mo = (size_t)(m0 + 16 * mt + r16) * ldo + n0;
+    float s2 = 0.f;
+    if constexpr (EPI == EPI_GATED_RES) {
       h4 o;
-      float s2 = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const _Float16 r = hadd(xo[mt][i], hmul(f2h(acc[mt][i]), gq[i]));
-        o[i] = r;
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 r = hadd(xo[i][e], hmul(f2h(own[i][e]), gq[e]));
+        o[e] = r;
         s2 += h2f(r) * h2f(r);
       }
-      if (mok[mt] && nok)
-        *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + (size_t)(m0 + 16 * mt + r16) * ldo + n0) = o;
-      ss[mt] = nok ? s2 : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+      if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = o;
+    } else {
       h4 y;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        _Float16 t = f2h(acc[mt][i]);
-        if (has_bias) t = hadd(t, bq[i]);
+      for (int e = 0; e < 4; ++e) {
+        _Float16 t = f2h(own[i][e]);
+        if (has_bias) t = hadd(t, bq[e]);
         if constexpr (EPI == EPI_STORE_SILU) t = f2h(silu_hw(h2f(t)));
-        y[i] = t;
+        y[e] = t;
       }
-      const size_t mo = (size_t)(m0 + 16 * mt + r16) * ldo + n0;
-      float s2 = 0.f;
       if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU) {
-        if (mok[mt] && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = y;
+        if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = y;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s2 += h2f(y[i]) * h2f(y[i]);
+        for (int e = 0; e < 4; ++e) s2 += h2f(y[e]) * h2f(y[e]);
       } else if constexpr (EPI == EPI_VOUT) {
-        if (mok[mt] && nok)
+        if (mok && nok)
           *reinterpret_cast<f4*>(reinterpret_cast<float*>(seg.out) + mo) = (f4){h2f(y[0]), h2f(y[1]), h2f(y[2]), h2f(y[3])};
       } else if constexpr (EPI == EPI_EULER) {
         f4 nx;
         h4 nh;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          nx[i] = euler_update(x32o[mt][i], op.dt, h2f(y[i]));
-          nh[i] = f2h(nx[i]);
+        for (int e = 0; e < 4; ++e) {
+          nx[e] = euler_update(x32o[i][e], op.dt, h2f(y[e]));
+          nh[e] = f2h(nx[e]);
         }
-        if (mok[mt] && nok) {
+        if (mok && nok) {
           *reinterpret_cast<f4*>(op.x32 + mo) = nx;
           *reinterpret_cast<h4*>(op.x16 + mo) = nh;
         }
       }
-      ss[mt] = nok ? s2 : 0.f;
     }
+    ss[i] = nok ? s2 : 0.f;
   }
   if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
     if (op.rowss_out) {
-      // over the wave's 16 columns (lanes g), then over the 4 waves in order
+      // this slab's 16 columns: the 4 lanes of a row hold 4 columns each
+      const int grp = (TR * lt + 16 * slab) / 16;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        ss[mt] += __shfl_xor(ss[mt], 16);
-        ss[mt] += __shfl_xor(ss[mt], 32);
+      for (int i = 0; i < NOWN; ++i) {
+        float v = ss[i];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        const int mt = kg + i * KG;
+        if (g == 0 && 16 * mt + r16 < mrows)
+          op.rowss_out[(size_t)(m0 + 16 * mt + r16) * op.rowss_ld + grp] = v;
       }
-      if (g == 0) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) red[w][16 * mt + r16] = ss[mt];
-      }
-      __syncthreads();
-      if (w == 0 && lane < mrows)
-        op.rowss_out[(size_t)lt * op.rowss_ld + m0 + lane] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
     }
   }
 }
@@ -451,14 +479,46 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ qw, const _Float1
   }
 }
 
-template <bool Q4, bool NORM, int EPI, bool TABLE = false>
+// instantiated (tile rows, prologue, epilogue) combinations -- the ones the engine uses:
+//   16: adaRMS + store (q/k/v);  32: adaRMS + GeGLU, gated residual, plain store (action_in);
+//   64: everything else
+template <bool NORM, int EPI, bool TABLE, int TR>
+constexpr bool sk_combo() {
+  if (TABLE) return TR == 64 && !NORM && EPI == EPI_STORE;
+  if (TR == 16) return NORM && EPI == EPI_STORE;
+  if (TR == 32) return (NORM && EPI == EPI_GEGLU) || (!NORM && (EPI == EPI_GATED_RES || EPI == EPI_STORE));
+  return TR == 64 && EPI != EPI_GATED_RES && EPI != EPI_GEGLU;
+}
+
+template <bool Q4, bool NORM, int EPI, bool TABLE, int TR>
 int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
-  switch (nc) {
-    case 1: skinny_kernel<Q4, NORM, EPI, 1, TABLE><<<grid, 256, 0, st>>>(op); break;
-    case 2: skinny_kernel<Q4, NORM, EPI, 2, TABLE><<<grid, 256, 0, st>>>(op); break;
-    default: skinny_kernel<Q4, NORM, EPI, 4, TABLE><<<grid, 256, 0, st>>>(op); break;
+  if constexpr (!sk_combo<NORM, EPI, TABLE, TR>()) {
+    MLCV_REQUIRE(false, "skinny GEMM: tile rows / prologue / epilogue combination not built");
+  } else {
+    constexpr int KG = 4 / (TR / 16);
+    if (nc < KG) nc = KG;
+    switch (nc) {
+      case 1:
+        if constexpr (KG <= 1) skinny_kernel<Q4, NORM, EPI, 1, TABLE, TR><<<grid, 256, 0, st>>>(op);
+        break;
+      case 2:
+        if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR><<<grid, 256, 0, st>>>(op);
+        break;
+      case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR><<<grid, 256, 0, st>>>(op); break;
+      default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR><<<grid, 256, 0, st>>>(op); break;
+    }
   }
   return 0;
+}
+
+template <bool Q4, bool NORM, int EPI, bool TABLE = false>
+int launch_tr(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
+  switch (op.tr) {
+    case 16: return launch_nc<Q4, NORM, EPI, TABLE, 16>(op, nc, grid, st);
+    case 32: return launch_nc<Q4, NORM, EPI, TABLE, 32>(op, nc, grid, st);
+    case 64: return launch_nc<Q4, NORM, EPI, TABLE, 64>(op, nc, grid, st);
+    default: MLCV_REQUIRE(false, "skinny GEMM tile rows must be 16, 32 or 64");
+  }
 }
 
 template <bool Q4>
@@ -466,21 +526,21 @@ int launch_q(const SkOp& op, bool norm, int nc, dim3 grid, hipStream_t st) {
   if (op.nseg > 3) {
     MLCV_REQUIRE(!norm && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs,
                  "more than 3 weight segments need equal sizes, a plain store and no prologue");
-    return launch_nc<Q4, false, EPI_STORE, true>(op, nc, grid, st);
+    return launch_tr<Q4, false, EPI_STORE, true>(op, nc, grid, st);
   }
   if (norm) {
     switch (op.epi) {
-      case EPI_STORE: return launch_nc<Q4, true, EPI_STORE>(op, nc, grid, st);
-      case EPI_GEGLU: return launch_nc<Q4, true, EPI_GEGLU>(op, nc, grid, st);
-      case EPI_VOUT: return launch_nc<Q4, true, EPI_VOUT>(op, nc, grid, st);
-      case EPI_EULER: return launch_nc<Q4, true, EPI_EULER>(op, nc, grid, st);
+      case EPI_STORE: return launch_tr<Q4, true, EPI_STORE>(op, nc, grid, st);
+      case EPI_GEGLU: return launch_tr<Q4, true, EPI_GEGLU>(op, nc, grid, st);
+      case EPI_VOUT: return launch_tr<Q4, true, EPI_VOUT>(op, nc, grid, st);
+      case EPI_EULER: return launch_tr<Q4, true, EPI_EULER>(op, nc, grid, st);
       default: break;
     }
   } else {
     switch (op.epi) {
-      case EPI_STORE: return launch_nc<Q4, false, EPI_STORE>(op, nc, grid, st);
-      case EPI_STORE_SILU: return launch_nc<Q4, false, EPI_STORE_SILU>(op, nc, grid, st);
-      case EPI_GATED_RES: return launch_nc<Q4, false, EPI_GATED_RES>(op, nc, grid, st);
+      case EPI_STORE: return launch_tr<Q4, false, EPI_STORE>(op, nc, grid, st);
+      case EPI_STORE_SILU: return launch_tr<Q4, false, EPI_STORE_SILU>(op, nc, grid, st);
+      case EPI_GATED_RES: return launch_tr<Q4, false, EPI_GATED_RES>(op, nc, grid, st);
       default: break;
     }
   }
@@ -489,14 +549,19 @@ int launch_q(const SkOp& op, bool norm, int nc, dim3 grid, hipStream_t st) {
 
 }  // namespace
 
-SkPlan sk_plan(int ntiles, int K, int mblocks) {
-  // one wave of workgroups (<= 256, one per CU); each split keeps >= 128 of K; at most 8 splits
+SkPlan sk_plan(int ntiles, int K, int mblocks, int splits) {
+  // splits > 0: that many K slices (at most one per 128-k chunk); otherwise one wave of
+  // workgroups (<= 256, one per CU) with at most 8 splits
   const int chunks = (K + KC - 1) / KC;
-  const int blocks = ntiles * mblocks;
-  int want = (256 + blocks - 1) / blocks;
-  if (want < 1) want = 1;
+  int want = splits;
+  if (want <= 0) {
+    const int blocks = ntiles * mblocks;
+    want = (256 + blocks - 1) / blocks;
+    if (want > MAX_SPLIT) want = MAX_SPLIT;
+  }
   if (want > MAX_SPLIT) want = MAX_SPLIT;
   if (want > chunks) want = chunks;
+  if (want < 1) want = 1;
   const int cps = (chunks + want - 1) / want;
   SkPlan p;
   p.kper = cps * KC;
@@ -504,8 +569,8 @@ SkPlan sk_plan(int ntiles, int K, int mblocks) {
   return p;
 }
 
-size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p) {
-  return p.splitk > 1 ? (size_t)ntiles * mblocks * p.splitk * TILE_F : 0;
+size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p, int tr) {
+  return p.splitk > 1 ? (size_t)ntiles * mblocks * p.splitk * tr * 64 : 0;
 }
 
 int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
@@ -515,8 +580,10 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   MLCV_REQUIRE(op.kper % KC == 0 && (long)op.kper * op.splitk >= op.K, "skinny GEMM split plan");
   MLCV_REQUIRE(op.zero != nullptr, "skinny GEMM needs the zero page");
   MLCV_REQUIRE(op.splitk == 1 || (op.ws && op.counters), "skinny GEMM split-K workspace missing");
-  MLCV_REQUIRE(op.scale == nullptr || (op.rowss_in && op.rowss_tiles >= 1),
-               "adaRMS prologue needs the producer's row statistics");
+  MLCV_REQUIRE(op.scale == nullptr || (op.rowss_in && op.rowss_tiles >= 4 && op.rowss_tiles % 4 == 0 &&
+                                       op.rowss_ld % 4 == 0),
+               "adaRMS prologue needs the producer's row statistics (groups of 16 columns, multiple of 4)");
+  MLCV_REQUIRE(op.rowss_out == nullptr || op.rowss_ld > 0, "row statistics stride");
   MLCV_REQUIRE(op.ldx % 8 == 0, "skinny GEMM needs 16-byte aligned X rows");
   MLCV_REQUIRE(op.nseg >= 1, "skinny GEMM needs a weight segment");
   for (int i = 0; i < op.nseg && i < 3; ++i) {
@@ -526,7 +593,8 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   dim3 grid(op.ntiles, op.splitk, mblocks);
   const bool norm = op.scale != nullptr;
   const int cps = op.kper / KC;
-  const int nc = cps >= 3 ? 4 : cps;
+  int nc = cps >= 5 ? 8 : cps >= 3 ? 4 : cps;
+  if (nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS) for big grids
   if (q4) MLCV_TRY(launch_q<true>(op, norm, nc, grid, st));
   else MLCV_TRY(launch_q<false>(op, norm, nc, grid, st));
   MLCV_HIP(hipGetLastError());

@@ -38,9 +38,9 @@ struct SkOp {
   const _Float16* scale; // [K] or null (no prologue)
   const _Float16* shift; // [K]
   float eps;
-  // row sums of squares of the residual stream, one partial per 64-column tile:
+  // row sums of squares of the residual stream, one partial per 16-column group:
   // read by the prologue (rowss_in, rowss_tiles partials) and written by epilogues
-  // that produce x (rowss_out); element [tile * rowss_ld + m]
+  // that produce x (rowss_out); element [m * rowss_ld + group]
   const float* rowss_in;
   float* rowss_out;
   int rowss_ld, rowss_tiles;
@@ -51,6 +51,7 @@ struct SkOp {
   const SkSeg* segs;     // device table when nseg > 3
   int nseg, ntiles;
   int seg_tiles;         // > 0: every segment has this many tiles (direct table index)
+  int tr;                // weight rows per tile: 16, 32 or 64 (GeGLU: half gate, half up)
   int splitk, kper;
   float* ws;             // split-K partials
   const float* zero;     // >= 64*64 zero floats, never written (absent bias)
@@ -63,8 +64,9 @@ struct SkOp {
 struct SkPlan {
   int splitk, kper;
 };
-SkPlan sk_plan(int ntiles, int K, int mblocks);
-size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p);
+// splits > 0: that many K slices; 0: enough to fill one wave of workgroups (<= 8)
+SkPlan sk_plan(int ntiles, int K, int mblocks, int splits);
+size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p, int tr);
 int sk_launch(const SkOp& op, bool q4, hipStream_t st);
 
 // q4f16_1 helpers
