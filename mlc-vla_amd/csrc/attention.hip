@@ -434,13 +434,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   if (!row_ok) return;
   if (a.nsplit == 1) {
     const float inv = 1.0f / l_run;
-    _Float16* orow = a.out + (size_t)t * a.out_ld + (size_t)h * HD;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       h4 o4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * inv);
-      *reinterpret_cast<h4*>(orow + 16 * dt + 4 * g) = o4;
+      const int col = h * HD + 16 * dt + 4 * g;
+      *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
     }
   } else {
     const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
@@ -484,7 +484,6 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   float wv[MAXS];
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) wv[s] = __shfl(wgt, s);
-  _Float16* orow = a.out + (size_t)t * a.out_ld + (size_t)h * hd;
   for (int d = lane * 4; d < hd; d += 256) {
     if (d != d0) {  // head dims past 256
 #pragma unroll
@@ -497,7 +496,8 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
     h4 o4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o4[i] = f2h(acc[i]);
-    *reinterpret_cast<h4*>(orow + d) = o4;
+    const int col = h * hd + d;
+    *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
   }
 }
 
@@ -580,6 +580,7 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE((long)nsp * a.kps >= (long)a.Sp && (a.Sp > 0 || nsp == 0), "attention splits do not cover the keys");
   MLCV_REQUIRE(a.Ts == 0 || (a.ks && a.vs), "suffix keys missing");
   MLCV_REQUIRE(a.nsplit == 1 || (a.part_o && a.part_ml), "attention workspace missing");
+  MLCV_REQUIRE(!a.out_frag || (a.Tq <= 64 && (a.H * a.hd) % 32 == 0), "fragment-major output needs Tq <= 64");
   MLCV_REQUIRE(a.nsplit <= 32, "at most 32 key splits");
   MLCV_REQUIRE(a.cos == nullptr || a.sin != nullptr, "rope needs cos and sin");
   MLCV_REQUIRE(a.Ts == 0 || a.cos != nullptr || a.ks_roped, "raw suffix keys need the rope tables");

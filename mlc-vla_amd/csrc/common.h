@@ -44,6 +44,14 @@ const char* get_error();
   } while (0)
 
 // ---- device numerics helpers ----------------------------------------------
+// Fragment-major activation layout for the skinny GEMMs (rows m < 64, K % 32 == 0,
+// 64 x K halfs): the B operand of mfma16x16x32 f16 for k step ks and m tile mt is one
+// contiguous 1 KB block, lane 16 g + r holding X[16 mt + r][32 ks + 8 g .. +7].  A wave
+// then loads each fragment with one fully coalesced instruction.
+__host__ __device__ __forceinline__ size_t xf_index(int m, int k) {
+  return ((size_t)((k >> 5) * 4 + (m >> 4)) * 64 + ((((k >> 3) & 3) << 4) | (m & 15))) * 8 + (k & 7);
+}
+
 // Load through a global-address-space pointer: a pointer the compiler cannot trace to
 // global memory becomes a flat load, which forces a full vmcnt(0) wait at its first use.
 template <class T>

@@ -39,19 +39,23 @@ struct OpDesc {
   int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0, seg_tiles = 0;
   int tr = 64, splits = 0;  // weight rows per tile, K slices (0: planner's choice)
   bool q4 = false;
+  bool frag = false;  // fragment-major X and weights (16-row tiles)
 };
 
-// Tiling of the step's GEMMs at M <= 64 (per-CU bytes through L1 are the first-order cost):
-// q/k/v and gate_up take the whole K per workgroup (no split-K exchange); o_proj and down
-// split K over 32-row tiles; everything else uses 64-row tiles and the planner's split.
+// Tiling of the step's layer GEMMs.  With fragment-major operands (M < 64): 16-row tiles
+// whose waves load their operand fragments straight into registers; q/k/v and gate_up
+// take the whole K per workgroup (no split-K exchange), o_proj and down split K.
+// Otherwise (M >= 64) the row-major kernels stage X through LDS with 16/32-row tiles.
+// Everything else uses 64-row tiles and the planner's split.
 struct Tiling {
   int tr, splits;
 };
-Tiling TILE_QKV = {16, 1}, TILE_O = {32, 4}, TILE_GU = {32, 1}, TILE_DOWN = {32, 8};
+Tiling TILE_QKV = {16, 1}, TILE_O = {16, 4}, TILE_GU = {16, 1}, TILE_DOWN = {16, 8};
+constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
 
-// MLCV_TILING="qkv=TR:S,o=TR:S,gu=TR:S,down=TR:S" overrides the layer GEMM tilings for
-// tuning (read at context creation; TR in {16, 32, 64}, S = K slices, 0 = planner).
+// MLCV_TILING="qkv=16:S,o=16:S,gu=16:S,down=16:S" overrides the K slices of the
+// fragment-major layer GEMMs for tuning (read at context creation; 0 = planner).
 void read_tiling_override() {
   const char* e = std::getenv("MLCV_TILING");
   if (!e) return;
@@ -66,7 +70,7 @@ void read_tiling_override() {
       const std::string name = item.substr(0, eq);
       const int tr = std::atoi(item.substr(eq + 1, colon - eq - 1).c_str());
       const int sp = std::atoi(item.substr(colon + 1).c_str());
-      if (tr == 16 || tr == 32 || tr == 64) {
+      if (tr == 16) {
         Tiling t{tr, sp};
         if (name == "qkv") TILE_QKV = t;
         else if (name == "o") TILE_O = t;
@@ -112,6 +116,14 @@ struct Ctx {
 
   // suffix path
   _Float16 *x16, *q, *k, *v, *attn, *h, *cond, *tmp, *mod, *te, *xin16;
+  // pre-scaled adaRMS input [T + 1][W1]: fp16(x * (1 + scale)) of the next norm, its
+  // shift in row T (written by the producer of x; used when T < 64)
+  _Float16* xu = nullptr;
+  bool prescaled = false;
+  // fragment-major operands for the layer GEMMs (M < 64, widths % 128 == 0): xu, attn
+  // and h are [64][K] in the xf_index layout; the action expert's layer and head weights
+  // get pre-shuffled copies at bind time
+  bool frag = false;
   float *x32, *x0, *vout, *cos, *sin, *mask, *rowss;
   int rss_tiles = 1;
   // prefill path
@@ -177,6 +189,7 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   op.counters = c.counters;
   op.rowss_ld = c.rss_tiles;
   op.rowss_tiles = c.rss_tiles;
+  op.frag = d.frag;
   return op;
 }
 
@@ -190,15 +203,39 @@ int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st) {
   return 0;
 }
 
+Tiling tile_qkv(const Ctx& c) { return c.frag ? TILE_QKV : ROWMAJOR_QKV; }
+Tiling tile_o(const Ctx& c) { return c.frag ? TILE_O : ROWMAJOR_O; }
+Tiling tile_gu(const Ctx& c) { return c.frag ? TILE_GU : ROWMAJOR_GU; }
+Tiling tile_down(const Ctx& c) { return c.frag ? TILE_DOWN : ROWMAJOR_DOWN; }
+Tiling tile_head(const Ctx& c) { return c.frag ? Tiling{16, 2} : Tiling{64, 0}; }
+
 // ---- the ops of one decoder layer of the suffix path (modulations in modp) ------
 const _Float16* mod_of(const Ctx& c, const _Float16* modp, int idx) { return modp + (size_t)idx * 3 * c.W1; }
 
+// adaRMS consumer: pre-scaled X (T < 64) or the per-element prologue; m = [scale|shift|gate]
+void set_norm(const Ctx& c, SkOp& op, const _Float16* m) {
+  op.rowss_in = c.rowss;
+  if (c.prescaled) {
+    op.prescaled = true;
+  } else {
+    op.scale = m;
+    op.shift = m + c.W1;
+  }
+}
+
+// producer of x: also write the next adaRMS's pre-scaled input
+void set_next_norm(const Ctx& c, SkOp& op, const _Float16* m) {
+  if (!c.prescaled) return;
+  op.xu_out = c.xu;
+  op.xu_scale = m;
+  op.xu_shift = m + c.W1;
+  op.frag_out = c.frag;
+}
+
 int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRMS (input) + q/k/v
   const _Float16* m_in = mod_of(c, modp, 2 * L);
-  SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.x16, c.W1, c.T);
-  op.scale = m_in;
-  op.shift = m_in + c.W1;
-  op.rowss_in = c.rowss;
+  SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.prescaled ? c.xu : c.x16, c.W1, c.T);
+  set_norm(c, op, m_in);
   return run_op(c, c.layer_ops[4 * L + 0], op, st);
 }
 
@@ -226,6 +263,7 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   a.ks_roped = 0;
   a.out = c.attn;
   a.out_ld = c.H * c.HD;
+  a.out_frag = c.frag;
   a.nsplit = c.st_nsplit;
   a.kps = c.st_kps;
   a.rows = c.T * (c.H / c.KV);
@@ -239,16 +277,16 @@ int enqueue_oproj(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // o_p
   SkOp op = make_op(c, c.layer_ops[4 * L + 1], c.attn, c.H * c.HD, c.T);
   op.gate = mod_of(c, modp, 2 * L) + 2 * c.W1;
   op.rowss_out = c.rowss;
+  set_next_norm(c, op, mod_of(c, modp, 2 * L + 1));
   return run_op(c, c.layer_ops[4 * L + 1], op, st);
 }
 
 int enqueue_gateup(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRMS (post) + gate_up + GeGLU
   const _Float16* m_post = mod_of(c, modp, 2 * L + 1);
-  SkOp op = make_op(c, c.layer_ops[4 * L + 2], c.x16, c.W1, c.T);
-  op.scale = m_post;
-  op.shift = m_post + c.W1;
-  op.rowss_in = c.rowss;
+  SkOp op = make_op(c, c.layer_ops[4 * L + 2], c.prescaled ? c.xu : c.x16, c.W1, c.T);
+  set_norm(c, op, m_post);
   op.geglu_F = c.F1;
+  op.frag_out = c.frag;
   return run_op(c, c.layer_ops[4 * L + 2], op, st);
 }
 
@@ -256,15 +294,14 @@ int enqueue_down(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // down
   SkOp op = make_op(c, c.layer_ops[4 * L + 3], c.h, c.F1, c.T);
   op.gate = mod_of(c, modp, 2 * L + 1) + 2 * c.W1;
   op.rowss_out = c.rowss;
+  set_next_norm(c, op, mod_of(c, modp, L + 1 < c.D ? 2 * (L + 1) : 2 * c.D));
   return run_op(c, c.layer_ops[4 * L + 3], op, st);
 }
 
 int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  // final adaRMS + action_out
   const _Float16* m_fin = mod_of(c, modp, 2 * c.D);
-  SkOp op = make_op(c, c.op_aout, c.x16, c.W1, c.T);
-  op.scale = m_fin;
-  op.shift = m_fin + c.W1;
-  op.rowss_in = c.rowss;
+  SkOp op = make_op(c, c.op_aout, c.prescaled ? c.xu : c.x16, c.W1, c.T);
+  set_norm(c, op, m_fin);
   if (euler) {
     op.epi = EPI_EULER;
     op.dt = (float)(-1.0 / c.NS);
@@ -279,6 +316,7 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
                  hipStream_t st) {
   SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
   ain.rowss_out = c.rowss;
+  set_next_norm(c, ain, mod_of(c, modp, 0));
   MLCV_TRY(run_op(c, c.op_ain, ain, st));
   for (int L = 0; L < c.D; ++L) {
     MLCV_TRY(enqueue_qkv(c, L, modp, st));
@@ -538,8 +576,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.q, T * nq);
   ALLOC(c.k, T * nkv);
   ALLOC(c.v, T * nkv);
-  ALLOC(c.attn, T * nq);
-  ALLOC(c.h, (size_t)T * c.F1);
+  ALLOC(c.attn, (size_t)std::max(T, 64) * nq);
+  ALLOC(c.h, (size_t)std::max(T, 64) * c.F1);
   ALLOC(c.cond, c.NS * W1);
   ALLOC(c.tmp, c.NS * W1);
   ALLOC(c.mod, (size_t)c.NS * c.NM * 3 * W1);
@@ -554,6 +592,9 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   MLCV_REQUIRE(W1 % 64 == 0, "ae_width must be a multiple of 64");
   c.rss_tiles = W1 / RSS_COLS;
   ALLOC(c.rowss, (size_t)T * c.rss_tiles);
+  c.frag = T < 64 && W1 % 128 == 0 && nq % 128 == 0 && c.F1 % 128 == 0 && nkv % 16 == 0 && c.A % 16 == 0;
+  c.prescaled = c.frag;
+  ALLOC(c.xu, (size_t)64 * W1);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
   ALLOC(c.pxn, P * c.W0);
@@ -596,14 +637,14 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   };
   auto tiles = [](int n, int cols) { return (n + cols - 1) / cols; };
   std::vector<Shape> shapes = {
-      {tiles(nq, TILE_QKV.tr) + 2 * tiles(nkv, TILE_QKV.tr), W1, mb_t, TILE_QKV.tr, TILE_QKV.splits},  // qkv
-      {tiles(W1, TILE_O.tr), nq, mb_t, TILE_O.tr, TILE_O.splits},                                   // o
-      {tiles(c.F1, TILE_GU.tr / 2), W1, mb_t, TILE_GU.tr, TILE_GU.splits},                          // gate_up
-      {tiles(W1, TILE_DOWN.tr), c.F1, mb_t, TILE_DOWN.tr, TILE_DOWN.splits},                        // down
+      {tiles(nq, tile_qkv(c).tr) + 2 * tiles(nkv, tile_qkv(c).tr), W1, mb_t, tile_qkv(c).tr, tile_qkv(c).splits},
+      {tiles(W1, tile_o(c).tr), nq, mb_t, tile_o(c).tr, tile_o(c).splits},
+      {tiles(c.F1, tile_gu(c).tr / 2), W1, mb_t, tile_gu(c).tr, tile_gu(c).splits},
+      {tiles(W1, tile_down(c).tr), c.F1, mb_t, tile_down(c).tr, tile_down(c).splits},
       {tiles(W1, 64), W1, mb_s, 64, 0},                                          // time mlp
       {c.NM * tiles(3 * W1, 64), W1, mb_s, 64, 1},                               // modulation
       {tiles(W1, TR_AIN), c.A, mb_t, TR_AIN, SPLIT_AIN},                         // action_in
-      {tiles(c.A, 64), W1, mb_t, 64, 0},                                         // action_out
+      {tiles(c.A, tile_head(c).tr), W1, mb_t, tile_head(c).tr, tile_head(c).splits},  // action_out
   };
   for (const Shape& s : shapes) {
     const SkPlan p = sk_plan(s.ntiles, s.K, s.mb, s.splits);
@@ -615,6 +656,9 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.zero, 64 * 64);
 #undef ALLOC
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(c.xu, 0, (size_t)64 * W1 * 2) != hipSuccess ||
+      hipMemset(c.attn, 0, (size_t)std::max(T, 64) * nq * 2) != hipSuccess ||
+      hipMemset(c.h, 0, (size_t)std::max(T, 64) * c.F1 * 2) != hipSuccess ||
       hipMemset(c.zero, 0, 64 * 64 * sizeof(float)) != hipSuccess ||
       hipStreamCreateWithFlags(&c.cap, hipStreamNonBlocking) != hipSuccess) {
     set_error("context setup failed");
@@ -714,6 +758,26 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     }
   }
 
+  // fragment-major copies of the action expert's layer and head weights
+  auto frag_copy = [&](const Lin& l, int geglu_F) -> Lin {
+    if (!c.frag) return l;
+    Lin f = l;
+    if (c.q4) {
+      uint32_t* qwf = nullptr;
+      _Float16* qsf = nullptr;
+      if (dalloc(&qwf, (size_t)l.N * l.K / 8, c.bind_owned) || dalloc(&qsf, (size_t)l.N * l.K / 32, c.bind_owned) ||
+          wf_shuffle_q4_launch(l.qw, l.qs, qwf, qsf, l.N, l.K, geglu_F, st))
+        f.N = -1;
+      f.qw = qwf;
+      f.qs = qsf;
+    } else {
+      _Float16* wf = nullptr;
+      if (dalloc(&wf, (size_t)l.N * l.K, c.bind_owned) || wf_shuffle_launch(l.w, wf, l.N, l.K, geglu_F, st)) f.N = -1;
+      f.w = wf;
+    }
+    return f;
+  };
+
   // skinny op tables
   c.h_segs.clear();
   c.layer_ops.assign(4 * c.D, OpDesc{});
@@ -721,12 +785,15 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
   for (int L = 0; L < c.D; ++L) {
     Layer& ly = c.layers[L];
     OpDesc* ops = &c.layer_ops[4 * L];
-    seg_ops(c, ops[0],
-            {seg_of(ly.q[1], c.q, nq, nq), seg_of(ly.k[1], c.k, nkv, nkv), seg_of(ly.v[1], c.v, nkv, nkv)}, W1,
-            EPI_STORE, c.q4, TILE_QKV.tr, TILE_QKV.splits);
-    seg_ops(c, ops[1], {seg_of(ly.o[1], c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, TILE_O.tr, TILE_O.splits);
-    seg_ops(c, ops[2], {seg_of(ly.gu[1], c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, TILE_GU.tr, TILE_GU.splits);
-    seg_ops(c, ops[3], {seg_of(ly.dn[1], c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, TILE_DOWN.tr, TILE_DOWN.splits);
+    const Lin fq = frag_copy(ly.q[1], 0), fk = frag_copy(ly.k[1], 0), fv = frag_copy(ly.v[1], 0);
+    const Lin fo = frag_copy(ly.o[1], 0), fgu = frag_copy(ly.gu[1], c.F1), fdn = frag_copy(ly.dn[1], 0);
+    for (const Lin* l : {&fq, &fk, &fv, &fo, &fgu, &fdn}) MLCV_REQUIRE(l->N >= 0, get_error());
+    seg_ops(c, ops[0], {seg_of(fq, c.q, nq, nq), seg_of(fk, c.k, nkv, nkv), seg_of(fv, c.v, nkv, nkv)}, W1,
+            EPI_STORE, c.q4, tile_qkv(c).tr, tile_qkv(c).splits);
+    seg_ops(c, ops[1], {seg_of(fo, c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, tile_o(c).tr, tile_o(c).splits);
+    seg_ops(c, ops[2], {seg_of(fgu, c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, tile_gu(c).tr, tile_gu(c).splits);
+    seg_ops(c, ops[3], {seg_of(fdn, c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, tile_down(c).tr, tile_down(c).splits);
+    for (int i = 0; i < 4; ++i) ops[i].frag = c.frag;
   }
   seg_ops(c, c.op_tin, {seg_of(c.tin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
   seg_ops(c, c.op_tout, {seg_of(c.tout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
@@ -741,7 +808,12 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     seg_ops(c, c.op_mod, ms, W1, EPI_STORE, c.q4, 64, 1);
   }
   seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, TR_AIN, SPLIT_AIN);
-  seg_ops(c, c.op_aout, {seg_of(c.aout, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, 64, 0);
+  {
+    const Lin fa = frag_copy(c.aout, 0);
+    MLCV_REQUIRE(fa.N >= 0, get_error());
+    seg_ops(c, c.op_aout, {seg_of(fa, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, tile_head(c).tr, tile_head(c).splits);
+    c.op_aout.frag = c.frag;
+  }
 
   if (c.d_segs) {
     (void)hipFree(c.d_segs);

@@ -55,6 +55,14 @@ __device__ __forceinline__ h8 dequant_word(uint32_t word, _Float16 s) {
   return r;
 }
 
+// pre-scaled adaRMS input: fp16(x * (1 + scale)) for 4 columns
+__device__ __forceinline__ void store_xu(_Float16* p, h4 x, h4 scale) {
+  h4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = f2h(h2f(x[e]) * (1.0f + h2f(scale[e])));
+  *reinterpret_cast<h4*>(p) = o;
+}
+
 __device__ __forceinline__ h8 perm8(h8 v) {
   h8 r;
   r[0] = v[0]; r[1] = v[4]; r[2] = v[1]; r[3] = v[5];
@@ -119,7 +127,10 @@ __device__ __forceinline__ void sum_splits(const float* base, size_t split_strid
 // Wave w = (slab, kg): slab w % SLABS, k group w / SLABS takes chunks kg*CPW .. +CPW of
 // every round.  The k groups of a slab are summed through LDS in k-group order; after
 // that wave (slab, kg) owns m tiles kg, kg + KG, ... of its slab (split-K, epilogue).
-template <bool Q4, bool NORM, int EPI, int NC, bool TABLE, int TR>
+// NORM: 0 none; 1 adaRMS applied to X per element (row scales from the row statistics);
+// 2 pre-scaled X (the producer wrote fp16(x * (1 + scale)) and the shift as row M), the
+// row scale and shift product applied in the epilogue.
+template <bool Q4, int NORM, int EPI, int NC, bool TABLE, int TR>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   constexpr int SLABS = TR / 16;
   constexpr int KG = 4 / SLABS;      // waves per slab
@@ -132,8 +143,15 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   constexpr int RPP = 256 / TPR;     // X rows per load pass
   constexpr int NXL = MB / RPP;      // X loads per thread
   constexpr int TILE_F = TR * 64;    // floats of one split-K partial tile
-  __shared__ __attribute__((aligned(16))) _Float16 xs[MB * XLD];
-  __shared__ float denom[4][MB];     // 1 / sqrt(mean(x^2) + eps) per row, one copy per wave
+  // 16-row tiles without the per-element prologue: every wave owns its own k range, so
+  // its MFMA B fragments are loaded straight from X into registers (no LDS staging, no
+  // barrier between loads and MFMAs: each MFMA waits only for its own operands)
+  constexpr bool DIRECT = TR == 16 && NORM != 1;
+  constexpr int XS_HALFS = DIRECT ? KG * SLABS * 4 * 64 * 8 : MB * XLD;
+  __shared__ __attribute__((aligned(16))) _Float16 xs[XS_HALFS];
+  __shared__ float denom[4][MB];     // NORM 1: 1 / sqrt(mean(x^2) + eps) per row, per wave;
+                                     // NORM 2: each wave's partial sum of squares per row
+  __shared__ f4 shiftacc[SLABS * 4]; // NORM 2: the shift row's product, per slab and lane group
   __shared__ int is_last;
   static_assert(KG == 1 || (size_t)KG * SLABS * 4 * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
   f4* red = reinterpret_cast<f4*>(xs);  // [KG][SLABS][4 m tiles][64 lanes] after the last round
@@ -146,6 +164,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   const int m0 = mb * MB;
   const int mlast = op.M - 1;
   const int mrows = min(MB, op.M - m0);
+  const int xlast = NORM == 2 ? op.M : mlast;  // pre-scaled X carries the shift as row M
 
   // the segment: up to 3 from the kernel arguments, picked by selects (no branch on an
   // argument value, so every argument load issues at once), or from a device table of
@@ -192,14 +211,29 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int i = 0; i < NOWN; ++i)
       x32o[i] = *reinterpret_cast<const f4*>(op.x32 + (size_t)min(m0 + 16 * (kg + i * KG) + r16, mlast) * ldo + ncl);
   }
+  // next adaRMS operands for the pre-scaled copy of x (STORE / GATED_RES producers)
+  h4 xus = (h4){0, 0, 0, 0}, xush = xus;
+  if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
+    const bool has_xu = op.xu_out != nullptr;
+    xus = load_global(reinterpret_cast<const h4*>(has_xu ? op.xu_scale + ncl : zero_h));
+    xush = load_global(reinterpret_cast<const h4*>(has_xu ? op.xu_shift + ncl : zero_h));
+  }
 
   // adaRMS row statistics: the producer's partial sums of squares per 16-column group,
   // stored [row][group]; one row per lane, every wave keeps its own copy of the row scales
   f4 rss[16];
-  if constexpr (NORM) {
+  if constexpr (NORM == 1) {
     const float* rr = op.rowss_in + (size_t)min(m0 + lane, mlast) * op.rowss_ld;
 #pragma unroll
     for (int q = 0; q < 16; ++q) rss[q] = *reinterpret_cast<const f4*>(rr + min(4 * q, op.rowss_tiles - 4));
+  }
+  // NORM 2: wave w sums groups 4(w + 4j) .. +3 of row `lane` once the product is done (the
+  // loads stay in flight meanwhile); the epilogue adds the 4 waves
+  f4 part[4];
+  if constexpr (NORM == 2) {
+    const float* rr = op.rowss_in + (size_t)min(m0 + lane, mlast) * op.rowss_ld;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[j] = load_global(reinterpret_cast<const f4*>(rr + min(4 * (w + 4 * j), op.rowss_tiles - 4)));
   }
 
   f4 acc[4];
@@ -209,6 +243,61 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   // one round: rounds after the first run in a loop, the first is peeled so that the
   // prefetched loads above stay in flight (a loop header would wait for all of them)
   const int kk = (tid % TPR) * 8, mr = tid / TPR;
+  auto round_direct = [&](const int kr) __attribute__((always_inline)) {
+    // fragment-major operands: every load below is one contiguous 1 KB per wave (q4 X:
+    // four 256 B runs).  Weights first (HBM), then this wave's X fragments (L2): chunk c,
+    // k step j, m tile mt holds X[16 mt + r16][kc + ko .. +7], the B operand of
+    // mfma16x16x32 in the k order of the weight fragments (q4: the dequantized nibble
+    // order, so the X fragment is permuted after the load).
+    const int KS = K >> 5, KCN = K >> 7;
+    WRaw<Q4> wr[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int kcs = kr + (kg * CPW + c) * KC;
+      if constexpr (!Q4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wr[c].v[j] = load_global(reinterpret_cast<const h8*>(
+              seg.w + (((size_t)lt * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
+      } else {
+        const size_t blk = ((size_t)lt * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
+        wr[c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
+        wr[c].s = load_global(seg.qs + blk);
+      }
+    }
+    h8 xf[CPW][4][4];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kcs = kr + (kg * CPW + c) * KC;
+        const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
+        const int piece = Q4 ? 16 * j + r16 : lane;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          xf[c][j][mt] = load_global(reinterpret_cast<const h8*>(op.x + (((size_t)ks * 4 + mt) * 64 + piece) * 8));
+      }
+    // every load of the round in flight before the first MFMA (the scheduler would
+    // otherwise interleave them and keep only a few outstanding)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // k past the slice: the weight fragment is zeroed (X there is finite data of the
+        // same rows, so the products vanish)
+        const bool kok = kr + (kg * CPW + c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g) < kend;
+        h8 a = wfrag<Q4>(wr[c], j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = kok ? a[e] : (_Float16)0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          h8 b = xf[c][j][mt];
+          if constexpr (Q4) b = perm8(b);
+          acc[mt] = mfma16x16x32(a, b, acc[mt]);
+        }
+      }
+  };
   auto round = [&](const int kr, const bool first) __attribute__((always_inline)) {
     // (1) the X slice [64 rows][XK]: thread -> 8 consecutive k of rows mr + RPP*i (rows
     //     past M repeat the last row; k past the slice is zeroed below)
@@ -218,9 +307,9 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     h8 v[NXL];
 #pragma unroll
     for (int i = 0; i < NXL; ++i)
-      v[i] = *reinterpret_cast<const h8*>(op.x + (size_t)min(m0 + mr + RPP * i, mlast) * op.ldx + kgc);
+      v[i] = *reinterpret_cast<const h8*>(op.x + (size_t)min(m0 + mr + RPP * i, xlast) * op.ldx + kgc);
     h8 sc = (h8){0, 0, 0, 0, 0, 0, 0, 0}, sh = sc;
-    if constexpr (NORM) {
+    if constexpr (NORM == 1) {
       sc = *reinterpret_cast<const h8*>(op.scale + kgc);
       sh = *reinterpret_cast<const h8*>(op.shift + kgc);
     }
@@ -228,7 +317,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     WRaw<Q4> wr[CPW];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) load_wraw<Q4>(wr[c], seg, row, kr + (kg * CPW + c) * KC, g, K);
-    if constexpr (NORM) {
+    if constexpr (NORM == 1) {
       if (first) {
         float ssum = 0.f;
 #pragma unroll
@@ -242,7 +331,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     }
     // (3) normalize / mask the X slice into LDS while the weights are in flight
     float a1[8], b1[8];
-    if constexpr (NORM) {
+    if constexpr (NORM == 1) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         a1[e] = kok ? 1.0f + h2f(sc[e]) : 0.f;
@@ -253,7 +342,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int i = 0; i < NXL; ++i) {
       const int m = mr + RPP * i;
       h8 o;
-      if constexpr (NORM) {
+      if constexpr (NORM == 1) {
         const float rinv = denom[w][m];
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = f2h(fmaf(h2f(v[i][e]) * rinv, a1[e], b1[e]));
@@ -281,8 +370,25 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     }
     __syncthreads();
   };
-  round(kbeg, true);
-  for (int kr = kbeg + XK; kr < kend; kr += XK) round(kr, false);
+  if constexpr (DIRECT) {
+    round_direct(kbeg);
+    for (int kr = kbeg + XK; kr < kend; kr += XK) round_direct(kr);
+  } else {
+    round(kbeg, true);
+    for (int kr = kbeg + XK; kr < kend; kr += XK) round(kr, false);
+  }
+
+  if constexpr (NORM == 2) {
+    const float* rr = op.rowss_in + (size_t)min(m0 + lane, mlast) * op.rowss_ld;
+    float ssum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * (w + 4 * j) < op.rowss_tiles) ssum += ((part[j][0] + part[j][1]) + part[j][2]) + part[j][3];
+    for (int t = 4 * (w + 16); t < op.rowss_tiles; t += 16)  // widths past 1024
+      ssum += ((rr[t] + rr[t + 1]) + rr[t + 2]) + rr[t + 3];
+    denom[w][lane] = ssum;
+    if constexpr (KG == 1) __syncthreads();  // otherwise the k-group sum below has one
+  }
 
   // ---- k groups of a slab summed in k-group order; wave keeps m tiles kg + i*KG ----------
   f4 own[NOWN];
@@ -341,6 +447,24 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     if (tid == 0) counter_reset(&op.counters[cidx]);
   }
 
+  // ---- pre-scaled adaRMS: y[m] = acc[m] / sqrt(mean(x^2) + eps) + acc[M] -----------------
+  if constexpr (NORM == 2) {
+    const int mtM = op.M >> 4, cM = op.M & 15;  // the shift row (M < 64: one m block)
+#pragma unroll
+    for (int i = 0; i < NOWN; ++i)
+      if (kg + i * KG == mtM && r16 == cM) shiftacc[slab * 4 + g] = own[i];
+    __syncthreads();
+    const f4 sv = shiftacc[slab * 4 + g];
+#pragma unroll
+    for (int i = 0; i < NOWN; ++i) {
+      const int m = 16 * (kg + i * KG) + r16;
+      const float tot = ((denom[0][m] + denom[1][m]) + denom[2][m]) + denom[3][m];
+      const float rinv = 1.0f / sqrtf(tot / (float)K + op.eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) own[i][e] = fmaf(own[i][e], rinv, sv[e]);
+    }
+  }
+
   // ---- epilogue in the D layout: row m0 + 16mt + r16 (owned mt), columns n0..n0+3 --------
   if constexpr (EPI == EPI_GEGLU) {
     // lanes g < 2 hold 4 gate columns, lane ^ 32 the matching 4 up columns: the pair
@@ -357,8 +481,11 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       h2 o;
       o[0] = hmul(f2h(gelu_tanh_hw(h2f(f2h(ga)))), f2h(ua));
       o[1] = hmul(f2h(gelu_tanh_hw(h2f(f2h(gb)))), f2h(ub));
-      if (16 * mt + r16 < mrows && nok)
-        *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(seg.out) + (size_t)(m0 + 16 * mt + r16) * ldo + col) = o;
+      if (16 * mt + r16 < mrows && nok) {
+        const int m = m0 + 16 * mt + r16;
+        _Float16* ob = reinterpret_cast<_Float16*>(seg.out);
+        *reinterpret_cast<h2*>(ob + (op.frag_out ? xf_index(m, col) : (size_t)m * ldo + col)) = o;
+      }
     }
     return;
   }
@@ -379,6 +506,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
         s2 += h2f(r) * h2f(r);
       }
       if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = o;
+      if (op.xu_out && mok && nok)
+        store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), o, xus);
     } else {
       h4 y;
 #pragma unroll
@@ -390,6 +519,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       }
       if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU) {
         if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = y;
+        if (EPI == EPI_STORE && op.xu_out && mok && nok)
+          store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), y, xus);
 #pragma unroll
         for (int e = 0; e < 4; ++e) s2 += h2f(y[e]) * h2f(y[e]);
       } else if constexpr (EPI == EPI_VOUT) {
@@ -410,6 +541,11 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       }
     }
     ss[i] = nok ? s2 : 0.f;
+  }
+  if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
+    // the shift row of the pre-scaled copy: one lane per 4 columns
+    if (op.xu_out && kg == 0 && r16 == 0 && nok)
+      *reinterpret_cast<h4*>(op.xu_out + (op.frag_out ? xf_index(op.M, n0) : (size_t)op.M * ldo + n0)) = xush;
   }
   if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
     if (op.rowss_out) {
@@ -479,18 +615,50 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ qw, const _Float1
   }
 }
 
+// fragment-major weight copies (layout in kernels.h): one thread per 16-byte piece
+__device__ __forceinline__ int wf_row(int s, int r, int geglu_F) {
+  return geglu_F > 0 ? (r < 8 ? 8 * s + r : geglu_F + 8 * s + r - 8) : 16 * s + r;
+}
+
+__global__ void wf_shuffle_kernel(const _Float16* __restrict__ w, _Float16* __restrict__ wf, int nslabs, int K,
+                                  int geglu_F) {
+  const int KS = K / 32;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)nslabs * KS * 64) return;
+  const int lane = (int)(i % 64);
+  const long blk = i / 64;
+  const int ks = (int)(blk % KS), s = (int)(blk / KS);
+  const int row = wf_row(s, lane & 15, geglu_F);
+  *reinterpret_cast<h8*>(wf + i * 8) = *reinterpret_cast<const h8*>(w + (size_t)row * K + 32 * ks + 8 * (lane >> 4));
+}
+
+__global__ void wf_shuffle_q4_kernel(const uint32_t* __restrict__ qw, const _Float16* __restrict__ qs,
+                                     uint32_t* __restrict__ qwf, _Float16* __restrict__ qsf, int nslabs, int K,
+                                     int geglu_F) {
+  const int KCN = K / 128;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)nslabs * KCN * 64) return;
+  const int lane = (int)(i % 64), g = lane >> 4;
+  const long blk = i / 64;
+  const int c = (int)(blk % KCN), s = (int)(blk / KCN);
+  const int row = wf_row(s, lane & 15, geglu_F);
+  *reinterpret_cast<u4*>(qwf + i * 4) = *reinterpret_cast<const u4*>(qw + (size_t)row * (K / 8) + 16 * c + 4 * g);
+  qsf[i] = qs[(size_t)row * (K / 32) + 4 * c + g];
+}
+
 // instantiated (tile rows, prologue, epilogue) combinations -- the ones the engine uses:
 //   16: adaRMS + store (q/k/v);  32: adaRMS + GeGLU, gated residual, plain store (action_in);
 //   64: everything else
-template <bool NORM, int EPI, bool TABLE, int TR>
+template <int NORM, int EPI, bool TABLE, int TR>
 constexpr bool sk_combo() {
-  if (TABLE) return TR == 64 && !NORM && EPI == EPI_STORE;
-  if (TR == 16) return NORM && EPI == EPI_STORE;
-  if (TR == 32) return (NORM && EPI == EPI_GEGLU) || (!NORM && (EPI == EPI_GATED_RES || EPI == EPI_STORE));
-  return TR == 64 && EPI != EPI_GATED_RES && EPI != EPI_GEGLU;
+  if (TABLE) return TR == 64 && NORM == 0 && EPI == EPI_STORE;
+  if (TR == 16) return (NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) ||
+                       (NORM == 1 && EPI == EPI_STORE) || (NORM == 0 && EPI == EPI_GATED_RES);
+  if (TR == 32) return (NORM == 1 && EPI == EPI_GEGLU) || (NORM == 0 && (EPI == EPI_GATED_RES || EPI == EPI_STORE));
+  return TR == 64 && NORM != 2 && EPI != EPI_GATED_RES && EPI != EPI_GEGLU;
 }
 
-template <bool Q4, bool NORM, int EPI, bool TABLE, int TR>
+template <bool Q4, int NORM, int EPI, bool TABLE, int TR>
 int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   if constexpr (!sk_combo<NORM, EPI, TABLE, TR>()) {
     MLCV_REQUIRE(false, "skinny GEMM: tile rows / prologue / epilogue combination not built");
@@ -511,7 +679,7 @@ int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   return 0;
 }
 
-template <bool Q4, bool NORM, int EPI, bool TABLE = false>
+template <bool Q4, int NORM, int EPI, bool TABLE = false>
 int launch_tr(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   switch (op.tr) {
     case 16: return launch_nc<Q4, NORM, EPI, TABLE, 16>(op, nc, grid, st);
@@ -521,28 +689,31 @@ int launch_tr(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   }
 }
 
-template <bool Q4>
-int launch_q(const SkOp& op, bool norm, int nc, dim3 grid, hipStream_t st) {
-  if (op.nseg > 3) {
-    MLCV_REQUIRE(!norm && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs,
-                 "more than 3 weight segments need equal sizes, a plain store and no prologue");
-    return launch_tr<Q4, false, EPI_STORE, true>(op, nc, grid, st);
+template <bool Q4, int NORM>
+int launch_norm(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
+  switch (op.epi) {
+    case EPI_STORE: return launch_tr<Q4, NORM, EPI_STORE>(op, nc, grid, st);
+    case EPI_GEGLU: return launch_tr<Q4, NORM, EPI_GEGLU>(op, nc, grid, st);
+    case EPI_VOUT: return launch_tr<Q4, NORM, EPI_VOUT>(op, nc, grid, st);
+    case EPI_EULER: return launch_tr<Q4, NORM, EPI_EULER>(op, nc, grid, st);
+    default: MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
   }
-  if (norm) {
-    switch (op.epi) {
-      case EPI_STORE: return launch_tr<Q4, true, EPI_STORE>(op, nc, grid, st);
-      case EPI_GEGLU: return launch_tr<Q4, true, EPI_GEGLU>(op, nc, grid, st);
-      case EPI_VOUT: return launch_tr<Q4, true, EPI_VOUT>(op, nc, grid, st);
-      case EPI_EULER: return launch_tr<Q4, true, EPI_EULER>(op, nc, grid, st);
-      default: break;
-    }
-  } else {
-    switch (op.epi) {
-      case EPI_STORE: return launch_tr<Q4, false, EPI_STORE>(op, nc, grid, st);
-      case EPI_STORE_SILU: return launch_tr<Q4, false, EPI_STORE_SILU>(op, nc, grid, st);
-      case EPI_GATED_RES: return launch_tr<Q4, false, EPI_GATED_RES>(op, nc, grid, st);
-      default: break;
-    }
+}
+
+template <bool Q4>
+int launch_q(const SkOp& op, int norm, int nc, dim3 grid, hipStream_t st) {
+  if (op.nseg > 3) {
+    MLCV_REQUIRE(norm == 0 && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs,
+                 "more than 3 weight segments need equal sizes, a plain store and no prologue");
+    return launch_tr<Q4, 0, EPI_STORE, true>(op, nc, grid, st);
+  }
+  if (norm == 1) return launch_norm<Q4, 1>(op, nc, grid, st);
+  if (norm == 2) return launch_norm<Q4, 2>(op, nc, grid, st);
+  switch (op.epi) {
+    case EPI_STORE: return launch_tr<Q4, 0, EPI_STORE>(op, nc, grid, st);
+    case EPI_STORE_SILU: return launch_tr<Q4, 0, EPI_STORE_SILU>(op, nc, grid, st);
+    case EPI_GATED_RES: return launch_tr<Q4, 0, EPI_GATED_RES>(op, nc, grid, st);
+    default: break;
   }
   MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
 }
@@ -591,12 +762,46 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   }
   const int mblocks = (op.M + MB - 1) / MB;
   dim3 grid(op.ntiles, op.splitk, mblocks);
-  const bool norm = op.scale != nullptr;
+  MLCV_REQUIRE(!op.prescaled || (op.rowss_in && op.M < MB && op.rowss_tiles >= 4 && op.rowss_tiles % 4 == 0 &&
+                                  op.rowss_ld % 4 == 0),
+               "pre-scaled adaRMS needs M < 64 (row M carries the shift) and the row statistics");
+  MLCV_REQUIRE(op.xu_out == nullptr || (op.M < MB && op.xu_scale && op.xu_shift &&
+                                        (op.epi == EPI_GATED_RES || op.epi == EPI_STORE) && op.nseg == 1),
+               "pre-scaled output needs M < 64, its scale and shift, and a STORE / GATED_RES epilogue");
+  const int norm = op.prescaled ? 2 : (op.scale != nullptr ? 1 : 0);
   const int cps = op.kper / KC;
   int nc = cps >= 5 ? 8 : cps >= 3 ? 4 : cps;
-  if (nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS) for big grids
+  const bool direct = op.tr == 16 && norm != 1;  // X fragments straight into registers, little LDS
+  MLCV_REQUIRE(direct == op.frag, "16-row tiles without the per-element prologue take fragment-major operands");
+  MLCV_REQUIRE(!op.frag || (op.M < MB && op.K % 128 == 0 && op.nseg <= 3),
+               "fragment-major operands need M < 64, K % 128 == 0 and at most 3 segments");
+  MLCV_REQUIRE(!op.frag_out || op.M < MB, "fragment-major outputs need M < 64");
+  if (!direct && nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS)
   if (q4) MLCV_TRY(launch_q<true>(op, norm, nc, grid, st));
   else MLCV_TRY(launch_q<false>(op, norm, nc, grid, st));
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, hipStream_t st) {
+  MLCV_REQUIRE(K % 128 == 0, "fragment-major weights need K % 128 == 0");
+  MLCV_REQUIRE(geglu_F > 0 ? (N == 2 * geglu_F && geglu_F % 8 == 0) : N % 16 == 0,
+               "fragment-major weights need 16-row slabs (GeGLU: F % 8 == 0)");
+  const int nslabs = geglu_F > 0 ? geglu_F / 8 : N / 16;
+  const long n = (long)nslabs * (K / 32) * 64;
+  wf_shuffle_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(w, wf, nslabs, K, geglu_F);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int wf_shuffle_q4_launch(const uint32_t* qw, const _Float16* qs, uint32_t* qwf, _Float16* qsf, int N, int K,
+                         int geglu_F, hipStream_t st) {
+  MLCV_REQUIRE(K % 128 == 0, "fragment-major weights need K % 128 == 0");
+  MLCV_REQUIRE(geglu_F > 0 ? (N == 2 * geglu_F && geglu_F % 8 == 0) : N % 16 == 0,
+               "fragment-major weights need 16-row slabs (GeGLU: F % 8 == 0)");
+  const int nslabs = geglu_F > 0 ? geglu_F / 8 : N / 16;
+  const long n = (long)nslabs * (K / 128) * 64;
+  wf_shuffle_q4_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(qw, qs, qwf, qsf, nslabs, K, geglu_F);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

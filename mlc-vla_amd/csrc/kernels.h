@@ -35,7 +35,7 @@ struct SkOp {
   const _Float16* x;     // X [M][ldx]
   int ldx, M, K;
   // adaRMS prologue: xn = fp16((x / sqrt(mean(x^2)+eps)) * (1 + scale) + shift)
-  const _Float16* scale; // [K] or null (no prologue)
+  const _Float16* scale; // [K] or null (no per-element prologue)
   const _Float16* shift; // [K]
   float eps;
   // row sums of squares of the residual stream, one partial per 16-column group:
@@ -44,6 +44,21 @@ struct SkOp {
   const float* rowss_in;
   float* rowss_out;
   int rowss_ld, rowss_tiles;
+  // pre-scaled adaRMS (consumer, M < 64): X rows [0, M) hold fp16(x * (1 + scale)) and
+  // row M holds the shift, so the product needs no per-element prologue; the epilogue
+  // forms y = acc[m] / sqrt(mean(x^2) + eps) + acc[M] from the row statistics
+  bool prescaled;
+  // producer side: with xu_out set, the STORE / GATED_RES epilogues also write
+  // xu_out[m][n] = fp16(x[m][n] * (1 + xu_scale[n])) and xu_out[M][n] = xu_shift[n]
+  // (stride ldo, M < 64): the next adaRMS GEMM's pre-scaled X
+  _Float16* xu_out;
+  const _Float16* xu_scale;
+  const _Float16* xu_shift;
+  // fragment-major operands (16-row tiles, M < 64, K % 128 == 0): X in the xf_index
+  // layout, the weights pre-shuffled by wf_shuffle_launch
+  bool frag;
+  // the GeGLU output and xu_out are written in the xf_index layout (M < 64)
+  bool frag_out;
   int epi;
   const _Float16* gate;  // [N] (EPI_GATED_RES)
   int geglu_F;           // EPI_GEGLU: rows [0,F) gate, [F,2F) up
@@ -68,6 +83,15 @@ struct SkPlan {
 SkPlan sk_plan(int ntiles, int K, int mblocks, int splits);
 size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p, int tr);
 int sk_launch(const SkOp& op, bool q4, hipStream_t st);
+
+// fragment-major copies of the weights of 16-row slabs for the 16-row skinny tiles:
+// fp16 block (slab s, k step ks) = 1 KB, lane 16 g + r holding W[row(s, r)][32 ks + 8 g ..
+// +7]; q4 block (s, 128-k chunk c) = 1 KB of words, lane 16 g + r holding the 4 words of
+// row(s, r) for k = 128 c + 32 g .. +31, and 64 scales in lane order.  row(s, r) = 16 s + r,
+// or with geglu_F > 0 gate row 8 s + r (r < 8) and up row F + 8 s + r - 8.
+int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, hipStream_t st);
+int wf_shuffle_q4_launch(const uint32_t* qw, const _Float16* qs, uint32_t* qwf, _Float16* qsf, int N, int K,
+                         int geglu_F, hipStream_t st);
 
 // q4f16_1 helpers
 int q4_quantize_launch(const _Float16* w, uint32_t* qw, _Float16* qs, int N, int K, hipStream_t st);
@@ -96,6 +120,7 @@ struct AttnArgs {
   int ks_roped;          // suffix k already roped
   _Float16* out;         // [Tq][out_ld], head h at h*hd
   int out_ld;
+  int out_frag;          // out in the fragment-major layout (xf_index, Tq <= 64, K = H*hd)
   float* part_o;         // [KV][nsplit][Rpad][hd]
   float* part_ml;        // [KV][nsplit][Rpad][2]
   int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
