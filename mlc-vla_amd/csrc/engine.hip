@@ -40,6 +40,7 @@ struct OpDesc {
   int tr = 64, splits = 0;  // weight rows per tile, K slices (0: planner's choice)
   bool q4 = false;
   bool frag = false;  // fragment-major X and weights (16-row tiles)
+  bool xrow = false;  // row-major X with M <= 16, fragment-major weights (16-row tiles)
 };
 
 // Tiling of the step's layer GEMMs.  With fragment-major operands (M < 64): 16-row tiles
@@ -53,6 +54,8 @@ struct Tiling {
 Tiling TILE_QKV = {16, 1}, TILE_O = {16, 4}, TILE_GU = {16, 1}, TILE_DOWN = {16, 8};
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
+constexpr int MOD_SPLITS = 1;   // modulation pieces (16-row tiles: 384 workgroups each)
+constexpr int TMLP_SPLITS = 2;  // time MLP (16-row tiles: 128 workgroups)
 
 // MLCV_TILING="qkv=16:S,o=16:S,gu=16:S,down=16:S" overrides the K slices of the
 // fragment-major layer GEMMs for tuning (read at context creation; 0 = planner).
@@ -124,6 +127,9 @@ struct Ctx {
   // and h are [64][K] in the xf_index layout; the action expert's layer and head weights
   // get pre-shuffled copies at bind time
   bool frag = false;
+  // the time MLP and modulation GEMVs (M = steps <= 16) on 16-row register-direct tiles
+  // with pre-shuffled weights
+  bool small_m = false;
   float *x32, *x0, *vout, *cos, *sin, *mask, *rowss;
   int rss_tiles = 1;
   // prefill path
@@ -142,7 +148,18 @@ struct Ctx {
   SkSeg* d_segs = nullptr;
   std::vector<SkSeg> h_segs;
   std::vector<OpDesc> layer_ops;  // 4 per layer: qkv, o, gate_up, down
-  OpDesc op_tin, op_tout, op_mod, op_ain, op_aout;
+  OpDesc op_tin, op_tout, op_ain, op_aout;
+  // the adaRMS modulations in 2 pieces: layer 0's two norms, then every other norm (one
+  // launch over a segment table).  With fork_mod the step runs them on `side` so that the
+  // second piece streams while layer 0 runs; ops wait for their piece (events mod_ev).
+  std::vector<OpDesc> mod_ops;
+  hipStream_t side = nullptr;
+  hipEvent_t cond_ev = nullptr;
+  std::vector<hipEvent_t> mod_ev;
+  bool fork_mod = false;
+  float* skws_side = nullptr;  // split-K workspace / counters of the side stream
+  unsigned* counters_side = nullptr;
+  size_t ncounters_side = 0;
 
   hipStream_t cap = nullptr;
   Graph g_step, g_loop, g_prefill, g_chunk;
@@ -159,6 +176,10 @@ struct Ctx {
     for (void* p : bind_owned) (void)hipFree(p);
     for (void* p : owned) (void)hipFree(p);
     if (cap) (void)hipStreamDestroy(cap);
+    if (side) (void)hipStreamDestroy(side);
+    if (cond_ev) (void)hipEventDestroy(cond_ev);
+    for (hipEvent_t e : mod_ev)
+      if (e) (void)hipEventDestroy(e);
     if (d_segs) (void)hipFree(d_segs);
   }
 };
@@ -190,16 +211,39 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   op.rowss_ld = c.rss_tiles;
   op.rowss_tiles = c.rss_tiles;
   op.frag = d.frag;
+  op.xrow = d.xrow;
   return op;
 }
 
 int run_op(const Ctx& c, const OpDesc& d, SkOp op, hipStream_t st) { return sk_launch(op, d.q4, st); }
 
 // ---- time MLP + all adaRMS modulations for M steps --------------------------
-int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st) {
+// fork: the modulation pieces go to the side stream after the time MLP, each followed by
+// its event; the caller waits for piece p (wait_mod) before the first op that reads it.
+int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool fork) {
   MLCV_TRY(run_op(c, c.op_tin, make_op(c, c.op_tin, te, c.W1, M), st));
   MLCV_TRY(run_op(c, c.op_tout, make_op(c, c.op_tout, c.tmp, c.W1, M), st));
-  MLCV_TRY(run_op(c, c.op_mod, make_op(c, c.op_mod, c.cond, c.W1, M), st));
+  hipStream_t ms = st;
+  if (fork) {
+    MLCV_HIP(hipEventRecord(c.cond_ev, st));
+    MLCV_HIP(hipStreamWaitEvent(c.side, c.cond_ev, 0));
+    ms = c.side;
+  }
+  for (int p = 0; p < (int)c.mod_ops.size(); ++p) {
+    SkOp op = make_op(c, c.mod_ops[p], c.cond, c.W1, M);
+    if (fork) {
+      op.ws = c.skws_side;
+      op.counters = c.counters_side;
+    }
+    MLCV_TRY(run_op(c, c.mod_ops[p], op, ms));
+    if (fork) MLCV_HIP(hipEventRecord(c.mod_ev[p], ms));
+  }
+  return 0;
+}
+
+// before the first op that reads the modulations of layer p (p == D: the final norm)
+int wait_mod(Ctx& c, int p, bool forked, hipStream_t st) {
+  if (forked) MLCV_HIP(hipStreamWaitEvent(st, c.mod_ev[p == 0 ? 0 : 1], 0));
   return 0;
 }
 
@@ -312,8 +356,10 @@ int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  //
 }
 
 // ---- one suffix-only velocity evaluation (modulations already in modp) -------
+// forked: the modulation pieces run on the side stream (enqueue_time_mod with fork)
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
-                 hipStream_t st) {
+                 hipStream_t st, bool forked = false) {
+  MLCV_TRY(wait_mod(c, 0, forked, st));
   SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
   ain.rowss_out = c.rowss;
   set_next_norm(c, ain, mod_of(c, modp, 0));
@@ -323,6 +369,7 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
     MLCV_TRY(enqueue_attn(c, L, keys, values, st));
     MLCV_TRY(enqueue_oproj(c, L, modp, st));
     MLCV_TRY(enqueue_gateup(c, L, modp, st));
+    MLCV_TRY(wait_mod(c, L + 1, forked, st));  // down writes the next norm's input
     MLCV_TRY(enqueue_down(c, L, modp, st));
   }
   return enqueue_head(c, modp, euler, st);
@@ -428,13 +475,14 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
 int enqueue_loop(Ctx& c, const float* keys, const _Float16* values, hipStream_t st) {
   const size_t modstep = (size_t)c.NM * 3 * c.W1;
   MLCV_TRY(euler_init_launch(c.x0, c.x32, c.xin16, c.T * c.A, st));
-  if (c.hoist) MLCV_TRY(enqueue_time_mod(c, c.te, c.NS, st));
+  if (c.hoist) MLCV_TRY(enqueue_time_mod(c, c.te, c.NS, st, c.fork_mod));
   for (int i = 0; i < c.NS; ++i) {
     if (c.hoist) {
-      MLCV_TRY(enqueue_step(c, keys, values, c.mod + i * modstep, true, st));
+      // step 0 waits for each piece; later steps follow it on the same stream
+      MLCV_TRY(enqueue_step(c, keys, values, c.mod + i * modstep, true, st, c.fork_mod && i == 0));
     } else {
-      MLCV_TRY(enqueue_time_mod(c, c.te + (size_t)i * c.W1, 1, st));
-      MLCV_TRY(enqueue_step(c, keys, values, c.mod, true, st));
+      MLCV_TRY(enqueue_time_mod(c, c.te + (size_t)i * c.W1, 1, st, c.fork_mod));
+      MLCV_TRY(enqueue_step(c, keys, values, c.mod, true, st, c.fork_mod));
     }
   }
   return 0;
@@ -594,6 +642,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.rowss, (size_t)T * c.rss_tiles);
   c.frag = T < 64 && W1 % 128 == 0 && nq % 128 == 0 && c.F1 % 128 == 0 && nkv % 16 == 0 && c.A % 16 == 0;
   c.prescaled = c.frag;
+  c.small_m = c.frag && c.NS <= 16;
   ALLOC(c.xu, (size_t)64 * W1);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
@@ -641,8 +690,10 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       {tiles(W1, tile_o(c).tr), nq, mb_t, tile_o(c).tr, tile_o(c).splits},
       {tiles(c.F1, tile_gu(c).tr / 2), W1, mb_t, tile_gu(c).tr, tile_gu(c).splits},
       {tiles(W1, tile_down(c).tr), c.F1, mb_t, tile_down(c).tr, tile_down(c).splits},
-      {tiles(W1, 64), W1, mb_s, 64, 0},                                          // time mlp
-      {c.NM * tiles(3 * W1, 64), W1, mb_s, 64, 1},                               // modulation
+      {tiles(W1, 16), W1, mb_s, 16, TMLP_SPLITS},                                // time mlp
+      {tiles(W1, 64), W1, mb_s, 64, 0},
+      {std::max(2, c.NM - 2) * tiles(3 * W1, 64), W1, mb_s, 64, 0},              // modulation pieces
+      {std::max(2, c.NM - 2) * tiles(3 * W1, 16), W1, mb_s, 16, MOD_SPLITS},
       {tiles(W1, TR_AIN), c.A, mb_t, TR_AIN, SPLIT_AIN},                         // action_in
       {tiles(c.A, tile_head(c).tr), W1, mb_t, tile_head(c).tr, tile_head(c).splits},  // action_out
   };
@@ -653,9 +704,30 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   }
   ALLOC(c.skws, c.skws_floats);
   ALLOC(c.counters, c.ncounters);
+  {
+    // modulation pieces: up to NM - 2 segments of 3 W1 rows; 16-row tiles take one split,
+    // 64-row tiles the planner's
+    const int segs = std::max(2, c.NM - 2);
+    const int nt = segs * tiles(3 * W1, 16);
+    const SkPlan p = sk_plan(segs * tiles(3 * W1, 64), W1, mb_s, 0);
+    ALLOC(c.skws_side, std::max<size_t>(1, sk_ws_floats(segs * tiles(3 * W1, 64), mb_s, p, 64)));
+    ALLOC(c.counters_side, (size_t)nt * mb_s);
+    c.ncounters_side = (size_t)nt * mb_s;
+  }
   ALLOC(c.zero, 64 * 64);
 #undef ALLOC
+  c.mod_ev.assign(2, nullptr);
+  // measured: the forked modulation slows the layer chain more than it hides, so it is
+  // off unless MLCV_FORK_MOD=1 (tuning)
+  c.fork_mod = std::getenv("MLCV_FORK_MOD") != nullptr && std::atoi(std::getenv("MLCV_FORK_MOD")) != 0;
+  bool ev_ok = hipEventCreateWithFlags(&c.cond_ev, hipEventDisableTiming) == hipSuccess;
+  for (hipEvent_t& e : c.mod_ev) ev_ok = ev_ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+  if (!ev_ok || hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking) != hipSuccess) {
+    set_error("modulation stream / event setup failed");
+    return fail(-1);
+  }
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(c.counters_side, 0, c.ncounters_side * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.xu, 0, (size_t)64 * W1 * 2) != hipSuccess ||
       hipMemset(c.attn, 0, (size_t)std::max(T, 64) * nq * 2) != hipSuccess ||
       hipMemset(c.h, 0, (size_t)std::max(T, 64) * c.F1 * 2) != hipSuccess ||
@@ -795,17 +867,31 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     seg_ops(c, ops[3], {seg_of(fdn, c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, tile_down(c).tr, tile_down(c).splits);
     for (int i = 0; i < 4; ++i) ops[i].frag = c.frag;
   }
-  seg_ops(c, c.op_tin, {seg_of(c.tin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
-  seg_ops(c, c.op_tout, {seg_of(c.tout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, 64, 0);
   {
-    std::vector<SkSeg> ms;
+    // small-M GEMVs: 16-row register-direct tiles on shuffled weights, or 64-row tiles
+    auto gemv_copy = [&](const Lin& l) -> Lin { return c.small_m ? frag_copy(l, 0) : l; };
+    const int gtr = c.small_m ? 16 : 64;
+    const Lin ftin = gemv_copy(c.tin), ftout = gemv_copy(c.tout);
+    MLCV_REQUIRE(ftin.N >= 0 && ftout.N >= 0, get_error());
+    seg_ops(c, c.op_tin, {seg_of(ftin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, c.small_m ? TMLP_SPLITS : 0);
+    seg_ops(c, c.op_tout, {seg_of(ftout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, c.small_m ? TMLP_SPLITS : 0);
+    c.op_tin.xrow = c.op_tout.xrow = c.small_m;
     const int ldo = c.NM * 3 * W1;
-    for (int L = 0; L < c.D; ++L) {
-      ms.push_back(seg_of(c.layers[L].mod_in, c.mod + (size_t)(2 * L) * 3 * W1, 3 * W1, ldo));
-      ms.push_back(seg_of(c.layers[L].mod_post, c.mod + (size_t)(2 * L + 1) * 3 * W1, 3 * W1, ldo));
+    std::vector<SkSeg> first, rest;
+    for (int L = 0; L <= c.D; ++L) {
+      std::vector<const Lin*> ls;
+      if (L < c.D) ls = {&c.layers[L].mod_in, &c.layers[L].mod_post};
+      else ls = {&c.final_mod};
+      for (size_t i = 0; i < ls.size(); ++i) {
+        const Lin f = gemv_copy(*ls[i]);
+        MLCV_REQUIRE(f.N >= 0, get_error());
+        (L == 0 ? first : rest).push_back(seg_of(f, c.mod + (size_t)(2 * L + i) * 3 * W1, 3 * W1, ldo));
+      }
     }
-    ms.push_back(seg_of(c.final_mod, c.mod + (size_t)(2 * c.D) * 3 * W1, 3 * W1, ldo));
-    seg_ops(c, c.op_mod, ms, W1, EPI_STORE, c.q4, 64, 1);
+    c.mod_ops.assign(2, OpDesc{});
+    seg_ops(c, c.mod_ops[0], first, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
+    seg_ops(c, c.mod_ops[1], rest, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
+    for (OpDesc& d : c.mod_ops) d.xrow = c.small_m;
   }
   seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, TR_AIN, SPLIT_AIN);
   {
@@ -864,8 +950,8 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
   MLCV_TRY(run_graph(c, c.g_step, {keys, values},
                      [&](hipStream_t s) {
-                       MLCV_TRY(enqueue_time_mod(c, c.te, 1, s));
-                       return enqueue_step(c, keys, vals, c.mod, false, s);
+                       MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
+                       return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod);
                      },
                      st));
   MLCV_HIP(hipMemcpyAsync(v_out, c.vout, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
@@ -922,8 +1008,10 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
   if (op == MLCV_OP_ATTENTION) MLCV_REQUIRE(keys && values, "attention needs keys and values");
   for (int i = 0; i < iters; ++i) {
     switch (op) {
-      case MLCV_OP_TIME_MOD: MLCV_TRY(enqueue_time_mod(c, c.te, 1, st)); break;
-      case MLCV_OP_MODULATION: MLCV_TRY(run_op(c, c.op_mod, make_op(c, c.op_mod, c.cond, c.W1, 1), st)); break;
+      case MLCV_OP_TIME_MOD: MLCV_TRY(enqueue_time_mod(c, c.te, 1, st, false)); break;
+      case MLCV_OP_MODULATION:
+        for (const OpDesc& d : c.mod_ops) MLCV_TRY(run_op(c, d, make_op(c, d, c.cond, c.W1, 1), st));
+        break;
       case MLCV_OP_QKV: MLCV_TRY(enqueue_qkv(c, layer, c.mod, st)); break;
       case MLCV_OP_ATTENTION: MLCV_TRY(enqueue_attn(c, layer, keys, vals, st)); break;
       case MLCV_OP_OPROJ: MLCV_TRY(enqueue_oproj(c, layer, c.mod, st)); break;

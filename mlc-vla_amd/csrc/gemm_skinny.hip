@@ -130,7 +130,10 @@ __device__ __forceinline__ void sum_splits(const float* base, size_t split_strid
 // NORM: 0 none; 1 adaRMS applied to X per element (row scales from the row statistics);
 // 2 pre-scaled X (the producer wrote fp16(x * (1 + scale)) and the shift as row M), the
 // row scale and shift product applied in the epilogue.
-template <bool Q4, int NORM, int EPI, int NC, bool TABLE, int TR>
+// XM: 0 X row-major, staged through LDS; 1 fragment-major X and weights, loaded straight
+// into registers (16-row tiles); 2 row-major X with M <= 16 (one m tile, lanes of rows
+// past M contribute zeros) and fragment-major weights, loaded straight into registers.
+template <bool Q4, int NORM, int EPI, int NC, bool TABLE, int TR, int XM>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   constexpr int SLABS = TR / 16;
   constexpr int KG = 4 / SLABS;      // waves per slab
@@ -146,7 +149,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   // 16-row tiles without the per-element prologue: every wave owns its own k range, so
   // its MFMA B fragments are loaded straight from X into registers (no LDS staging, no
   // barrier between loads and MFMAs: each MFMA waits only for its own operands)
-  constexpr bool DIRECT = TR == 16 && NORM != 1;
+  constexpr bool DIRECT = XM != 0;
+  constexpr int XMT = XM == 2 ? 1 : 4;  // m tiles loaded and multiplied by the direct path
   constexpr int XS_HALFS = DIRECT ? KG * SLABS * 4 * 64 * 8 : MB * XLD;
   __shared__ __attribute__((aligned(16))) _Float16 xs[XS_HALFS];
   __shared__ float denom[4][MB];     // NORM 1: 1 / sqrt(mean(x^2) + eps) per row, per wave;
@@ -265,17 +269,22 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
         wr[c].s = load_global(seg.qs + blk);
       }
     }
-    h8 xf[CPW][4][4];
+    h8 xf[CPW][4][XMT];
 #pragma unroll
     for (int c = 0; c < CPW; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int kcs = kr + (kg * CPW + c) * KC;
-        const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
-        const int piece = Q4 ? 16 * j + r16 : lane;
+        if constexpr (XM == 1) {
+          const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
+          const int piece = Q4 ? 16 * j + r16 : lane;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          xf[c][j][mt] = load_global(reinterpret_cast<const h8*>(op.x + (((size_t)ks * 4 + mt) * 64 + piece) * 8));
+          for (int mt = 0; mt < 4; ++mt)
+            xf[c][j][mt] = load_global(reinterpret_cast<const h8*>(op.x + (((size_t)ks * 4 + mt) * 64 + piece) * 8));
+        } else {
+          const int kx = min(kcs + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g), K - 8);
+          xf[c][j][0] = load_global(reinterpret_cast<const h8*>(op.x + (size_t)min(r16, mlast) * op.ldx + kx));
+        }
       }
     // every load of the round in flight before the first MFMA (the scheduler would
     // otherwise interleave them and keep only a few outstanding)
@@ -291,8 +300,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = kok ? a[e] : (_Float16)0.0f;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < XMT; ++mt) {
           h8 b = xf[c][j][mt];
+          if constexpr (XM == 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) b[e] = r16 < op.M ? b[e] : (_Float16)0.0f;
+          }
           if constexpr (Q4) b = perm8(b);
           acc[mt] = mfma16x16x32(a, b, acc[mt]);
         }
@@ -649,53 +662,68 @@ __global__ void wf_shuffle_q4_kernel(const uint32_t* __restrict__ qw, const _Flo
 // instantiated (tile rows, prologue, epilogue) combinations -- the ones the engine uses:
 //   16: adaRMS + store (q/k/v);  32: adaRMS + GeGLU, gated residual, plain store (action_in);
 //   64: everything else
-template <int NORM, int EPI, bool TABLE, int TR>
+template <int NORM, int EPI, bool TABLE, int TR, int XM>
 constexpr bool sk_combo() {
+  if (XM == 1)
+    return TR == 16 && !TABLE &&
+           ((NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) || (NORM == 0 && EPI == EPI_GATED_RES));
+  if (XM == 2) return TR == 16 && NORM == 0 && (EPI == EPI_STORE || (EPI == EPI_STORE_SILU && !TABLE));
   if (TABLE) return TR == 64 && NORM == 0 && EPI == EPI_STORE;
-  if (TR == 16) return (NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) ||
-                       (NORM == 1 && EPI == EPI_STORE) || (NORM == 0 && EPI == EPI_GATED_RES);
+  if (TR == 16) return NORM == 1 && EPI == EPI_STORE;
   if (TR == 32) return (NORM == 1 && EPI == EPI_GEGLU) || (NORM == 0 && (EPI == EPI_GATED_RES || EPI == EPI_STORE));
   return TR == 64 && NORM != 2 && EPI != EPI_GATED_RES && EPI != EPI_GEGLU;
 }
 
-template <bool Q4, int NORM, int EPI, bool TABLE, int TR>
+template <bool Q4, int NORM, int EPI, bool TABLE, int TR, int XM>
 int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
-  if constexpr (!sk_combo<NORM, EPI, TABLE, TR>()) {
+  if constexpr (!sk_combo<NORM, EPI, TABLE, TR, XM>()) {
     MLCV_REQUIRE(false, "skinny GEMM: tile rows / prologue / epilogue combination not built");
   } else {
     constexpr int KG = 4 / (TR / 16);
     if (nc < KG) nc = KG;
     switch (nc) {
       case 1:
-        if constexpr (KG <= 1) skinny_kernel<Q4, NORM, EPI, 1, TABLE, TR><<<grid, 256, 0, st>>>(op);
+        if constexpr (KG <= 1) skinny_kernel<Q4, NORM, EPI, 1, TABLE, TR, XM><<<grid, 256, 0, st>>>(op);
         break;
       case 2:
-        if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR><<<grid, 256, 0, st>>>(op);
+        if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR, XM><<<grid, 256, 0, st>>>(op);
         break;
-      case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR><<<grid, 256, 0, st>>>(op); break;
-      default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR><<<grid, 256, 0, st>>>(op); break;
+      case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR, XM><<<grid, 256, 0, st>>>(op); break;
+      default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR, XM><<<grid, 256, 0, st>>>(op); break;
     }
   }
   return 0;
 }
 
-template <bool Q4, int NORM, int EPI, bool TABLE = false>
+template <bool Q4, int NORM, int EPI, bool TABLE, int XM>
 int launch_tr(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   switch (op.tr) {
-    case 16: return launch_nc<Q4, NORM, EPI, TABLE, 16>(op, nc, grid, st);
-    case 32: return launch_nc<Q4, NORM, EPI, TABLE, 32>(op, nc, grid, st);
-    case 64: return launch_nc<Q4, NORM, EPI, TABLE, 64>(op, nc, grid, st);
+    case 16: return launch_nc<Q4, NORM, EPI, TABLE, 16, XM>(op, nc, grid, st);
+    case 32: return launch_nc<Q4, NORM, EPI, TABLE, 32, XM>(op, nc, grid, st);
+    case 64: return launch_nc<Q4, NORM, EPI, TABLE, 64, XM>(op, nc, grid, st);
     default: MLCV_REQUIRE(false, "skinny GEMM tile rows must be 16, 32 or 64");
   }
 }
 
-template <bool Q4, int NORM>
+template <bool Q4, int NORM, int XM>
 int launch_norm(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   switch (op.epi) {
-    case EPI_STORE: return launch_tr<Q4, NORM, EPI_STORE>(op, nc, grid, st);
-    case EPI_GEGLU: return launch_tr<Q4, NORM, EPI_GEGLU>(op, nc, grid, st);
-    case EPI_VOUT: return launch_tr<Q4, NORM, EPI_VOUT>(op, nc, grid, st);
-    case EPI_EULER: return launch_tr<Q4, NORM, EPI_EULER>(op, nc, grid, st);
+    case EPI_STORE: return launch_tr<Q4, NORM, EPI_STORE, false, XM>(op, nc, grid, st);
+    case EPI_GEGLU: return launch_tr<Q4, NORM, EPI_GEGLU, false, XM>(op, nc, grid, st);
+    case EPI_VOUT: return launch_tr<Q4, NORM, EPI_VOUT, false, XM>(op, nc, grid, st);
+    case EPI_EULER: return launch_tr<Q4, NORM, EPI_EULER, false, XM>(op, nc, grid, st);
+    default: MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
+  }
+}
+
+template <bool Q4, int XM>
+int launch_epi(const SkOp& op, int norm, int nc, dim3 grid, hipStream_t st) {
+  if (norm == 1) return launch_norm<Q4, 1, XM>(op, nc, grid, st);
+  if (norm == 2) return launch_norm<Q4, 2, XM>(op, nc, grid, st);
+  switch (op.epi) {
+    case EPI_STORE: return launch_tr<Q4, 0, EPI_STORE, false, XM>(op, nc, grid, st);
+    case EPI_STORE_SILU: return launch_tr<Q4, 0, EPI_STORE_SILU, false, XM>(op, nc, grid, st);
+    case EPI_GATED_RES: return launch_tr<Q4, 0, EPI_GATED_RES, false, XM>(op, nc, grid, st);
     default: MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
   }
 }
@@ -703,19 +731,14 @@ int launch_norm(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
 template <bool Q4>
 int launch_q(const SkOp& op, int norm, int nc, dim3 grid, hipStream_t st) {
   if (op.nseg > 3) {
-    MLCV_REQUIRE(norm == 0 && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs,
+    MLCV_REQUIRE(norm == 0 && op.epi == EPI_STORE && op.seg_tiles > 0 && op.segs && !op.frag,
                  "more than 3 weight segments need equal sizes, a plain store and no prologue");
-    return launch_tr<Q4, 0, EPI_STORE, true>(op, nc, grid, st);
+    if (op.xrow) return launch_tr<Q4, 0, EPI_STORE, true, 2>(op, nc, grid, st);
+    return launch_tr<Q4, 0, EPI_STORE, true, 0>(op, nc, grid, st);
   }
-  if (norm == 1) return launch_norm<Q4, 1>(op, nc, grid, st);
-  if (norm == 2) return launch_norm<Q4, 2>(op, nc, grid, st);
-  switch (op.epi) {
-    case EPI_STORE: return launch_tr<Q4, 0, EPI_STORE>(op, nc, grid, st);
-    case EPI_STORE_SILU: return launch_tr<Q4, 0, EPI_STORE_SILU>(op, nc, grid, st);
-    case EPI_GATED_RES: return launch_tr<Q4, 0, EPI_GATED_RES>(op, nc, grid, st);
-    default: break;
-  }
-  MLCV_REQUIRE(false, "unsupported skinny GEMM prologue/epilogue combination");
+  if (op.frag) return launch_epi<Q4, 1>(op, norm, nc, grid, st);
+  if (op.xrow) return launch_epi<Q4, 2>(op, norm, nc, grid, st);
+  return launch_epi<Q4, 0>(op, norm, nc, grid, st);
 }
 
 }  // namespace
@@ -771,8 +794,11 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   const int norm = op.prescaled ? 2 : (op.scale != nullptr ? 1 : 0);
   const int cps = op.kper / KC;
   int nc = cps >= 5 ? 8 : cps >= 3 ? 4 : cps;
-  const bool direct = op.tr == 16 && norm != 1;  // X fragments straight into registers, little LDS
-  MLCV_REQUIRE(direct == op.frag, "16-row tiles without the per-element prologue take fragment-major operands");
+  const bool direct = op.frag || op.xrow;  // operands straight into registers, little LDS
+  MLCV_REQUIRE(!(op.frag && op.xrow), "fragment-major and row-major X at once");
+  MLCV_REQUIRE(!direct || op.tr == 16, "register-direct operands need 16-row tiles");
+  MLCV_REQUIRE(!op.xrow || (op.M <= 16 && op.K % 128 == 0 && norm == 0),
+               "row-major direct X needs M <= 16, K % 128 == 0 and no prologue");
   MLCV_REQUIRE(!op.frag || (op.M < MB && op.K % 128 == 0 && op.nseg <= 3),
                "fragment-major operands need M < 64, K % 128 == 0 and at most 3 segments");
   MLCV_REQUIRE(!op.frag_out || op.M < MB, "fragment-major outputs need M < 64");

@@ -59,6 +59,9 @@ struct SkOp {
   bool frag;
   // the GeGLU output and xu_out are written in the xf_index layout (M < 64)
   bool frag_out;
+  // row-major X with M <= 16 and fragment-major weights (16-row tiles, no prologue):
+  // the small-M time MLP and modulation GEMVs
+  bool xrow;
   int epi;
   const _Float16* gate;  // [N] (EPI_GATED_RES)
   int geglu_F;           // EPI_GEGLU: rows [0,F) gate, [F,2F) up
