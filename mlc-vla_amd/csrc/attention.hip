@@ -46,6 +46,15 @@ struct AttnSmem {
   float msk[KCH];
 };
 
+// One 32-key chunk of prefix K/V as a byte image of AttnSmem (K split hi/lo, V
+// transposed, the mask), rounded up to whole passes of 256 threads x 16 bytes.  Images
+// are built once per call by attn_img_prep_kernel; the attention kernel copies them into
+// LDS with 16-byte loads and stores (no conversion on the critical path).
+template <int HD>
+constexpr int img_bytes() {
+  return ((int)sizeof(AttnSmem<HD>) + NT * 16 - 1) / (NT * 16) * (NT * 16);
+}
+
 // One key chunk in registers between its global loads and its LDS stores.
 //   K item (key j, dims dp..dp+7 and dp+HD/2..+7) as fp32 (the RoPE pair of the suffix
 //   loader is one item); V item (keys 2jp, 2jp+1; dims d0..d0+7).  Items past the
@@ -191,6 +200,17 @@ __device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>
   r.msk = in.msk;
 }
 
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS accesses, not for
+// its outstanding global loads (__syncthreads also drains vmcnt, which would expose the
+// latency of every prefetch issued before it).  The empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt not waited
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int HD>
 __device__ __forceinline__ void store_chunk(const ChunkRegs<HD>& r, AttnSmem<HD>& sm, int tid) {
   constexpr int KLD = AttnSmem<HD>::KLD, HALF = HD / 2;
@@ -305,160 +325,11 @@ __device__ __forceinline__ void make_q(const AttnArgs& a, const QRaw<HD>& r, int
   }
 }
 
-template <int HD, bool KF32, bool ROPE>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) AttnSmem<HD> sm;
-  constexpr int KLD = AttnSmem<HD>::KLD;
-  constexpr int NKS = (HD + 31) / 32;  // k-steps of 32 dims
-  constexpr int NDT = HD / 16;         // output d tiles
-
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = lane >> 4, r16 = lane & 15;
-  const int kvh = blockIdx.z, split = blockIdx.y;
-  const int grp = a.H / a.KV;
-  const int row = blockIdx.x * ROWS + 16 * w + r16;   // this lane's query row (B-operand column)
-  const bool row_ok = row < a.rows;
-  const int rowc = min(row, a.rows - 1);
-  const int hl = rowc / a.Tq, t = rowc % a.Tq;
-  const int h = kvh * grp + hl;
-  const int nsp = a.nsplit - (a.Ts > 0 ? 1 : 0);     // prefix splits; the last split is the suffix
-  const bool suffix = split >= nsp;
-  const int kbeg = suffix ? 0 : split * a.kps;
-  const int kend = suffix ? a.Ts : min(a.Sp, kbeg + a.kps);
-  const int nch = (kend - kbeg + KCH - 1) / KCH;
-
-  h8 qh[NKS], ql[NKS];
-  f4 oacc[NDT];
-#pragma unroll
-  for (int i = 0; i < NDT; ++i) oacc[i] = (f4){0.f, 0.f, 0.f, 0.f};
-  float m_run = -1e30f, l_run = 0.f;
-
-  auto body = [&](auto suffix_tag) {
-    constexpr bool SUF = decltype(suffix_tag)::value;
-    using Regs = typename std::conditional<SUF, SufRegs<HD>, ChunkRegs<HD>>::type;
-    Regs regs;
-    auto load = [&](int c0) {
-      if constexpr (SUF) load_suffix<HD, ROPE>(regs, a, kvh, c0, kend, tid);
-      else load_prefix<HD, KF32>(regs, a, kvh, c0, kend, tid);
-    };
-    auto store = [&]() {
-      if constexpr (SUF) {
-        ChunkRegs<HD> k32;
-        rope_suffix<HD, ROPE>(regs, k32, a.ks_roped != 0);
-        store_chunk<HD>(k32, sm, tid);
-      } else {
-        store_chunk<HD>(regs, sm, tid);
-      }
-    };
-    // Q and the first chunk go out as one batch of loads: Q half 0, the chunk, Q half 1
-    QRaw<HD> qa, qb;
-    load_q<HD, ROPE>(a, t, h, g, qa, 0);
-    load(kbeg);
-    if constexpr (QRaw<HD>::NHALF > 1) load_q<HD, ROPE>(a, t, h, g, qb, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    make_q<HD, ROPE>(a, qa, g, qh, ql, 0);
-    if constexpr (QRaw<HD>::NHALF > 1) make_q<HD, ROPE>(a, qb, g, qh, ql, 1);
-    for (int c = 0; c < nch; ++c) {
-      store();
-      __syncthreads();
-      load(kbeg + min(c + 1, nch - 1) * KCH);  // next chunk (the last one again at the end)
-      __builtin_amdgcn_sched_barrier(0);       // keep the prefetch ahead of this chunk's MFMAs
-
-      // ---- logits S^T for the 2 key tiles of 16: 6 independent accumulation chains --
-      f4 acc3[2][3];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc3[kt][j] = (f4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const int d0 = 32 * ks + 8 * g;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          h8 ah = *reinterpret_cast<const h8*>(&sm.kh[(16 * kt + r16) * KLD + d0]);
-          h8 al = *reinterpret_cast<const h8*>(&sm.kl[(16 * kt + r16) * KLD + d0]);
-          if constexpr (HD < 32) {
-            if (d0 >= HD) ah = al = (h8){0, 0, 0, 0, 0, 0, 0, 0};
-          }
-          acc3[kt][0] = mfma16x16x32(al, qh[ks], acc3[kt][0]);
-          acc3[kt][1] = mfma16x16x32(ah, ql[ks], acc3[kt][1]);
-          acc3[kt][2] = mfma16x16x32(ah, qh[ks], acc3[kt][2]);
-        }
-      }
-      // lane holds keys 16kt + 4g + i of row r16
-      float p[8];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          p[4 * kt + i] = (acc3[kt][0][i] + acc3[kt][1][i]) + acc3[kt][2][i] + sm.msk[16 * kt + 4 * g + i];
-      // ---- online softmax over this chunk (row r16: lanes r16, +16, +32, +48) --------
-      float cmax = p[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) cmax = fmaxf(cmax, p[i]);
-      cmax = xor_max_16_32(cmax);
-      const float m_new = fmaxf(m_run, cmax);
-      const float alpha = exp_hw(m_run - m_new);
-      float psum = 0.f;
-      h8 pb;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float e = exp_hw(p[i] - m_new);
-        psum += e;
-        pb[i] = f2h(e);
-      }
-      psum = xor_sum_16_32(psum);
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-
-      // ---- O^T += V^T . P^T (V^T read in the key order of P: 4g..4g+3, 16+4g..16+4g+3) --
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const _Float16* vr = &sm.vt[(16 * dt + r16) * VLD];
-        const h4 v0 = *reinterpret_cast<const h4*>(vr + 4 * g);
-        const h4 v1 = *reinterpret_cast<const h4*>(vr + 16 + 4 * g);
-        const h8 av = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        f4 o = oacc[dt];
-        o[0] *= alpha;
-        o[1] *= alpha;
-        o[2] *= alpha;
-        o[3] *= alpha;
-        oacc[dt] = mfma16x16x32(av, pb, o);
-      }
-      __syncthreads();
-    }
-  };
-  if (suffix) body(std::true_type{});
-  else body(std::false_type{});
-
-  if (!row_ok) return;
-  if (a.nsplit == 1) {
-    const float inv = 1.0f / l_run;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      h4 o4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * inv);
-      const int col = h * HD + 16 * dt + 4 * g;
-      *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
-    }
-  } else {
-    const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
-    float* po = a.part_o + pr * HD;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f4*>(po + 16 * dt + 4 * g) = oacc[dt];
-    if (g == 0) {
-      a.part_ml[pr * 2 + 0] = m_run;
-      a.part_ml[pr * 2 + 1] = l_run;
-    }
-  }
-}
-
-// combine the per-split partial softmax states of one row (one wave per row); every
-// load goes out at once (split indices past nsplit repeat a valid split with weight 0)
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
+// Combine the per-split partial softmax states of one query row with one wave (lane s
+// holds split s's weight); every partial load goes out at once (split indices past
+// nsplit repeat a valid split with weight 0).
+__device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row, int lane) {
   constexpr int MAXS = 32;
-  const int row = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
   const int hd = a.hd;
   const int grp = a.H / a.KV;
   const int hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
@@ -473,7 +344,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll
   for (int s = 0; s < MAXS; ++s)
     o[s] = *reinterpret_cast<const f4*>(a.part_o + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0);
-  // split weights w_s = exp(m_s - max) / sum_s l_s exp(m_s - max), lane s holds split s
+  // split weights w_s = exp(m_s - max) / sum_s l_s exp(m_s - max)
   // (computed by all 64 lanes: the shuffles below need every lane active)
   const float m = lane < ns ? m_l : -INFINITY;
   float mmax = m;
@@ -499,6 +370,273 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
     const int col = h * hd + d;
     *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
   }
+}
+
+// Chunks stream through two LDS buffers with two chunks of loads in flight in registers.
+// IMG: prefix splits copy prebuilt chunk images; otherwise (and for the suffix split)
+// the chunk is converted in registers (hi/lo split, V transposed, suffix RoPE).
+template <int HD, bool KF32, bool ROPE, bool IMG>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  constexpr int IMGB = img_bytes<HD>();
+  constexpr int BUFB = IMG ? IMGB : ((int)sizeof(AttnSmem<HD>) + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(16))) char lds_raw[2 * BUFB];
+  constexpr int KLD = AttnSmem<HD>::KLD;
+  constexpr int NKS = (HD + 31) / 32;  // k-steps of 32 dims
+  constexpr int NDT = HD / 16;         // output d tiles
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int kvh = blockIdx.z, split = blockIdx.y;
+  const int grp = a.H / a.KV;
+  const int row = blockIdx.x * ROWS + 16 * w + r16;   // this lane's query row (B-operand column)
+  const bool row_ok = row < a.rows;
+  const int rowc = min(row, a.rows - 1);
+  const int hl = rowc / a.Tq, t = rowc % a.Tq;
+  const int h = kvh * grp + hl;
+  const int nsp = a.nsplit - (a.Ts > 0 ? 1 : 0);     // prefix splits; the last split is the suffix
+  const bool suffix = split >= nsp;
+  const int kbeg = suffix ? 0 : split * a.kps;
+  const int kend = suffix ? a.Ts : min(a.Sp, kbeg + a.kps);
+  const int nch = (kend - kbeg + KCH - 1) / KCH;
+
+  h8 qh[NKS], ql[NKS];
+  f4 oacc[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) oacc[i] = (f4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -1e30f, l_run = 0.f;
+
+  // logits, online softmax and O^T += V^T . P^T for one chunk resident in LDS
+  auto chunk_math = [&](const AttnSmem<HD>& sk) __attribute__((always_inline)) {
+    // ---- logits S^T for the 2 key tiles of 16: 6 independent accumulation chains --
+    f4 acc3[2][3];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc3[kt][j] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 32 * ks + 8 * g;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        h8 ah = *reinterpret_cast<const h8*>(&sk.kh[(16 * kt + r16) * KLD + d0]);
+        h8 al = *reinterpret_cast<const h8*>(&sk.kl[(16 * kt + r16) * KLD + d0]);
+        if constexpr (HD < 32) {
+          if (d0 >= HD) ah = al = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        acc3[kt][0] = mfma16x16x32(al, qh[ks], acc3[kt][0]);
+        acc3[kt][1] = mfma16x16x32(ah, ql[ks], acc3[kt][1]);
+        acc3[kt][2] = mfma16x16x32(ah, qh[ks], acc3[kt][2]);
+      }
+    }
+    // lane holds keys 16kt + 4g + i of row r16
+    float p[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        p[4 * kt + i] = (acc3[kt][0][i] + acc3[kt][1][i]) + acc3[kt][2][i] + sk.msk[16 * kt + 4 * g + i];
+    // ---- online softmax over this chunk (row r16: lanes r16, +16, +32, +48) --------
+    float cmax = p[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) cmax = fmaxf(cmax, p[i]);
+    cmax = xor_max_16_32(cmax);
+    // lazy running max: it moves only when a chunk's max exceeds it by more than 8, so
+    // p = exp(s - m_run) stays below e^8 (fp16-safe) and most chunks skip the rescale of
+    // the accumulators (the result is the same softmax: m_run, l_run and O agree)
+    const bool grow = cmax > m_run + 8.0f;
+    const float m_new = grow ? cmax : m_run;
+    const float alpha = exp_hw(m_run - m_new);
+    const bool rescale = __any(grow);
+    float psum = 0.f;
+    h8 pb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float e = exp_hw(p[i] - m_new);
+      psum += e;
+      pb[i] = f2h(e);
+    }
+    psum = xor_sum_16_32(psum);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+
+    if (rescale) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+    }
+    // ---- O^T += V^T . P^T (V^T read in the key order of P: 4g..4g+3, 16+4g..16+4g+3) --
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const _Float16* vr = &sk.vt[(16 * dt + r16) * VLD];
+      const h4 v0 = *reinterpret_cast<const h4*>(vr + 4 * g);
+      const h4 v1 = *reinterpret_cast<const h4*>(vr + 16 + 4 * g);
+      const h8 av = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      oacc[dt] = mfma16x16x32(av, pb, oacc[dt]);
+    }
+  };
+
+  auto buf = [&](int b) -> const AttnSmem<HD>& { return *reinterpret_cast<const AttnSmem<HD>*>(lds_raw + b * BUFB); };
+  auto wbuf = [&](int b) -> AttnSmem<HD>& { return *reinterpret_cast<AttnSmem<HD>*>(lds_raw + b * BUFB); };
+
+  // Chunk c is computed from buffer c & 1.  Register stage R0 / R1 carries chunk c + 2
+  // (loaded two chunks ahead) until buffer c & 1 is free again after chunk c.
+  //   load(c, R): issue the loads of chunk c;  store(R, b): write it into buffer b.
+  auto pipeline = [&](auto& R0, auto& R1, auto&& load, auto&& store) __attribute__((always_inline)) {
+    load(0, R0);
+    if (nch > 1) load(1, R1);
+    QRaw<HD> qa, qb;
+    load_q<HD, ROPE>(a, t, h, g, qa, 0);
+    if constexpr (QRaw<HD>::NHALF > 1) load_q<HD, ROPE>(a, t, h, g, qb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    make_q<HD, ROPE>(a, qa, g, qh, ql, 0);
+    if constexpr (QRaw<HD>::NHALF > 1) make_q<HD, ROPE>(a, qb, g, qh, ql, 1);
+    store(R0, 0);
+    if (nch > 1) store(R1, 1);
+    lds_barrier();
+    if (nch > 2) load(2, R0);
+    if (nch > 3) load(3, R1);
+    for (int c = 0; c < nch; c += 2) {
+      chunk_math(buf(0));
+      lds_barrier();
+      if (c + 2 < nch) {
+        store(R0, 0);
+        if (c + 4 < nch) load(c + 4, R0);
+      }
+      if (c + 1 < nch) {
+        chunk_math(buf(1));
+        lds_barrier();
+        if (c + 3 < nch) {
+          store(R1, 1);
+          if (c + 5 < nch) load(c + 5, R1);
+        }
+      }
+    }
+  };
+  if (suffix) {
+    SufRegs<HD> R0, R1;
+    pipeline(
+        R0, R1, [&](int c, SufRegs<HD>& R) { load_suffix<HD, ROPE>(R, a, kvh, c * KCH, kend, tid); },
+        [&](const SufRegs<HD>& R, int b) {
+          ChunkRegs<HD> k32;
+          rope_suffix<HD, ROPE>(R, k32, a.ks_roped != 0);
+          store_chunk<HD>(k32, wbuf(b), tid);
+        });
+  } else if constexpr (IMG) {
+    constexpr int NI = IMGB / (NT * 16);
+    struct ImgRegs {
+      u4 v[NI];
+    };
+    const char* ib = a.kimg + ((size_t)kvh * a.img_chunks + kbeg / KCH) * IMGB;
+    ImgRegs R0, R1;
+    pipeline(
+        R0, R1,
+        [&](int c, ImgRegs& R) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+            R.v[i] = load_global(reinterpret_cast<const u4*>(ib + (size_t)c * IMGB + (size_t)(i * NT + tid) * 16));
+        },
+        [&](const ImgRegs& R, int b) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i) *reinterpret_cast<u4*>(lds_raw + b * BUFB + (i * NT + tid) * 16) = R.v[i];
+        });
+  } else {
+    ChunkRegs<HD> R0, R1;
+    pipeline(
+        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_prefix<HD, KF32>(R, a, kvh, kbeg + c * KCH, kend, tid); },
+        [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
+  }
+
+  if (!row_ok) return;
+  if (a.nsplit == 1) {
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      h4 o4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * inv);
+      const int col = h * HD + 16 * dt + 4 * g;
+      *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
+    }
+  } else {
+    const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
+    float* po = a.part_o + pr * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f4*>(po + 16 * dt + 4 * g) = oacc[dt];
+    if (g == 0) {
+      a.part_ml[pr * 2 + 0] = m_run;
+      a.part_ml[pr * 2 + 1] = l_run;
+    }
+  }
+}
+
+// chunk images of the prefix K/V of `layers` layers: grid (chunks, KV, layers)
+template <int HD, bool KF32>
+__global__ __launch_bounds__(256) void attn_img_prep_kernel(const void* __restrict__ keys,
+                                                            const _Float16* __restrict__ values,
+                                                            const float* __restrict__ mask, int Sp, int KV,
+                                                            char* __restrict__ img, size_t layer_bytes) {
+  constexpr int KLD = AttnSmem<HD>::KLD;
+  constexpr int IMGB = img_bytes<HD>();
+  __shared__ __attribute__((aligned(16))) _Float16 sv[KCH * HD];
+  const int c = blockIdx.x, kvh = blockIdx.y, layer = blockIdx.z, tid = threadIdx.x;
+  const int c0 = c * KCH;
+  const size_t kvbase = ((size_t)layer * KV + kvh) * Sp * HD;
+  AttnSmem<HD>* im =
+      reinterpret_cast<AttnSmem<HD>*>(img + layer * layer_bytes + ((size_t)kvh * gridDim.x + c) * IMGB);
+  const h8 zero8 = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+  // K rows split hi/lo (the pad columns past HD and keys past Sp are zero)
+  for (int i = tid; i < KCH * (KLD / 8); i += 256) {
+    const int j = i / (KLD / 8), dq = (i % (KLD / 8)) * 8;
+    h8 hi = zero8, lo = zero8;
+    if (dq < HD && c0 + j < Sp) {
+      float v[8];
+      if constexpr (KF32) {
+        const float* kp = reinterpret_cast<const float*>(keys) + kvbase + (size_t)(c0 + j) * HD + dq;
+        const f4 x = *reinterpret_cast<const f4*>(kp), y = *reinterpret_cast<const f4*>(kp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = x[e];
+          v[e + 4] = y[e];
+        }
+      } else {
+        const h8 x = *reinterpret_cast<const h8*>(reinterpret_cast<const _Float16*>(keys) + kvbase +
+                                                  (size_t)(c0 + j) * HD + dq);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = h2f(x[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        _Float16 hh, ll;
+        split_f32(v[e], hh, ll);
+        hi[e] = hh;
+        lo[e] = ll;
+      }
+    }
+    *reinterpret_cast<h8*>(&im->kh[j * KLD + dq]) = hi;
+    *reinterpret_cast<h8*>(&im->kl[j * KLD + dq]) = lo;
+  }
+  // V: staged in LDS, written transposed vt[d][j] = V[c0 + j][d] (keys past Sp and the
+  // pad slots past 32 are zero)
+  for (int i = tid; i < KCH * HD / 8; i += 256) {
+    const int j = i / (HD / 8), d8 = (i % (HD / 8)) * 8;
+    const h8 v = c0 + j < Sp ? *reinterpret_cast<const h8*>(values + kvbase + (size_t)(c0 + j) * HD + d8) : zero8;
+    *reinterpret_cast<h8*>(&sv[j * HD + d8]) = v;
+  }
+  __syncthreads();
+  for (int i = tid; i < HD * (VLD / 8); i += 256) {
+    const int d = i / (VLD / 8), j8 = (i % (VLD / 8)) * 8;
+    h8 o = zero8;
+    if (j8 < KCH) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = sv[(j8 + e) * HD + d];
+    }
+    *reinterpret_cast<h8*>(&im->vt[d * VLD + j8]) = o;
+  }
+  if (tid < KCH) im->msk[tid] = c0 + tid < Sp ? (mask ? mask[c0 + tid] : 0.f) : -INFINITY;
+}
+
+// combine the per-split partial softmax states, one wave per row
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
+  combine_row(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 // post-RoPE K (fp32) and V (fp16) of one prefill layer into the [KV][P][hd] cache slices
@@ -582,17 +720,21 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.nsplit == 1 || (a.part_o && a.part_ml), "attention workspace missing");
   MLCV_REQUIRE(!a.out_frag || (a.Tq <= 64 && (a.H * a.hd) % 32 == 0), "fragment-major output needs Tq <= 64");
   MLCV_REQUIRE(a.nsplit <= 32, "at most 32 key splits");
+  MLCV_REQUIRE(!a.kimg || a.img_chunks == (a.Sp + KCH - 1) / KCH, "chunk images do not match the prefix length");
   MLCV_REQUIRE(a.cos == nullptr || a.sin != nullptr, "rope needs cos and sin");
   MLCV_REQUIRE(a.Ts == 0 || a.cos != nullptr || a.ks_roped, "raw suffix keys need the rope tables");
   dim3 grid((a.rows + ROWS - 1) / ROWS, a.nsplit, a.KV);
 #define MLCV_ATTN_CASE(HDV)                                                            \
   case HDV:                                                                            \
-    if (a.kp_f32) {                                                                    \
-      if (a.cos) attn_kernel<HDV, true, true><<<grid, 256, 0, st>>>(a);                \
-      else attn_kernel<HDV, true, false><<<grid, 256, 0, st>>>(a);                     \
+    if (a.kimg) {                                                                      \
+      if (a.cos) attn_kernel<HDV, true, true, true><<<grid, 256, 0, st>>>(a);          \
+      else attn_kernel<HDV, true, false, true><<<grid, 256, 0, st>>>(a);               \
+    } else if (a.kp_f32) {                                                             \
+      if (a.cos) attn_kernel<HDV, true, true, false><<<grid, 256, 0, st>>>(a);         \
+      else attn_kernel<HDV, true, false, false><<<grid, 256, 0, st>>>(a);              \
     } else {                                                                           \
-      if (a.cos) attn_kernel<HDV, false, true><<<grid, 256, 0, st>>>(a);               \
-      else attn_kernel<HDV, false, false><<<grid, 256, 0, st>>>(a);                    \
+      if (a.cos) attn_kernel<HDV, false, true, false><<<grid, 256, 0, st>>>(a);        \
+      else attn_kernel<HDV, false, false, false><<<grid, 256, 0, st>>>(a);             \
     }                                                                                  \
     break;
   switch (a.hd) {
@@ -609,6 +751,43 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
     attn_combine_kernel<<<dim3(a.rows, a.KV), 64, 0, st>>>(a);
     MLCV_HIP(hipGetLastError());
   }
+  return 0;
+}
+
+size_t attn_img_bytes(int KV, int Sp, int hd) {
+  int ib = 0;
+  switch (hd) {
+    case 16: ib = img_bytes<16>(); break;
+    case 32: ib = img_bytes<32>(); break;
+    case 64: ib = img_bytes<64>(); break;
+    case 128: ib = img_bytes<128>(); break;
+    case 256: ib = img_bytes<256>(); break;
+    default: return 0;
+  }
+  return (size_t)KV * ((Sp + KCH - 1) / KCH) * ib;
+}
+
+int attn_img_prep_launch(const void* keys, int k_f32, const _Float16* values, const float* mask, int layers, int KV,
+                         int Sp, int hd, char* img, hipStream_t st) {
+  MLCV_REQUIRE(Sp > 0 && layers > 0 && KV > 0 && img, "chunk image preparation arguments");
+  const size_t lb = attn_img_bytes(KV, Sp, hd);
+  MLCV_REQUIRE(lb > 0, "head_dim must be one of 16, 32, 64, 128, 256");
+  dim3 grid((Sp + KCH - 1) / KCH, KV, layers);
+#define MLCV_PREP_CASE(HDV)                                                                              \
+  case HDV:                                                                                              \
+    if (k_f32) attn_img_prep_kernel<HDV, true><<<grid, 256, 0, st>>>(keys, values, mask, Sp, KV, img, lb);  \
+    else attn_img_prep_kernel<HDV, false><<<grid, 256, 0, st>>>(keys, values, mask, Sp, KV, img, lb);       \
+    break;
+  switch (hd) {
+    MLCV_PREP_CASE(16)
+    MLCV_PREP_CASE(32)
+    MLCV_PREP_CASE(64)
+    MLCV_PREP_CASE(128)
+    MLCV_PREP_CASE(256)
+    default: MLCV_REQUIRE(false, "head_dim must be one of 16, 32, 64, 128, 256");
+  }
+#undef MLCV_PREP_CASE
+  MLCV_HIP(hipGetLastError());
   return 0;
 }
 

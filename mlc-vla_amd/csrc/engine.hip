@@ -142,6 +142,12 @@ struct Ctx {
   unsigned* counters = nullptr;
   size_t ncounters = 0;
   float* attn_ws = nullptr;
+  // prefix K/V chunk images of every layer (built once per call from keys / values)
+  char* kvimg = nullptr;
+  size_t img_layer_bytes = 0;
+  // the enqueued sequence built the images (the loop: one build serves every step); a
+  // single step reads the f32 keys directly (a build would cost about what it saves)
+  bool use_img = false;
   size_t attn_ws_floats_n = 0;
   int st_nsplit = 1, st_kps = 32, pf_nsplit = 1, pf_kps = 32;
 
@@ -283,6 +289,11 @@ int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRM
   return run_op(c, c.layer_ops[4 * L + 0], op, st);
 }
 
+// the chunk images of every layer's prefix K/V (once per call; read by enqueue_attn)
+int enqueue_kv_prep(Ctx& c, const float* keys, const _Float16* values, hipStream_t st) {
+  return attn_img_prep_launch(keys, 1, values, c.mask, c.D, c.KV, c.P, c.HD, c.kvimg, st);
+}
+
 int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipStream_t st) {
   AttnArgs a{};
   a.q = c.q;
@@ -310,6 +321,8 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   a.out_frag = c.frag;
   a.nsplit = c.st_nsplit;
   a.kps = c.st_kps;
+  a.kimg = c.use_img ? c.kvimg + (size_t)L * c.img_layer_bytes : nullptr;
+  a.img_chunks = (c.P + 31) / 32;
   a.rows = c.T * (c.H / c.KV);
   a.rpad = ((a.rows + 63) / 64) * 64;
   a.part_o = c.attn_ws;
@@ -475,6 +488,8 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
 int enqueue_loop(Ctx& c, const float* keys, const _Float16* values, hipStream_t st) {
   const size_t modstep = (size_t)c.NM * 3 * c.W1;
   MLCV_TRY(euler_init_launch(c.x0, c.x32, c.xin16, c.T * c.A, st));
+  MLCV_TRY(enqueue_kv_prep(c, keys, values, st));
+  c.use_img = true;
   if (c.hoist) MLCV_TRY(enqueue_time_mod(c, c.te, c.NS, st, c.fork_mod));
   for (int i = 0; i < c.NS; ++i) {
     if (c.hoist) {
@@ -678,6 +693,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
                                 attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
   ALLOC(c.attn_ws, c.attn_ws_floats_n);
+  c.img_layer_bytes = attn_img_bytes(c.KV, c.P, hd);
+  ALLOC(c.kvimg, (size_t)c.D * c.img_layer_bytes);
 
   // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
   const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
@@ -950,6 +967,7 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
   MLCV_TRY(run_graph(c, c.g_step, {keys, values},
                      [&](hipStream_t s) {
+                       c.use_img = false;
                        MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
                        return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod);
                      },
@@ -1013,7 +1031,10 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
         for (const OpDesc& d : c.mod_ops) MLCV_TRY(run_op(c, d, make_op(c, d, c.cond, c.W1, 1), st));
         break;
       case MLCV_OP_QKV: MLCV_TRY(enqueue_qkv(c, layer, c.mod, st)); break;
-      case MLCV_OP_ATTENTION: MLCV_TRY(enqueue_attn(c, layer, keys, vals, st)); break;
+      case MLCV_OP_ATTENTION:
+        c.use_img = false;
+        MLCV_TRY(enqueue_attn(c, layer, keys, vals, st));
+        break;
       case MLCV_OP_OPROJ: MLCV_TRY(enqueue_oproj(c, layer, c.mod, st)); break;
       case MLCV_OP_GATEUP: MLCV_TRY(enqueue_gateup(c, layer, c.mod, st)); break;
       case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;
@@ -1092,9 +1113,17 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
   attn_plan(a.rows, Sp, Ts, 128, &a.nsplit, &a.kps);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
   const size_t need = attn_ws_floats(KV, a.rows, hd, a.nsplit);
-  MLCV_TRY(scratch_reserve(need, 1));
+  // the production path: prefix chunk images, then the attention over them
+  const size_t img_floats = Sp > 0 ? (attn_img_bytes(KV, Sp, hd) + 3) / 4 : 0;
+  MLCV_TRY(scratch_reserve(need + img_floats + 4, 1));
   a.part_o = g_scratch.ws;
   a.part_ml = g_scratch.ws + (size_t)KV * a.nsplit * a.rpad * hd;
+  if (Sp > 0) {
+    char* img = reinterpret_cast<char*>(g_scratch.ws + ((need + 3) / 4) * 4);
+    MLCV_TRY(attn_img_prep_launch(kp, k_f32, a.vp, mask, 1, KV, Sp, hd, img, st));
+    a.kimg = img;
+    a.img_chunks = (Sp + 31) / 32;
+  }
   return attn_launch(a, st);
 }
 

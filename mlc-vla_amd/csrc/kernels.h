@@ -124,6 +124,8 @@ struct AttnArgs {
   _Float16* out;         // [Tq][out_ld], head h at h*hd
   int out_ld;
   int out_frag;          // out in the fragment-major layout (xf_index, Tq <= 64, K = H*hd)
+  const char* kimg;      // prefix chunk images of this layer [KV][img_chunks] (attn_img_prep_launch), or null
+  int img_chunks;
   float* part_o;         // [KV][nsplit][Rpad][hd]
   float* part_ml;        // [KV][nsplit][Rpad][2]
   int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
@@ -132,6 +134,11 @@ struct AttnArgs {
 // nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
 void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps);
 size_t attn_ws_floats(int KV, int rows, int hd, int nsplit);
+// prefix K (split hi/lo), V (transposed) and mask of `layers` consecutive layers (keys /
+// values [layers][KV][Sp][hd]) as per-chunk LDS images: attn_img_bytes(KV, Sp, hd) bytes per layer
+size_t attn_img_bytes(int KV, int Sp, int hd);
+int attn_img_prep_launch(const void* keys, int k_f32, const _Float16* values, const float* mask, int layers, int KV,
+                         int Sp, int hd, char* img, hipStream_t st);
 int attn_launch(const AttnArgs& a, hipStream_t st);
 
 // prefill helpers

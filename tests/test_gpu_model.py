@@ -95,6 +95,22 @@ def test_denoise_step_kv_vs_oracle(which, tiny, dummy):
     _tol(got, ref)
 
 
+def test_long_horizon_rowmajor_path():
+    """Action horizon 72 (two 64-row blocks): the row-major kernels with the per-element
+    adaRMS prologue instead of the fragment-major path, for one step and the graph loop."""
+    m = Model(dict(TINY_KWARGS, action_horizon=72))
+    pm = make_prefix_mask_np(m.cfg.prefix_len)
+    k, v = _prefill(m, pm)
+    cos, sin = make_rope_np(m.cfg.suffix_len, m.cfg.vlm.head_dim, m.cfg.rope_theta, offset=m.cfg.prefix_len)
+    te = make_time_embs(m.cfg.num_denoise_steps, m.cfg.action_expert.width)[3].astype(np.float16)
+    got = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                         m.params).numpy()
+    k_ref, v_ref = O.prefill(m.p32, m.d, m.prefix, pm, F32)
+    _tol(got, O.denoise_step_kv(m.p32, m.d, k_ref, v_ref, m.x_t, te, cos, sin, pm, F32))
+    graph = m.runner.sample_graph(m.params, m.prefix, noise=m.noise)
+    _tol(graph, O.sample(m.p32, m.d, m.prefix, m.noise, F32, graph=True))
+
+
 def test_m1_vs_m0_joint_forward(tiny):
     """compare_kv: the GPU M1 path against the float64 joint (M0) forward."""
     m = tiny
