@@ -174,6 +174,30 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
   r.msk = c0 + (tid & (KCH - 1)) < kend ? 0.f : -INFINITY;
 }
 
+// suffix keys handed over roped in fp32 ([Ts][ks_ld], the qkv epilogue's output) and the
+// suffix v: the prefix loader's chunk layout with the suffix row strides
+template <int HD>
+__device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
+  constexpr int HALF = HD / 2;
+#pragma unroll
+  for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
+    int j, dp;
+    kitem<HD>(i, tid, j, dp);
+    const float* kr = a.ks32 + (size_t)min(c0 + j, kend - 1) * a.ks_ld + (size_t)kvh * HD + dp;
+    ld8f(kr, r.k[i]);
+    ld8f(kr + HALF, r.k[i] + 8);
+  }
+#pragma unroll
+  for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
+    int jp, d0;
+    vitem<HD>(i, tid, jp, d0);
+    const _Float16* vb = a.vs + (size_t)kvh * HD + d0;
+    r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * a.vs_ld));
+    r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld));
+  }
+  r.msk = c0 + (tid & (KCH - 1)) < kend ? 0.f : -INFINITY;
+}
+
 // rope the suffix keys (unless handed over roped) into the fp32 chunk layout
 template <int HD, bool ROPE>
 __device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>& r, bool roped) {
@@ -375,7 +399,9 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
 // Chunks stream through two LDS buffers with two chunks of loads in flight in registers.
 // IMG: prefix splits copy prebuilt chunk images; otherwise (and for the suffix split)
 // the chunk is converted in registers (hi/lo split, V transposed, suffix RoPE).
-template <int HD, bool KF32, bool ROPE, bool IMG>
+// QF: q arrives roped, scaled and split in fragment order (a.qf) and the suffix k roped in
+// fp32 (a.ks32), both from the qkv epilogue.
+template <int HD, bool KF32, bool ROPE, bool IMG, bool QF>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int IMGB = img_bytes<HD>();
   constexpr int BUFB = IMG ? IMGB : ((int)sizeof(AttnSmem<HD>) + 15) / 16 * 16;
@@ -483,12 +509,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   auto pipeline = [&](auto& R0, auto& R1, auto&& load, auto&& store) __attribute__((always_inline)) {
     load(0, R0);
     if (nch > 1) load(1, R1);
-    QRaw<HD> qa, qb;
-    load_q<HD, ROPE>(a, t, h, g, qa, 0);
-    if constexpr (QRaw<HD>::NHALF > 1) load_q<HD, ROPE>(a, t, h, g, qb, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    make_q<HD, ROPE>(a, qa, g, qh, ql, 0);
-    if constexpr (QRaw<HD>::NHALF > 1) make_q<HD, ROPE>(a, qb, g, qh, ql, 1);
+    if constexpr (QF) {
+      const size_t tile = (size_t)kvh * (a.rpad / 16) + (blockIdx.x * ROWS + 16 * w) / 16;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const _Float16* qb = a.qf + ((tile * NKS + ks) * 2) * 512 + lane * 8;
+        qh[ks] = load_global(reinterpret_cast<const h8*>(qb));
+        ql[ks] = load_global(reinterpret_cast<const h8*>(qb + 512));
+      }
+    } else {
+      QRaw<HD> qa, qb;
+      load_q<HD, ROPE>(a, t, h, g, qa, 0);
+      if constexpr (QRaw<HD>::NHALF > 1) load_q<HD, ROPE>(a, t, h, g, qb, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      make_q<HD, ROPE>(a, qa, g, qh, ql, 0);
+      if constexpr (QRaw<HD>::NHALF > 1) make_q<HD, ROPE>(a, qb, g, qh, ql, 1);
+    }
     store(R0, 0);
     if (nch > 1) store(R1, 1);
     lds_barrier();
@@ -511,7 +547,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       }
     }
   };
-  if (suffix) {
+  if (QF && suffix) {
+    ChunkRegs<HD> R0, R1;
+    pipeline(
+        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_suffix32<HD>(R, a, kvh, c * KCH, kend, tid); },
+        [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
+  } else if (suffix) {
     SufRegs<HD> R0, R1;
     pipeline(
         R0, R1, [&](int c, SufRegs<HD>& R) { load_suffix<HD, ROPE>(R, a, kvh, c * KCH, kend, tid); },
@@ -722,20 +763,25 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.nsplit <= 32, "at most 32 key splits");
   MLCV_REQUIRE(!a.kimg || a.img_chunks == (a.Sp + KCH - 1) / KCH, "chunk images do not match the prefix length");
   MLCV_REQUIRE(a.cos == nullptr || a.sin != nullptr, "rope needs cos and sin");
-  MLCV_REQUIRE(a.Ts == 0 || a.cos != nullptr || a.ks_roped, "raw suffix keys need the rope tables");
+  MLCV_REQUIRE(a.Ts == 0 || a.cos != nullptr || a.ks_roped || a.qf, "raw suffix keys need the rope tables");
+  MLCV_REQUIRE(!a.qf || ((a.Ts == 0 || a.ks32) && a.kp_f32 && a.rpad % 64 == 0),
+               "fragment-order q needs the fp32 suffix keys and an fp32 prefix cache");
   dim3 grid((a.rows + ROWS - 1) / ROWS, a.nsplit, a.KV);
-#define MLCV_ATTN_CASE(HDV)                                                            \
-  case HDV:                                                                            \
-    if (a.kimg) {                                                                      \
-      if (a.cos) attn_kernel<HDV, true, true, true><<<grid, 256, 0, st>>>(a);          \
-      else attn_kernel<HDV, true, false, true><<<grid, 256, 0, st>>>(a);               \
-    } else if (a.kp_f32) {                                                             \
-      if (a.cos) attn_kernel<HDV, true, true, false><<<grid, 256, 0, st>>>(a);         \
-      else attn_kernel<HDV, true, false, false><<<grid, 256, 0, st>>>(a);              \
-    } else {                                                                           \
-      if (a.cos) attn_kernel<HDV, false, true, false><<<grid, 256, 0, st>>>(a);        \
-      else attn_kernel<HDV, false, false, false><<<grid, 256, 0, st>>>(a);             \
-    }                                                                                  \
+#define MLCV_ATTN_CASE(HDV)                                                                 \
+  case HDV:                                                                                 \
+    if (a.qf) {                                                                             \
+      if (a.kimg) attn_kernel<HDV, true, false, true, true><<<grid, 256, 0, st>>>(a);       \
+      else attn_kernel<HDV, true, false, false, true><<<grid, 256, 0, st>>>(a);             \
+    } else if (a.kimg) {                                                                    \
+      if (a.cos) attn_kernel<HDV, true, true, true, false><<<grid, 256, 0, st>>>(a);        \
+      else attn_kernel<HDV, true, false, true, false><<<grid, 256, 0, st>>>(a);             \
+    } else if (a.kp_f32) {                                                                  \
+      if (a.cos) attn_kernel<HDV, true, true, false, false><<<grid, 256, 0, st>>>(a);       \
+      else attn_kernel<HDV, true, false, false, false><<<grid, 256, 0, st>>>(a);            \
+    } else {                                                                                \
+      if (a.cos) attn_kernel<HDV, false, true, false, false><<<grid, 256, 0, st>>>(a);      \
+      else attn_kernel<HDV, false, false, false, false><<<grid, 256, 0, st>>>(a);           \
+    }                                                                                       \
     break;
   switch (a.hd) {
     MLCV_ATTN_CASE(16)

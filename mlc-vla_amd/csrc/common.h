@@ -12,6 +12,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -50,6 +51,15 @@ const char* get_error();
 // then loads each fragment with one fully coalesced instruction.
 __host__ __device__ __forceinline__ size_t xf_index(int m, int k) {
   return ((size_t)((k >> 5) * 4 + (m >> 4)) * 64 + ((((k >> 3) & 3) << 4) | (m & 15))) * 8 + (k & 7);
+}
+
+// Attention query fragments (q roped and scaled, split fp16 hi + lo): the B operand of
+// mfma16x16x32 for (kv head, 16-row tile, k step, hi/lo) is one contiguous 1 KB block,
+// lane 16 g + r holding Q[row 16 tile + r][32 ks + 8 g .. +7]; row = (q head within the kv
+// group) * Tq + token, tiles = rows padded to 64 / 16.
+__host__ __device__ __forceinline__ size_t attn_qf_index(int kvh, int ntiles, int nks, int row, int d, int lo) {
+  return ((((size_t)kvh * ntiles + (row >> 4)) * nks + (d >> 5)) * 2 + lo) * 512 +
+         ((((d >> 3) & 3) << 4) | (row & 15)) * 8 + (d & 7);
 }
 
 // Load through a global-address-space pointer: a pointer the compiler cannot trace to

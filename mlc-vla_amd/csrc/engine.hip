@@ -123,6 +123,11 @@ struct Ctx {
   // shift in row T (written by the producer of x; used when T < 64)
   _Float16* xu = nullptr;
   bool prescaled = false;
+  // fragment-major path: q roped + scaled as fp16 hi/lo in the attention's fragment order
+  // (attn_qf_index, zero outside the written rows) and the suffix k roped in fp32
+  _Float16* qf = nullptr;
+  float* k32 = nullptr;
+  int attn_rpad = 64;
   // fragment-major operands for the layer GEMMs (M < 64, widths % 128 == 0): xu, attn
   // and h are [64][K] in the xf_index layout; the action expert's layer and head weights
   // get pre-shuffled copies at bind time
@@ -286,6 +291,12 @@ int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRM
   const _Float16* m_in = mod_of(c, modp, 2 * L);
   SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.prescaled ? c.xu : c.x16, c.W1, c.T);
   set_norm(c, op, m_in);
+  op.rope_cos = c.cos;
+  op.rope_sin = c.sin;
+  op.rope_scale = 1.0f / std::sqrt((float)c.HD);
+  op.rope_hd = c.HD;
+  op.rope_grp = c.H / c.KV;
+  op.rope_rpad = c.attn_rpad;
   return run_op(c, c.layer_ops[4 * L + 0], op, st);
 }
 
@@ -319,6 +330,10 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   a.out = c.attn;
   a.out_ld = c.H * c.HD;
   a.out_frag = c.frag;
+  if (c.frag) {
+    a.qf = c.qf;
+    a.ks32 = c.k32;
+  }
   a.nsplit = c.st_nsplit;
   a.kps = c.st_kps;
   a.kimg = c.use_img ? c.kvimg + (size_t)L * c.img_layer_bytes : nullptr;
@@ -659,6 +674,10 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   c.prescaled = c.frag;
   c.small_m = c.frag && c.NS <= 16;
   ALLOC(c.xu, (size_t)64 * W1);
+  c.attn_rpad = ((T * (c.H / c.KV) + 63) / 64) * 64;
+  const size_t qf_halfs = (size_t)c.KV * c.attn_rpad * ((hd + 31) / 32) * 64;
+  ALLOC(c.qf, qf_halfs);
+  ALLOC(c.k32, (size_t)T * nkv);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
   ALLOC(c.pxn, P * c.W0);
@@ -746,6 +765,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.counters_side, 0, c.ncounters_side * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.xu, 0, (size_t)64 * W1 * 2) != hipSuccess ||
+      hipMemset(c.qf, 0, qf_halfs * 2) != hipSuccess ||
       hipMemset(c.attn, 0, (size_t)std::max(T, 64) * nq * 2) != hipSuccess ||
       hipMemset(c.h, 0, (size_t)std::max(T, 64) * c.F1 * 2) != hipSuccess ||
       hipMemset(c.zero, 0, 64 * 64 * sizeof(float)) != hipSuccess ||
@@ -848,20 +868,21 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
   }
 
   // fragment-major copies of the action expert's layer and head weights
-  auto frag_copy = [&](const Lin& l, int geglu_F) -> Lin {
+  auto frag_copy = [&](const Lin& l, int geglu_F, int rope_hd = 0) -> Lin {
     if (!c.frag) return l;
     Lin f = l;
     if (c.q4) {
       uint32_t* qwf = nullptr;
       _Float16* qsf = nullptr;
       if (dalloc(&qwf, (size_t)l.N * l.K / 8, c.bind_owned) || dalloc(&qsf, (size_t)l.N * l.K / 32, c.bind_owned) ||
-          wf_shuffle_q4_launch(l.qw, l.qs, qwf, qsf, l.N, l.K, geglu_F, st))
+          wf_shuffle_q4_launch(l.qw, l.qs, qwf, qsf, l.N, l.K, geglu_F, rope_hd, st))
         f.N = -1;
       f.qw = qwf;
       f.qs = qsf;
     } else {
       _Float16* wf = nullptr;
-      if (dalloc(&wf, (size_t)l.N * l.K, c.bind_owned) || wf_shuffle_launch(l.w, wf, l.N, l.K, geglu_F, st)) f.N = -1;
+      if (dalloc(&wf, (size_t)l.N * l.K, c.bind_owned) || wf_shuffle_launch(l.w, wf, l.N, l.K, geglu_F, rope_hd, st))
+        f.N = -1;
       f.w = wf;
     }
     return f;
@@ -874,11 +895,22 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
   for (int L = 0; L < c.D; ++L) {
     Layer& ly = c.layers[L];
     OpDesc* ops = &c.layer_ops[4 * L];
-    const Lin fq = frag_copy(ly.q[1], 0), fk = frag_copy(ly.k[1], 0), fv = frag_copy(ly.v[1], 0);
+    // q and k with their rows paired for RoPE in the store epilogue (q then goes to the
+    // attention's fragment buffer, the suffix k to fp32 rows)
+    const Lin fq = frag_copy(ly.q[1], 0, c.HD), fk = frag_copy(ly.k[1], 0, c.HD), fv = frag_copy(ly.v[1], 0);
     const Lin fo = frag_copy(ly.o[1], 0), fgu = frag_copy(ly.gu[1], c.F1), fdn = frag_copy(ly.dn[1], 0);
     for (const Lin* l : {&fq, &fk, &fv, &fo, &fgu, &fdn}) MLCV_REQUIRE(l->N >= 0, get_error());
-    seg_ops(c, ops[0], {seg_of(fq, c.q, nq, nq), seg_of(fk, c.k, nkv, nkv), seg_of(fv, c.v, nkv, nkv)}, W1,
-            EPI_STORE, c.q4, tile_qkv(c).tr, tile_qkv(c).splits);
+    {
+      SkSeg sq = seg_of(fq, c.q, nq, nq), sk = seg_of(fk, c.k, nkv, nkv);
+      if (c.frag) {
+        sq.out = c.qf;
+        sq.rope = 1;
+        sk.out = c.k32;
+        sk.rope = 2;
+      }
+      seg_ops(c, ops[0], {sq, sk, seg_of(fv, c.v, nkv, nkv)}, W1, EPI_STORE, c.q4, tile_qkv(c).tr,
+              tile_qkv(c).splits);
+    }
     seg_ops(c, ops[1], {seg_of(fo, c.x16, W1, W1)}, nq, EPI_GATED_RES, c.q4, tile_o(c).tr, tile_o(c).splits);
     seg_ops(c, ops[2], {seg_of(fgu, c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, tile_gu(c).tr, tile_gu(c).splits);
     seg_ops(c, ops[3], {seg_of(fdn, c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, tile_down(c).tr, tile_down(c).splits);

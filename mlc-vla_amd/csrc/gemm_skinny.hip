@@ -215,6 +215,20 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int i = 0; i < NOWN; ++i)
       x32o[i] = *reinterpret_cast<const f4*>(op.x32 + (size_t)min(m0 + 16 * (kg + i * KG) + r16, mlast) * ldo + ncl);
   }
+  // RoPE segments: this lane's two dims d, d + 1 of the first half (rows paired (d, d + hd/2)
+  // in the slab; after the lane ^ 32 exchange, lanes g < 2 take i = 0, 1 and g >= 2 i = 2, 3)
+  f4 rcs = (f4){0.f, 0.f, 0.f, 0.f};  // cos d, cos d+1, sin d, sin d+1 of this lane's token
+  int rope_d = 0;
+  if constexpr (EPI == EPI_STORE && XM == 1) {
+    if (seg.rope) {
+      const int spb = op.rope_hd / 16;
+      rope_d = 8 * (lt % spb) + 4 * (g & 1) + (g < 2 ? 0 : 2);
+      const size_t tr0 = (size_t)min(m0 + 16 * kg + r16, mlast) * (op.rope_hd / 2) + rope_d;
+      const f2 cc = load_global(reinterpret_cast<const f2*>(op.rope_cos + tr0));
+      const f2 ss = load_global(reinterpret_cast<const f2*>(op.rope_sin + tr0));
+      rcs = (f4){cc[0], cc[1], ss[0], ss[1]};
+    }
+  }
   // next adaRMS operands for the pre-scaled copy of x (STORE / GATED_RES producers)
   h4 xus = (h4){0, 0, 0, 0}, xush = xus;
   if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
@@ -503,6 +517,57 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     return;
   }
 
+  if constexpr (EPI == EPI_STORE && XM == 1) {
+    if (seg.rope) {
+      // the projection rounds to fp16 (the reference's q / k), RoPE in fp32 on those values
+      static_assert(NOWN == 1, "RoPE epilogue: one owned m tile per wave");
+      const bool lo = g < 2;
+      const int HD = op.rope_hd, HALF = HD / 2;
+      const int hh = lt / (HD / 16);  // head of this slab
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        _Float16 t = f2h(own[0][e]);
+        if (has_bias) t = hadd(t, bq[e]);
+        y[e] = h2f(t);
+      }
+      const float r0 = __shfl_xor(lo ? y[2] : y[0], 32);
+      const float r1 = __shfl_xor(lo ? y[3] : y[1], 32);
+      const float x1a = lo ? y[0] : r0, x1b = lo ? y[1] : r1;
+      const float x2a = lo ? r0 : y[2], x2b = lo ? r1 : y[3];
+      const float o1a = x1a * rcs[0] - x2a * rcs[2], o1b = x1b * rcs[1] - x2b * rcs[3];
+      const float o2a = x2a * rcs[0] + x1a * rcs[2], o2b = x2b * rcs[1] + x1b * rcs[3];
+      const int m = m0 + 16 * kg + r16;
+      if (m < op.M) {
+        if (seg.rope == 1) {
+          const int kvh = hh / op.rope_grp, row = (hh % op.rope_grp) * op.M + m;
+          const int ntiles = op.rope_rpad / 16, nks = (HD + 31) / 32;
+          _Float16* qf = reinterpret_cast<_Float16*>(seg.out);
+          const float o[2][2] = {{o1a, o1b}, {o2a, o2b}};
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            h2 hi, lo2;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              _Float16 hv, lv;
+              split_f32(o[hf][e] * op.rope_scale, hv, lv);
+              hi[e] = hv;
+              lo2[e] = lv;
+            }
+            const int d = rope_d + hf * HALF;
+            *reinterpret_cast<h2*>(qf + attn_qf_index(kvh, ntiles, nks, row, d, 0)) = hi;
+            *reinterpret_cast<h2*>(qf + attn_qf_index(kvh, ntiles, nks, row, d, 1)) = lo2;
+          }
+        } else {
+          float* kr = reinterpret_cast<float*>(seg.out) + (size_t)m * ldo + (size_t)hh * HD + rope_d;
+          *reinterpret_cast<f2*>(kr) = (f2){o1a, o1b};
+          *reinterpret_cast<f2*>(kr + HALF) = (f2){o2a, o2b};
+        }
+      }
+      return;
+    }
+  }
+
   float ss[NOWN];  // row sums of squares of the stored x over this lane's 4 columns
 #pragma unroll
   for (int i = 0; i < NOWN; ++i) {
@@ -629,32 +694,37 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ qw, const _Float1
 }
 
 // fragment-major weight copies (layout in kernels.h): one thread per 16-byte piece
-__device__ __forceinline__ int wf_row(int s, int r, int geglu_F) {
-  return geglu_F > 0 ? (r < 8 ? 8 * s + r : geglu_F + 8 * s + r - 8) : 16 * s + r;
+__device__ __forceinline__ int wf_row(int s, int r, int geglu_F, int rope_hd) {
+  if (geglu_F > 0) return r < 8 ? 8 * s + r : geglu_F + 8 * s + r - 8;
+  if (rope_hd > 0) {
+    const int spb = rope_hd / 16, h = s / spb, j = s % spb;
+    return h * rope_hd + (r < 8 ? 8 * j + r : rope_hd / 2 + 8 * j + r - 8);
+  }
+  return 16 * s + r;
 }
 
 __global__ void wf_shuffle_kernel(const _Float16* __restrict__ w, _Float16* __restrict__ wf, int nslabs, int K,
-                                  int geglu_F) {
+                                  int geglu_F, int rope_hd) {
   const int KS = K / 32;
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long)nslabs * KS * 64) return;
   const int lane = (int)(i % 64);
   const long blk = i / 64;
   const int ks = (int)(blk % KS), s = (int)(blk / KS);
-  const int row = wf_row(s, lane & 15, geglu_F);
+  const int row = wf_row(s, lane & 15, geglu_F, rope_hd);
   *reinterpret_cast<h8*>(wf + i * 8) = *reinterpret_cast<const h8*>(w + (size_t)row * K + 32 * ks + 8 * (lane >> 4));
 }
 
 __global__ void wf_shuffle_q4_kernel(const uint32_t* __restrict__ qw, const _Float16* __restrict__ qs,
                                      uint32_t* __restrict__ qwf, _Float16* __restrict__ qsf, int nslabs, int K,
-                                     int geglu_F) {
+                                     int geglu_F, int rope_hd) {
   const int KCN = K / 128;
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long)nslabs * KCN * 64) return;
   const int lane = (int)(i % 64), g = lane >> 4;
   const long blk = i / 64;
   const int c = (int)(blk % KCN), s = (int)(blk / KCN);
-  const int row = wf_row(s, lane & 15, geglu_F);
+  const int row = wf_row(s, lane & 15, geglu_F, rope_hd);
   *reinterpret_cast<u4*>(qwf + i * 4) = *reinterpret_cast<const u4*>(qw + (size_t)row * (K / 8) + 16 * c + 4 * g);
   qsf[i] = qs[(size_t)row * (K / 32) + 4 * c + g];
 }
@@ -802,6 +872,11 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   MLCV_REQUIRE(!op.frag || (op.M < MB && op.K % 128 == 0 && op.nseg <= 3),
                "fragment-major operands need M < 64, K % 128 == 0 and at most 3 segments");
   MLCV_REQUIRE(!op.frag_out || op.M < MB, "fragment-major outputs need M < 64");
+  for (int i = 0; i < op.nseg && i < 3; ++i)
+    MLCV_REQUIRE(op.inl[i].rope == 0 || (op.frag && op.tr == 16 && op.epi == EPI_STORE && op.rope_cos &&
+                                         op.rope_sin && op.rope_hd >= 16 && op.rope_hd % 16 == 0 &&
+                                         op.rope_grp >= 1 && op.rope_rpad % 64 == 0),
+                 "RoPE epilogue needs fragment-major 16-row store tiles and its tables");
   if (!direct && nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS)
   if (q4) MLCV_TRY(launch_q<true>(op, norm, nc, grid, st));
   else MLCV_TRY(launch_q<false>(op, norm, nc, grid, st));
@@ -809,25 +884,27 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   return 0;
 }
 
-int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, hipStream_t st) {
+int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, int rope_hd, hipStream_t st) {
   MLCV_REQUIRE(K % 128 == 0, "fragment-major weights need K % 128 == 0");
   MLCV_REQUIRE(geglu_F > 0 ? (N == 2 * geglu_F && geglu_F % 8 == 0) : N % 16 == 0,
                "fragment-major weights need 16-row slabs (GeGLU: F % 8 == 0)");
+  MLCV_REQUIRE(rope_hd <= 0 || (geglu_F <= 0 && rope_hd % 16 == 0 && N % rope_hd == 0), "RoPE pairing shape");
   const int nslabs = geglu_F > 0 ? geglu_F / 8 : N / 16;
   const long n = (long)nslabs * (K / 32) * 64;
-  wf_shuffle_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(w, wf, nslabs, K, geglu_F);
+  wf_shuffle_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(w, wf, nslabs, K, geglu_F, rope_hd);
   MLCV_HIP(hipGetLastError());
   return 0;
 }
 
 int wf_shuffle_q4_launch(const uint32_t* qw, const _Float16* qs, uint32_t* qwf, _Float16* qsf, int N, int K,
-                         int geglu_F, hipStream_t st) {
+                         int geglu_F, int rope_hd, hipStream_t st) {
   MLCV_REQUIRE(K % 128 == 0, "fragment-major weights need K % 128 == 0");
   MLCV_REQUIRE(geglu_F > 0 ? (N == 2 * geglu_F && geglu_F % 8 == 0) : N % 16 == 0,
                "fragment-major weights need 16-row slabs (GeGLU: F % 8 == 0)");
+  MLCV_REQUIRE(rope_hd <= 0 || (geglu_F <= 0 && rope_hd % 16 == 0 && N % rope_hd == 0), "RoPE pairing shape");
   const int nslabs = geglu_F > 0 ? geglu_F / 8 : N / 16;
   const long n = (long)nslabs * (K / 128) * 64;
-  wf_shuffle_q4_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(qw, qs, qwf, qsf, nslabs, K, geglu_F);
+  wf_shuffle_q4_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(qw, qs, qwf, qsf, nslabs, K, geglu_F, rope_hd);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

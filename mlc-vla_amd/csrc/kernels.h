@@ -28,7 +28,10 @@ struct SkSeg {
   int n;                 // output rows of this segment
   int tile0;             // first tile id of this segment
   int ldo;               // output stride between m rows (elements)
-  int m_stride_out;      // unused, reserved
+  // RoPE in the store epilogue (fragment-major 16-row tiles whose weight rows are paired
+  // (d, d + hd/2), see wf_shuffle_launch): 1 = q, written scaled as fp16 hi/lo in the
+  // attention's B-fragment order (attn_qf_index); 2 = k, written as fp32 [m][ldo]
+  int rope;
 };
 
 struct SkOp {
@@ -62,6 +65,12 @@ struct SkOp {
   // row-major X with M <= 16 and fragment-major weights (16-row tiles, no prologue):
   // the small-M time MLP and modulation GEMVs
   bool xrow;
+  // RoPE segments (SkSeg::rope): tables [M][hd/2] fp32, q scale, head dim, q heads per
+  // kv head and the attention's padded rows per kv head
+  const float* rope_cos;
+  const float* rope_sin;
+  float rope_scale;
+  int rope_hd, rope_grp, rope_rpad;
   int epi;
   const _Float16* gate;  // [N] (EPI_GATED_RES)
   int geglu_F;           // EPI_GEGLU: rows [0,F) gate, [F,2F) up
@@ -90,11 +99,12 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st);
 // fragment-major copies of the weights of 16-row slabs for the 16-row skinny tiles:
 // fp16 block (slab s, k step ks) = 1 KB, lane 16 g + r holding W[row(s, r)][32 ks + 8 g ..
 // +7]; q4 block (s, 128-k chunk c) = 1 KB of words, lane 16 g + r holding the 4 words of
-// row(s, r) for k = 128 c + 32 g .. +31, and 64 scales in lane order.  row(s, r) = 16 s + r,
-// or with geglu_F > 0 gate row 8 s + r (r < 8) and up row F + 8 s + r - 8.
-int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, hipStream_t st);
+// row(s, r) for k = 128 c + 32 g .. +31, and 64 scales in lane order.  row(s, r) = 16 s + r;
+// with geglu_F > 0 gate row 8 s + r (r < 8) and up row F + 8 s + r - 8; with rope_hd > 0
+// (heads of rope_hd rows, slab j of head h) h hd + 8 j + r (r < 8) and h hd + hd/2 + 8 j + r - 8.
+int wf_shuffle_launch(const _Float16* w, _Float16* wf, int N, int K, int geglu_F, int rope_hd, hipStream_t st);
 int wf_shuffle_q4_launch(const uint32_t* qw, const _Float16* qs, uint32_t* qwf, _Float16* qsf, int N, int K,
-                         int geglu_F, hipStream_t st);
+                         int geglu_F, int rope_hd, hipStream_t st);
 
 // q4f16_1 helpers
 int q4_quantize_launch(const _Float16* w, uint32_t* qw, _Float16* qs, int N, int K, hipStream_t st);
@@ -105,6 +115,8 @@ int q4_dequant_launch(const uint32_t* qw, const _Float16* qs, _Float16* out, int
 // ---------------------------------------------------------------------------
 struct AttnArgs {
   const _Float16* q;     // raw q [Tq][q_ld], head h at h*hd
+  const _Float16* qf;    // or: q roped and scaled, fp16 hi/lo in B-fragment order (attn_qf_index)
+  const float* ks32;     // with qf: suffix k roped, fp32 [Ts][ks_ld]
   int q_ld;
   const float* cos;      // [Tq][hd/2] rope for q (and suffix k); null = already roped
   const float* sin;
