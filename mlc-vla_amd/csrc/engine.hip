@@ -51,9 +51,10 @@ struct OpDesc {
 struct Tiling {
   int tr, splits;
 };
-Tiling TILE_QKV = {16, 1}, TILE_O = {16, 4}, TILE_GU = {16, 1}, TILE_DOWN = {16, 8};
+Tiling TILE_QKV = {16, 1}, TILE_O = {16, 2}, TILE_GU = {16, 1}, TILE_DOWN = {16, 4};
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
+constexpr int ATTN_TARGET = 128;  // workgroups of the step's attention (row blocks x key splits)
 constexpr int MOD_SPLITS = 1;   // modulation pieces (16-row tiles: 384 workgroups each)
 constexpr int TMLP_SPLITS = 2;  // time MLP (16-row tiles: 128 workgroups)
 
@@ -707,7 +708,9 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   }
   // attention split plans and workspace
   const int st_rows = T * (c.H / c.KV), pf_rows = c.P * (c.H / c.KV);
-  attn_plan(st_rows, c.P, T, 128, &c.st_nsplit, &c.st_kps);
+  // the step's attention: about ATTN_TARGET workgroups (MLCV_ATTN_TARGET overrides, tuning)
+  const int attn_target = std::getenv("MLCV_ATTN_TARGET") ? std::atoi(std::getenv("MLCV_ATTN_TARGET")) : ATTN_TARGET;
+  attn_plan(st_rows, c.P, T, attn_target > 0 ? attn_target : ATTN_TARGET, &c.st_nsplit, &c.st_kps);
   attn_plan(pf_rows, c.P, 0, 256, &c.pf_nsplit, &c.pf_kps);
   c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
                                 attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
