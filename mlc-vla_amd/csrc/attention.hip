@@ -439,16 +439,27 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int j = 0; j < 3; ++j) acc3[kt][j] = (f4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
+    // K fragments of k step ks + 1 are read from LDS while step ks multiplies
+    h8 kf[2][2][2];  // [buffer][key tile][hi, lo]
+    auto ldk = [&](int ks, int b) __attribute__((always_inline)) {
       const int d0 = 32 * ks + 8 * g;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        h8 ah = *reinterpret_cast<const h8*>(&sk.kh[(16 * kt + r16) * KLD + d0]);
-        h8 al = *reinterpret_cast<const h8*>(&sk.kl[(16 * kt + r16) * KLD + d0]);
+        kf[b][kt][0] = *reinterpret_cast<const h8*>(&sk.kh[(16 * kt + r16) * KLD + d0]);
+        kf[b][kt][1] = *reinterpret_cast<const h8*>(&sk.kl[(16 * kt + r16) * KLD + d0]);
         if constexpr (HD < 32) {
-          if (d0 >= HD) ah = al = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+          if (d0 >= HD) kf[b][kt][0] = kf[b][kt][1] = (h8){0, 0, 0, 0, 0, 0, 0, 0};
         }
+      }
+    };
+    ldk(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (ks + 1 < NKS) ldk(ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead (the scheduler would sink them)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const h8 ah = kf[ks & 1][kt][0], al = kf[ks & 1][kt][1];
         acc3[kt][0] = mfma16x16x32(al, qh[ks], acc3[kt][0]);
         acc3[kt][1] = mfma16x16x32(ah, ql[ks], acc3[kt][1]);
         acc3[kt][2] = mfma16x16x32(ah, qh[ks], acc3[kt][2]);
@@ -490,11 +501,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
     }
     // ---- O^T += V^T . P^T (V^T read in the key order of P: 4g..4g+3, 16+4g..16+4g+3) --
+    // V^T fragments read two d tiles ahead of their MFMA
+    h4 vf[3][2];
+    auto ldv = [&](int dt, int b) __attribute__((always_inline)) {
+      const _Float16* vr = &sk.vt[(16 * dt + r16) * VLD];
+      vf[b][0] = *reinterpret_cast<const h4*>(vr + 4 * g);
+      vf[b][1] = *reinterpret_cast<const h4*>(vr + 16 + 4 * g);
+    };
+    ldv(0, 0);
+    if (NDT > 1) ldv(1, 1);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      const _Float16* vr = &sk.vt[(16 * dt + r16) * VLD];
-      const h4 v0 = *reinterpret_cast<const h4*>(vr + 4 * g);
-      const h4 v1 = *reinterpret_cast<const h4*>(vr + 16 + 4 * g);
+      if (dt + 2 < NDT) ldv(dt + 2, (dt + 2) % 3);
+      __builtin_amdgcn_sched_barrier(0);
+      const h4 v0 = vf[dt % 3][0], v1 = vf[dt % 3][1];
       const h8 av = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
       oacc[dt] = mfma16x16x32(av, pb, oacc[dt]);
     }

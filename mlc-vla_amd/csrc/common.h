@@ -102,16 +102,31 @@ __device__ __forceinline__ float gelu_tanh_hw(float x) {
 }
 __device__ __forceinline__ float silu_hw(float x) { return x * __builtin_amdgcn_rcpf(1.0f + exp_hw(-x)); }
 
-// wave-level reductions over lanes l, l^16, l^32 (the 4 row groups of a 16x16 MFMA tile)
+// wave-level reductions over lanes l, l^16, l^32 (the 4 row groups of a 16x16 MFMA tile),
+// on the gfx950 row-swap instructions instead of the LDS crossbar: swapping two copies of
+// v pairs every lane with its xor-16 (xor-32) partner, so max / sum of the two results is
+// the reduction step in every lane
 __device__ __forceinline__ float xor_max_16_32(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const unsigned b = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const unsigned c = __float_as_uint(v);
+  const auto s = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 __device__ __forceinline__ float xor_sum_16_32(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const unsigned b = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const unsigned c = __float_as_uint(v);
+  const auto s = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+// lanes l < 32 receive hi_src of lane l + 32, lanes l >= 32 lo_src of lane l - 32 (the
+// xor-32 exchange where the two halves send different values), one row-swap instruction
+__device__ __forceinline__ float swap_halves(float lo_src, float hi_src, bool lo_lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(hi_src), __float_as_uint(lo_src), false, false);
+  return __uint_as_float(lo_lane ? r[1] : r[0]);
 }
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);

@@ -501,8 +501,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
     for (int i = 0; i < NOWN; ++i) {
       const int mt = kg + i * KG;
-      const float r0 = __shfl_xor(lo ? own[i][2] : own[i][0], 32);
-      const float r1 = __shfl_xor(lo ? own[i][3] : own[i][1], 32);
+      const float r0 = swap_halves(own[i][2], own[i][0], lo);  // = lane ^ 32's (lo ? [2] : [0])
+      const float r1 = swap_halves(own[i][3], own[i][1], lo);
       const float ga = lo ? own[i][0] : r0, gb = lo ? own[i][1] : r1;
       const float ua = lo ? r0 : own[i][2], ub = lo ? r1 : own[i][3];
       h2 o;
@@ -531,8 +531,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
         if (has_bias) t = hadd(t, bq[e]);
         y[e] = h2f(t);
       }
-      const float r0 = __shfl_xor(lo ? y[2] : y[0], 32);
-      const float r1 = __shfl_xor(lo ? y[3] : y[1], 32);
+      const float r0 = swap_halves(y[2], y[0], lo);
+      const float r1 = swap_halves(y[3], y[1], lo);
       const float x1a = lo ? y[0] : r0, x1b = lo ? y[1] : r1;
       const float x2a = lo ? r0 : y[2], x2b = lo ? r1 : y[3];
       const float o1a = x1a * rcs[0] - x2a * rcs[2], o1b = x1b * rcs[1] - x2b * rcs[3];
@@ -632,8 +632,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
       for (int i = 0; i < NOWN; ++i) {
         float v = ss[i];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
+        v = xor_sum_16_32(v);
         const int mt = kg + i * KG;
         if (g == 0 && 16 * mt + r16 < mrows)
           op.rowss_out[(size_t)(m0 + 16 * mt + r16) * op.rowss_ld + grp] = v;
