@@ -349,11 +349,12 @@ __device__ __forceinline__ void make_q(const AttnArgs& a, const QRaw<HD>& r, int
   }
 }
 
-// Combine the per-split partial softmax states of one query row with one wave (lane s
-// holds split s's weight); every partial load goes out at once (split indices past
-// nsplit repeat a valid split with weight 0).
+// Combine the per-split partial softmax states of one query row with one wave: every
+// partial load goes out at once (split indices past nsplit repeat a valid split with
+// weight 0); the split statistics are read lane by lane into uniform registers
+// (v_readlane), so the weights need no cross-lane LDS traffic.
+template <int MAXS>
 __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row, int lane) {
-  constexpr int MAXS = 32;
   const int hd = a.hd;
   const int grp = a.H / a.KV;
   const int hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
@@ -368,17 +369,22 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
 #pragma unroll
   for (int s = 0; s < MAXS; ++s)
     o[s] = *reinterpret_cast<const f4*>(a.part_o + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0);
-  // split weights w_s = exp(m_s - max) / sum_s l_s exp(m_s - max)
-  // (computed by all 64 lanes: the shuffles below need every lane active)
-  const float m = lane < ns ? m_l : -INFINITY;
-  float mmax = m;
-  for (int off = 32; off > 0; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
-  const float e = lane < ns ? exp_hw(m - mmax) : 0.f;
-  const float lsum = wave_sum(l_l * e);
-  const float wgt = e / lsum;
-  float wv[MAXS];
+  // w_s = exp(m_s - max) / sum_s l_s exp(m_s - max)
+  float ms[MAXS], wv[MAXS];
+  float mmax = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < MAXS; ++s) wv[s] = __shfl(wgt, s);
+  for (int s = 0; s < MAXS; ++s) {
+    ms[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), s));
+    if (s < ns) mmax = fmaxf(mmax, ms[s]);
+  }
+  float lsum = 0.f;
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    const float ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), s));
+    wv[s] = s < ns ? exp_hw(ms[s] - mmax) : 0.f;
+    lsum += ls * wv[s];
+  }
+  const float inv = 1.0f / lsum;
   for (int d = lane * 4; d < hd; d += 256) {
     if (d != d0) {  // head dims past 256
 #pragma unroll
@@ -387,7 +393,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
     }
     f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s) acc += wv[s] * o[s];
+    for (int s = 0; s < MAXS; ++s) acc += (wv[s] * inv) * o[s];
     h4 o4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o4[i] = f2h(acc[i]);
@@ -696,8 +702,9 @@ __global__ __launch_bounds__(256) void attn_img_prep_kernel(const void* __restri
 }
 
 // combine the per-split partial softmax states, one wave per row
+template <int MAXS>
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
-  combine_row(a, blockIdx.y, blockIdx.x, threadIdx.x);
+  combine_row<MAXS>(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 // post-RoPE K (fp32) and V (fp16) of one prefill layer into the [KV][P][hd] cache slices
@@ -814,7 +821,11 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
 #undef MLCV_ATTN_CASE
   MLCV_HIP(hipGetLastError());
   if (a.nsplit > 1) {
-    attn_combine_kernel<<<dim3(a.rows, a.KV), 64, 0, st>>>(a);
+    const dim3 cg(a.rows, a.KV);
+    if (a.nsplit <= 8) attn_combine_kernel<8><<<cg, 64, 0, st>>>(a);
+    else if (a.nsplit <= 16) attn_combine_kernel<16><<<cg, 64, 0, st>>>(a);
+    else if (a.nsplit <= 24) attn_combine_kernel<24><<<cg, 64, 0, st>>>(a);
+    else attn_combine_kernel<32><<<cg, 64, 0, st>>>(a);
     MLCV_HIP(hipGetLastError());
   }
   return 0;
