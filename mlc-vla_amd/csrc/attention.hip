@@ -363,13 +363,14 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
   const int sl = min(lane, ns - 1);
   const float m_l = a.part_ml[(pr0 + (size_t)sl * a.rpad) * 2];
   const float l_l = a.part_ml[(pr0 + (size_t)sl * a.rpad) * 2 + 1];
-  // the O loads of the first 256 dims go out with the m / l loads
+  // the O loads of the first 256 dims go out with the m / l loads (partials: fp16 O_s / l_s)
+  const _Float16* po = reinterpret_cast<const _Float16*>(a.part_o);
   const int d0 = min(lane * 4, hd - 4);
-  f4 o[MAXS];
+  h4 o[MAXS];
 #pragma unroll
   for (int s = 0; s < MAXS; ++s)
-    o[s] = *reinterpret_cast<const f4*>(a.part_o + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0);
-  // w_s = exp(m_s - max) / sum_s l_s exp(m_s - max)
+    o[s] = *reinterpret_cast<const h4*>(po + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0);
+  // out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s with w_s = exp(m_s - max)
   float ms[MAXS], wv[MAXS];
   float mmax = -INFINITY;
 #pragma unroll
@@ -381,19 +382,23 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) {
     const float ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), s));
-    wv[s] = s < ns ? exp_hw(ms[s] - mmax) : 0.f;
-    lsum += ls * wv[s];
+    wv[s] = s < ns ? exp_hw(ms[s] - mmax) * ls : 0.f;
+    lsum += wv[s];
   }
   const float inv = 1.0f / lsum;
   for (int d = lane * 4; d < hd; d += 256) {
     if (d != d0) {  // head dims past 256
 #pragma unroll
       for (int s = 0; s < MAXS; ++s)
-        o[s] = *reinterpret_cast<const f4*>(a.part_o + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d);
+        o[s] = *reinterpret_cast<const h4*>(po + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d);
     }
     f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s) acc += (wv[s] * inv) * o[s];
+    for (int s = 0; s < MAXS; ++s) {
+      const float ws = wv[s] * inv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += ws * h2f(o[s][i]);
+    }
     h4 o4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o4[i] = f2h(acc[i]);
@@ -624,10 +629,18 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
     }
   } else {
+    // the split's output normalized by its own softmax sum (a convex combination of V
+    // rows, so fp16 holds it), with (m, l) in fp32 for the combine
     const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
-    float* po = a.part_o + pr * HD;
+    _Float16* po = reinterpret_cast<_Float16*>(a.part_o) + pr * HD;
+    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f4*>(po + 16 * dt + 4 * g) = oacc[dt];
+    for (int dt = 0; dt < NDT; ++dt) {
+      h4 o4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * linv);
+      *reinterpret_cast<h4*>(po + 16 * dt + 4 * g) = o4;
+    }
     if (g == 0) {
       a.part_ml[pr * 2 + 0] = m_run;
       a.part_ml[pr * 2 + 1] = l_run;

@@ -138,7 +138,7 @@ struct AttnArgs {
   int out_frag;          // out in the fragment-major layout (xf_index, Tq <= 64, K = H*hd)
   const char* kimg;      // prefix chunk images of this layer [KV][img_chunks] (attn_img_prep_launch), or null
   int img_chunks;
-  float* part_o;         // [KV][nsplit][Rpad][hd]
+  float* part_o;         // [KV][nsplit][Rpad][hd] fp16 O_s / l_s (the buffer is sized in floats)
   float* part_ml;        // [KV][nsplit][Rpad][2]
   int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
   int rows, rpad;        // rows per kv head (Tq*H/KV) and padded
