@@ -35,8 +35,6 @@ constexpr int ROWS = 64;       // query rows per workgroup (4 waves x 16)
 constexpr int VLD = KCH + 8;   // halfs per V^T row
 constexpr int NT = 256;        // threads per workgroup (4 waves, one 16-row query tile each)
 
-__device__ const float kZeroF = 0.0f;
-
 template <int HD>
 struct AttnSmem {
   static constexpr int KLD = HD + 8;  // halfs per K row
@@ -68,7 +66,8 @@ struct ChunkRegs {
   static constexpr int NV = (VITEMS + NT - 1) / NT;
   float k[NK][16];
   h8 v[NV][2];
-  float msk;
+  float msk;  // the mask value as loaded; keys past the range get -inf when stored (mok)
+  bool mok;
 };
 
 template <int HD>
@@ -126,10 +125,12 @@ __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a,
     r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * HD));
     r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * HD));
   }
+  // a global-space load whose value is untouched until store time: a flat load, or
+  // arithmetic on the loaded value here, would make the compiler wait for every load in
+  // flight (this chunk's and the previous one's) before the loader returns
   const int kj = c0 + (tid & (KCH - 1));
-  const float* mp = a.mask ? a.mask : &kZeroF;
-  const float mv = mp[a.mask ? min(kj, kend - 1) : 0];
-  r.msk = kj < kend ? mv : -INFINITY;
+  r.msk = a.mask ? load_global(a.mask + min(kj, kend - 1)) : 0.f;
+  r.mok = kj < kend;
 }
 
 // Suffix keys [c0, c0+32): the raw fp16 k of the suffix rows and their rope tables stay
@@ -141,6 +142,7 @@ struct SufRegs {
   f4 c[NK][2], s[NK][2];
   h8 v[NV][2];
   float msk;
+  bool mok;
 };
 
 template <int HD, bool ROPE>
@@ -171,7 +173,8 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
     r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * a.vs_ld));
     r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld));
   }
-  r.msk = c0 + (tid & (KCH - 1)) < kend ? 0.f : -INFINITY;
+  r.msk = 0.f;
+  r.mok = c0 + (tid & (KCH - 1)) < kend;
 }
 
 // suffix keys handed over roped in fp32 ([Ts][ks_ld], the qkv epilogue's output) and the
@@ -195,7 +198,8 @@ __device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& 
     r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * a.vs_ld));
     r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld));
   }
-  r.msk = c0 + (tid & (KCH - 1)) < kend ? 0.f : -INFINITY;
+  r.msk = 0.f;
+  r.mok = c0 + (tid & (KCH - 1)) < kend;
 }
 
 // rope the suffix keys (unless handed over roped) into the fp32 chunk layout
@@ -222,6 +226,7 @@ __device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>
     r.v[i][1] = in.v[i][1];
   }
   r.msk = in.msk;
+  r.mok = in.mok;
 }
 
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS accesses, not for
@@ -266,7 +271,7 @@ __device__ __forceinline__ void store_chunk(const ChunkRegs<HD>& r, AttnSmem<HD>
       *reinterpret_cast<h2*>(&sm.vt[(d0 + e) * VLD + 2 * jp]) = pair;
     }
   }
-  if (tid < KCH) sm.msk[tid] = r.msk;
+  if (tid < KCH) sm.msk[tid] = r.mok ? r.msk : -INFINITY;
 }
 
 // Q^T fragments of this lane's row: roped (fp32) unless already roped, scaled, split hi/lo.
@@ -420,6 +425,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int KLD = AttnSmem<HD>::KLD;
   constexpr int NKS = (HD + 31) / 32;  // k-steps of 32 dims
   constexpr int NDT = HD / 16;         // output d tiles
+  if (blockIdx.y >= a.nsplit) {  // prefetch workgroups (grid rows past the key splits)
+    if (blockIdx.z == 0) prefetch_run(a.pf, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * a.nsplit);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
@@ -806,21 +815,29 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.Ts == 0 || a.cos != nullptr || a.ks_roped || a.qf, "raw suffix keys need the rope tables");
   MLCV_REQUIRE(!a.qf || ((a.Ts == 0 || a.ks32) && a.kp_f32 && a.rpad % 64 == 0),
                "fragment-order q needs the fp32 suffix keys and an fp32 prefix cache");
-  dim3 grid((a.rows + ROWS - 1) / ROWS, a.nsplit, a.KV);
+  MLCV_REQUIRE(a.pf.nreg >= 0 && a.pf.nreg <= PF_MAX_REGIONS, "prefetch regions");
+  for (int i = 0; i < a.pf.nreg; ++i)
+    MLCV_REQUIRE(a.pf.r[i].slab_bytes > 0 && a.pf.r[i].slab_bytes % 64 == 0 && a.pf.r[i].nslabs >= 0,
+                 "prefetch slabs must be whole 64-byte lines");
+  const int rb = (a.rows + ROWS - 1) / ROWS;
+  AttnArgs ka = a;
+  const int pf_rows = a.pf.nreg > 0 && a.pf.nblocks > 0 ? (a.pf.nblocks + rb - 1) / rb : 0;
+  ka.pf.nblocks = pf_rows * rb;
+  dim3 grid(rb, a.nsplit + pf_rows, a.KV);
 #define MLCV_ATTN_CASE(HDV)                                                                 \
   case HDV:                                                                                 \
     if (a.qf) {                                                                             \
-      if (a.kimg) attn_kernel<HDV, true, false, true, true><<<grid, 256, 0, st>>>(a);       \
-      else attn_kernel<HDV, true, false, false, true><<<grid, 256, 0, st>>>(a);             \
+      if (a.kimg) attn_kernel<HDV, true, false, true, true><<<grid, 256, 0, st>>>(ka);       \
+      else attn_kernel<HDV, true, false, false, true><<<grid, 256, 0, st>>>(ka);             \
     } else if (a.kimg) {                                                                    \
-      if (a.cos) attn_kernel<HDV, true, true, true, false><<<grid, 256, 0, st>>>(a);        \
-      else attn_kernel<HDV, true, false, true, false><<<grid, 256, 0, st>>>(a);             \
+      if (a.cos) attn_kernel<HDV, true, true, true, false><<<grid, 256, 0, st>>>(ka);        \
+      else attn_kernel<HDV, true, false, true, false><<<grid, 256, 0, st>>>(ka);             \
     } else if (a.kp_f32) {                                                                  \
-      if (a.cos) attn_kernel<HDV, true, true, false, false><<<grid, 256, 0, st>>>(a);       \
-      else attn_kernel<HDV, true, false, false, false><<<grid, 256, 0, st>>>(a);            \
+      if (a.cos) attn_kernel<HDV, true, true, false, false><<<grid, 256, 0, st>>>(ka);       \
+      else attn_kernel<HDV, true, false, false, false><<<grid, 256, 0, st>>>(ka);            \
     } else {                                                                                \
-      if (a.cos) attn_kernel<HDV, false, true, false, false><<<grid, 256, 0, st>>>(a);      \
-      else attn_kernel<HDV, false, false, false, false><<<grid, 256, 0, st>>>(a);           \
+      if (a.cos) attn_kernel<HDV, false, true, false, false><<<grid, 256, 0, st>>>(ka);      \
+      else attn_kernel<HDV, false, false, false, false><<<grid, 256, 0, st>>>(ka);           \
     }                                                                                       \
     break;
   switch (a.hd) {

@@ -57,6 +57,18 @@ constexpr int TR_AIN = 32, SPLIT_AIN = 1;
 constexpr int ATTN_TARGET = 128;  // workgroups of the step's attention (row blocks x key splits)
 constexpr int MOD_SPLITS = 1;   // modulation pieces (16-row tiles: 384 workgroups each)
 constexpr int TMLP_SPLITS = 2;  // time MLP (16-row tiles: 128 workgroups)
+// prefetch assignments (which launch of a layer fetches which later operand into the
+// memory-side cache): the attention runs on half the CUs for the longest span of the layer
+enum : unsigned {
+  PF_QKV_KV = 1,       // q/k/v fetches the layer's prefix K / V
+  PF_ATTN_O = 2,       // attention fetches the o_proj weights
+  PF_ATTN_GU = 4,      // ... the gate_up weights
+  PF_ATTN_DOWN = 8,    // ... the down weights
+  PF_ATTN_QKV = 16,    // ... the next layer's q/k/v weights
+  PF_O_DOWN = 32,      // o_proj fetches the down weights
+  PF_DOWN_QKV = 64,    // down fetches the next layer's q/k/v weights
+};
+constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 
 // MLCV_TILING="qkv=16:S,o=16:S,gu=16:S,down=16:S" overrides the K slices of the
 // fragment-major layer GEMMs for tuning (read at context creation; 0 = planner).
@@ -169,6 +181,10 @@ struct Ctx {
   hipEvent_t cond_ev = nullptr;
   std::vector<hipEvent_t> mod_ev;
   bool fork_mod = false;
+  // prefetch of later ops' operands by spare workgroups of the step's launches
+  // (fragment-major path), PF_* bits: which launch fetches what
+  unsigned prefetch = PF_DEFAULT;
+  int pf_blocks = 64;  // prefetch workgroups per hosting launch (more slow the host, fewer stretch it)
   float* skws_side = nullptr;  // split-K workspace / counters of the side stream
   unsigned* counters_side = nullptr;
   size_t ncounters_side = 0;
@@ -288,9 +304,47 @@ void set_next_norm(const Ctx& c, SkOp& op, const _Float16* m) {
   op.frag_out = c.frag;
 }
 
-int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // adaRMS (input) + q/k/v
+// ---- L2 prefetch descriptors --------------------------------------------------
+void pf_add(Prefetch& pf, const void* base, size_t slab_bytes, int nslabs, int xoff, int every_xcd) {
+  if (pf.nreg >= PF_MAX_REGIONS || nslabs <= 0 || base == nullptr) return;
+  pf.r[pf.nreg++] = PfRegion{static_cast<const char*>(base), (int)slab_bytes, nslabs, xoff & 7, every_xcd};
+}
+// the weight slabs of a fragment-major layer op: one 16-row slab per tile, read by the
+// tile's workgroups on XCD tile % 8
+void pf_weights(const Ctx& c, Prefetch& pf, const OpDesc& d, unsigned bit) {
+  if (!(c.prefetch & bit) || !d.frag) return;
+  pf.nblocks = c.pf_blocks;
+  for (int i = 0; i < d.nseg; ++i) {
+    const SkSeg& sg = c.h_segs[d.seg_off + i];
+    const int tiles = (i + 1 < d.nseg ? c.h_segs[d.seg_off + i + 1].tile0 : d.ntiles) - sg.tile0;
+    if (d.q4) {
+      pf_add(pf, sg.qw, (size_t)8 * d.K, tiles, sg.tile0, 0);  // 16 rows x K/8 words
+      pf_add(pf, sg.qs, (size_t)d.K, tiles, sg.tile0, 0);      // 16 rows x K/32 scales
+    } else {
+      pf_add(pf, sg.w, (size_t)32 * d.K, tiles, sg.tile0, 0);  // 16 rows x K halfs
+    }
+  }
+}
+// the prefix K / V of layer L (or its chunk images), read by the attention on every XCD
+void pf_kv(const Ctx& c, Prefetch& pf, int L, const float* keys, const _Float16* values) {
+  if (!(c.prefetch & PF_QKV_KV) || !c.frag || keys == nullptr) return;
+  pf.nblocks = c.pf_blocks;
+  if (c.use_img) {
+    const int chunks = (c.P + 31) / 32;
+    pf_add(pf, c.kvimg + (size_t)L * c.img_layer_bytes, c.img_layer_bytes / ((size_t)c.KV * chunks), c.KV * chunks,
+           0, 1);
+  } else {
+    const int slabs = (int)(kv_slice(c) / ((size_t)8 * c.HD));  // 8 keys per slab
+    pf_add(pf, keys + L * kv_slice(c), (size_t)8 * c.HD * sizeof(float), slabs, 0, 1);
+    pf_add(pf, values + L * kv_slice(c), (size_t)8 * c.HD * sizeof(_Float16), slabs, 0, 1);
+  }
+}
+
+int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st, const float* keys = nullptr,
+                const _Float16* values = nullptr) {  // adaRMS (input) + q/k/v
   const _Float16* m_in = mod_of(c, modp, 2 * L);
   SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.prescaled ? c.xu : c.x16, c.W1, c.T);
+  pf_kv(c, op.pf, L, keys, values);
   set_norm(c, op, m_in);
   op.rope_cos = c.cos;
   op.rope_sin = c.sin;
@@ -343,6 +397,10 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   a.rpad = ((a.rows + 63) / 64) * 64;
   a.part_o = c.attn_ws;
   a.part_ml = c.attn_ws + (size_t)c.KV * a.nsplit * a.rpad * c.HD;
+  pf_weights(c, a.pf, c.layer_ops[4 * L + 1], PF_ATTN_O);
+  pf_weights(c, a.pf, c.layer_ops[4 * L + 2], PF_ATTN_GU);
+  pf_weights(c, a.pf, c.layer_ops[4 * L + 3], PF_ATTN_DOWN);
+  if (L + 1 < c.D) pf_weights(c, a.pf, c.layer_ops[4 * (L + 1)], PF_ATTN_QKV);
   return attn_launch(a, st);
 }
 
@@ -351,6 +409,7 @@ int enqueue_oproj(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // o_p
   op.gate = mod_of(c, modp, 2 * L) + 2 * c.W1;
   op.rowss_out = c.rowss;
   set_next_norm(c, op, mod_of(c, modp, 2 * L + 1));
+  pf_weights(c, op.pf, c.layer_ops[4 * L + 3], PF_O_DOWN);
   return run_op(c, c.layer_ops[4 * L + 1], op, st);
 }
 
@@ -368,6 +427,7 @@ int enqueue_down(Ctx& c, int L, const _Float16* modp, hipStream_t st) {  // down
   op.gate = mod_of(c, modp, 2 * L + 1) + 2 * c.W1;
   op.rowss_out = c.rowss;
   set_next_norm(c, op, mod_of(c, modp, L + 1 < c.D ? 2 * (L + 1) : 2 * c.D));
+  if (L + 1 < c.D) pf_weights(c, op.pf, c.layer_ops[4 * (L + 1)], PF_DOWN_QKV);
   return run_op(c, c.layer_ops[4 * L + 3], op, st);
 }
 
@@ -394,7 +454,7 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
   set_next_norm(c, ain, mod_of(c, modp, 0));
   MLCV_TRY(run_op(c, c.op_ain, ain, st));
   for (int L = 0; L < c.D; ++L) {
-    MLCV_TRY(enqueue_qkv(c, L, modp, st));
+    MLCV_TRY(enqueue_qkv(c, L, modp, st, keys, values));
     MLCV_TRY(enqueue_attn(c, L, keys, values, st));
     MLCV_TRY(enqueue_oproj(c, L, modp, st));
     MLCV_TRY(enqueue_gateup(c, L, modp, st));
@@ -759,6 +819,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // measured: the forked modulation slows the layer chain more than it hides, so it is
   // off unless MLCV_FORK_MOD=1 (tuning)
   c.fork_mod = std::getenv("MLCV_FORK_MOD") != nullptr && std::atoi(std::getenv("MLCV_FORK_MOD")) != 0;
+  if (const char* e = std::getenv("MLCV_PREFETCH")) c.prefetch = (unsigned)std::strtoul(e, nullptr, 0);
+  if (const char* e = std::getenv("MLCV_PF_BLOCKS")) c.pf_blocks = std::max(8, std::atoi(e));
   bool ev_ok = hipEventCreateWithFlags(&c.cond_ev, hipEventDisableTiming) == hipSuccess;
   for (hipEvent_t& e : c.mod_ev) ev_ok = ev_ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
   if (!ev_ok || hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking) != hipSuccess) {

@@ -163,8 +163,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int slab = w % SLABS, kg = w / SLABS;
+  if (blockIdx.y >= op.splitk) {  // prefetch workgroups (grid rows past the K slices)
+    if (blockIdx.z == 0) prefetch_run(op.pf, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * op.splitk);
+    return;
+  }
   const int tile_id = blockIdx.x, s = blockIdx.y, mb = blockIdx.z;
-  const int S = gridDim.y;
+  const int S = op.splitk;
   const int m0 = mb * MB;
   const int mlast = op.M - 1;
   const int mrows = min(MB, op.M - m0);
@@ -263,26 +267,13 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   const int kk = (tid % TPR) * 8, mr = tid / TPR;
   auto round_direct = [&](const int kr) __attribute__((always_inline)) {
     // fragment-major operands: every load below is one contiguous 1 KB per wave (q4 X:
-    // four 256 B runs).  Weights first (HBM), then this wave's X fragments (L2): chunk c,
-    // k step j, m tile mt holds X[16 mt + r16][kc + ko .. +7], the B operand of
-    // mfma16x16x32 in the k order of the weight fragments (q4: the dequantized nibble
-    // order, so the X fragment is permuted after the load).
+    // four 256 B runs).  This wave's X fragments (L2) first, then the weights (HBM / MALL):
+    // a wave's loads return in issue order, so X issued behind the weights would wait for
+    // the weights' memory latency before streaming in.  Chunk c, k step j, m tile mt
+    // holds X[16 mt + r16][kc + ko .. +7], the B operand of mfma16x16x32 in the k order
+    // of the weight fragments (q4: the dequantized nibble order, so the X fragment is
+    // permuted after the load).
     const int KS = K >> 5, KCN = K >> 7;
-    WRaw<Q4> wr[CPW];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int kcs = kr + (kg * CPW + c) * KC;
-      if constexpr (!Q4) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wr[c].v[j] = load_global(reinterpret_cast<const h8*>(
-              seg.w + (((size_t)lt * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
-      } else {
-        const size_t blk = ((size_t)lt * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
-        wr[c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
-        wr[c].s = load_global(seg.qs + blk);
-      }
-    }
     h8 xf[CPW][4][XMT];
 #pragma unroll
     for (int c = 0; c < CPW; ++c)
@@ -300,6 +291,21 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
           xf[c][j][0] = load_global(reinterpret_cast<const h8*>(op.x + (size_t)min(r16, mlast) * op.ldx + kx));
         }
       }
+    WRaw<Q4> wr[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int kcs = kr + (kg * CPW + c) * KC;
+      if constexpr (!Q4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wr[c].v[j] = load_global(reinterpret_cast<const h8*>(
+              seg.w + (((size_t)lt * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
+      } else {
+        const size_t blk = ((size_t)lt * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
+        wr[c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
+        wr[c].s = load_global(seg.qs + blk);
+      }
+    }
     // every load of the round in flight before the first MFMA (the scheduler would
     // otherwise interleave them and keep only a few outstanding)
     __builtin_amdgcn_sched_barrier(0);
@@ -877,8 +883,16 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
                                          op.rope_grp >= 1 && op.rope_rpad % 64 == 0),
                  "RoPE epilogue needs fragment-major 16-row store tiles and its tables");
   if (!direct && nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS)
-  if (q4) MLCV_TRY(launch_q<true>(op, norm, nc, grid, st));
-  else MLCV_TRY(launch_q<false>(op, norm, nc, grid, st));
+  MLCV_REQUIRE(op.pf.nreg >= 0 && op.pf.nreg <= PF_MAX_REGIONS, "prefetch regions");
+  for (int i = 0; i < op.pf.nreg; ++i)
+    MLCV_REQUIRE(op.pf.r[i].slab_bytes > 0 && op.pf.r[i].slab_bytes % 64 == 0 && op.pf.r[i].nslabs >= 0,
+                 "prefetch slabs must be whole 64-byte lines");
+  SkOp kop = op;
+  const int pf_rows = op.pf.nreg > 0 && op.pf.nblocks > 0 ? (op.pf.nblocks + op.ntiles - 1) / op.ntiles : 0;
+  kop.pf.nblocks = pf_rows * op.ntiles;
+  grid.y += pf_rows;
+  if (q4) MLCV_TRY(launch_q<true>(kop, norm, nc, grid, st));
+  else MLCV_TRY(launch_q<false>(kop, norm, nc, grid, st));
   MLCV_HIP(hipGetLastError());
   return 0;
 }

@@ -6,6 +6,64 @@
 namespace mlcv {
 
 // ---------------------------------------------------------------------------
+// L2 prefetch by spare workgroups.  A launch can append `nblocks` workgroups that only
+// read the regions a later kernel of the sequence will read, so that the later kernel
+// finds them in the L2 of the XCD its workgroups run on (workgroups are dealt to the 8
+// XCDs round-robin by linear id, and a consumer tile t of a grid whose x extent is a
+// multiple of 8 runs on XCD t % 8).  The loads touch one dword per 64-byte line and
+// change nothing; a wrong guess of the placement costs only the extra reads.
+// ---------------------------------------------------------------------------
+struct PfRegion {
+  const char* base;
+  int slab_bytes;  // a multiple of 64
+  int nslabs;
+  int xoff;        // slab j is read on XCD (j + xoff) % 8 ...
+  int every_xcd;   // ... or, when set, on every XCD
+};
+constexpr int PF_MAX_REGIONS = 6;
+struct Prefetch {
+  PfRegion r[PF_MAX_REGIONS];
+  int nreg;
+  int nblocks;     // prefetch workgroups (the launch rounds this up to whole grid rows)
+  unsigned* sink;  // null: the loaded values are discarded (a non-null sink keeps them)
+};
+
+// In a prefetch workgroup: `lin` = its linear workgroup id, `lin0` = the linear id of the
+// launch's first prefetch workgroup.  The lines of the slabs this XCD reads are spread
+// over the XCD's prefetch workgroups, 16 loads in flight per lane.
+__device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
+  const int xcd = lin & 7;
+  const int p = lin - lin0;
+  const int p0 = (xcd - lin0) & 7;  // the first prefetch workgroup on this XCD
+  const int rank = (p - p0) >> 3;
+  const int nrank = (pf.nblocks - p0 + 7) >> 3;
+  const int tid = threadIdx.x;
+  unsigned acc = 0;
+  for (int ri = 0; ri < pf.nreg; ++ri) {
+    const PfRegion R = pf.r[ri];
+    const int lps = R.slab_bytes >> 6;
+    const int first = R.every_xcd ? 0 : (xcd - R.xoff) & 7;
+    const int step = R.every_xcd ? 1 : 8;
+    const int nsl = R.every_xcd ? R.nslabs : (R.nslabs - first + 7) >> 3;
+    const int nlines = nsl * lps;
+    const int gstep = nrank * 256;
+    for (int g = rank * 256 + tid; g < nlines; g += 16 * gstep) {
+      unsigned v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int gg = min(g + u * gstep, nlines - 1);
+        const int j = gg / lps, off = gg - j * lps;
+        v[u] = load_global(reinterpret_cast<const unsigned*>(R.base + (size_t)(first + step * j) * R.slab_bytes +
+                                                             (size_t)off * 64));
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc ^= v[u];
+    }
+  }
+  if (pf.sink) pf.sink[tid] = acc;
+}
+
+// ---------------------------------------------------------------------------
 // skinny GEMM: Y[M, N] = X[M, K] . W[N, K]^T for M <= 64 per m-block, fp16 or
 // q4f16_1 weights, fp32 accumulation on MFMA 16x16x32, fused prologue/epilogue.
 // ---------------------------------------------------------------------------
@@ -86,6 +144,7 @@ struct SkOp {
   float dt;              // EPI_EULER
   float* x32;            // EPI_EULER state [M][ldo]
   _Float16* x16;         // EPI_EULER fp16 copy
+  Prefetch pf;           // prefetch workgroups appended as grid rows y >= splitk
 };
 
 struct SkPlan {
@@ -142,6 +201,7 @@ struct AttnArgs {
   float* part_ml;        // [KV][nsplit][Rpad][2]
   int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
   int rows, rpad;        // rows per kv head (Tq*H/KV) and padded
+  Prefetch pf;           // prefetch workgroups appended as grid rows y >= nsplit
 };
 // nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
 void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps);
