@@ -626,8 +626,42 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
   }
 
+  if (a.nsplit > 1) {
+    // the split's output normalized by its own softmax sum (a convex combination of V
+    // rows, so fp16 holds it), with (m, l) in fp32 for the combine.  The wave's 16 rows go
+    // through its own LDS rows (free after the last chunk's barrier) so that every store
+    // writes two whole rows of the partial (1 KB contiguous) instead of 16 pieces of 32 B.
+    constexpr int PLD = HD + 8;  // halfs per LDS row
+    _Float16* pl = reinterpret_cast<_Float16*>(lds_raw) + (size_t)w * 16 * PLD;
+    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      h4 o4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * linv);
+      *reinterpret_cast<h4*>(pl + r16 * PLD + 16 * dt + 4 * g) = o4;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    constexpr int LPR = HD / 8;           // 8-half pieces per row
+    constexpr int ITEMS = 16 * LPR;       // pieces of the wave's 16 rows, 64 per store
+    const size_t pr0 = ((size_t)kvh * a.nsplit + split) * a.rpad + blockIdx.x * ROWS + 16 * w;
+    _Float16* po = reinterpret_cast<_Float16*>(a.part_o);
+#pragma unroll
+    for (int it = 0; it < (ITEMS + 63) / 64; ++it) {
+      const int idx = 64 * it + lane, rr = idx / LPR, cc = (idx % LPR) * 8;
+      if (idx < ITEMS && blockIdx.x * ROWS + 16 * w + rr < a.rows)
+        *reinterpret_cast<h8*>(po + (pr0 + rr) * HD + cc) = *reinterpret_cast<const h8*>(pl + rr * PLD + cc);
+    }
+    if (g == 0 && row_ok) {
+      const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
+      a.part_ml[pr * 2 + 0] = m_run;
+      a.part_ml[pr * 2 + 1] = l_run;
+    }
+    return;
+  }
   if (!row_ok) return;
-  if (a.nsplit == 1) {
+  {
     const float inv = 1.0f / l_run;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -636,23 +670,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * inv);
       const int col = h * HD + 16 * dt + 4 * g;
       *reinterpret_cast<h4*>(a.out + (a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col)) = o4;
-    }
-  } else {
-    // the split's output normalized by its own softmax sum (a convex combination of V
-    // rows, so fp16 holds it), with (m, l) in fp32 for the combine
-    const size_t pr = ((size_t)kvh * a.nsplit + split) * a.rpad + row;
-    _Float16* po = reinterpret_cast<_Float16*>(a.part_o) + pr * HD;
-    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      h4 o4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o4[i] = f2h(oacc[dt][i] * linv);
-      *reinterpret_cast<h4*>(po + 16 * dt + 4 * g) = o4;
-    }
-    if (g == 0) {
-      a.part_ml[pr * 2 + 0] = m_run;
-      a.part_ml[pr * 2 + 1] = l_run;
     }
   }
 }

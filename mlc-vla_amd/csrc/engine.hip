@@ -51,7 +51,9 @@ struct OpDesc {
 struct Tiling {
   int tr, splits;
 };
-Tiling TILE_QKV = {16, 1}, TILE_O = {16, 2}, TILE_GU = {16, 1}, TILE_DOWN = {16, 4};
+struct LayerTilings {
+  Tiling qkv = {16, 1}, o = {16, 2}, gu = {16, 1}, down = {16, 4};
+};
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
 constexpr int ATTN_TARGET = 128;  // workgroups of the step's attention (row blocks x key splits)
@@ -67,14 +69,17 @@ enum : unsigned {
   PF_ATTN_QKV = 16,    // ... the next layer's q/k/v weights
   PF_O_DOWN = 32,      // o_proj fetches the down weights
   PF_DOWN_QKV = 64,    // down fetches the next layer's q/k/v weights
+  PF_ATTN_KV = 128,    // attention fetches the next layer's prefix K / V (each line once)
 };
 constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 
-// MLCV_TILING="qkv=16:S,o=16:S,gu=16:S,down=16:S" overrides the K slices of the
-// fragment-major layer GEMMs for tuning (read at context creation; 0 = planner).
-void read_tiling_override() {
+// MLCV_TILING="qkv=16:S,o=TR:S,gu=TR:S,down=TR:S" overrides the tile rows (16, or 32 for
+// o / gate_up / down) and K slices of the fragment-major layer GEMMs for tuning (read at
+// context creation; 0 = planner).
+LayerTilings read_tilings() {
+  LayerTilings lt;
   const char* e = std::getenv("MLCV_TILING");
-  if (!e) return;
+  if (!e) return lt;
   std::string spec(e);
   size_t pos = 0;
   while (pos < spec.size()) {
@@ -86,16 +91,17 @@ void read_tiling_override() {
       const std::string name = item.substr(0, eq);
       const int tr = std::atoi(item.substr(eq + 1, colon - eq - 1).c_str());
       const int sp = std::atoi(item.substr(colon + 1).c_str());
-      if (tr == 16) {
+      if (tr == 16 || (tr == 32 && name != "qkv")) {
         Tiling t{tr, sp};
-        if (name == "qkv") TILE_QKV = t;
-        else if (name == "o") TILE_O = t;
-        else if (name == "gu") TILE_GU = t;
-        else if (name == "down") TILE_DOWN = t;
+        if (name == "qkv") lt.qkv = t;
+        else if (name == "o") lt.o = t;
+        else if (name == "gu") lt.gu = t;
+        else if (name == "down") lt.down = t;
       }
     }
     pos = end + 1;
   }
+  return lt;
 }
 constexpr int RSS_COLS = 16;  // residual row statistics: one partial per 16 columns
 
@@ -181,6 +187,7 @@ struct Ctx {
   hipEvent_t cond_ev = nullptr;
   std::vector<hipEvent_t> mod_ev;
   bool fork_mod = false;
+  LayerTilings tilings;  // fragment-major layer GEMM tiles (MLCV_TILING at creation)
   // prefetch of later ops' operands by spare workgroups of the step's launches
   // (fragment-major path), PF_* bits: which launch fetches what
   unsigned prefetch = PF_DEFAULT;
@@ -275,10 +282,10 @@ int wait_mod(Ctx& c, int p, bool forked, hipStream_t st) {
   return 0;
 }
 
-Tiling tile_qkv(const Ctx& c) { return c.frag ? TILE_QKV : ROWMAJOR_QKV; }
-Tiling tile_o(const Ctx& c) { return c.frag ? TILE_O : ROWMAJOR_O; }
-Tiling tile_gu(const Ctx& c) { return c.frag ? TILE_GU : ROWMAJOR_GU; }
-Tiling tile_down(const Ctx& c) { return c.frag ? TILE_DOWN : ROWMAJOR_DOWN; }
+Tiling tile_qkv(const Ctx& c) { return c.frag ? c.tilings.qkv : ROWMAJOR_QKV; }
+Tiling tile_o(const Ctx& c) { return c.frag ? c.tilings.o : ROWMAJOR_O; }
+Tiling tile_gu(const Ctx& c) { return c.frag ? c.tilings.gu : ROWMAJOR_GU; }
+Tiling tile_down(const Ctx& c) { return c.frag ? c.tilings.down : ROWMAJOR_DOWN; }
 Tiling tile_head(const Ctx& c) { return c.frag ? Tiling{16, 2} : Tiling{64, 0}; }
 
 // ---- the ops of one decoder layer of the suffix path (modulations in modp) ------
@@ -309,34 +316,37 @@ void pf_add(Prefetch& pf, const void* base, size_t slab_bytes, int nslabs, int x
   if (pf.nreg >= PF_MAX_REGIONS || nslabs <= 0 || base == nullptr) return;
   pf.r[pf.nreg++] = PfRegion{static_cast<const char*>(base), (int)slab_bytes, nslabs, xoff & 7, every_xcd};
 }
-// the weight slabs of a fragment-major layer op: one 16-row slab per tile, read by the
-// tile's workgroups on XCD tile % 8
+// the weights of a fragment-major layer op: one tile's slabs (tr / 16 consecutive 16-row
+// slabs) per region slab, read by the tile's workgroups on XCD tile % 8
 void pf_weights(const Ctx& c, Prefetch& pf, const OpDesc& d, unsigned bit) {
   if (!(c.prefetch & bit) || !d.frag) return;
   pf.nblocks = c.pf_blocks;
+  const size_t sl = d.tr / 16;
   for (int i = 0; i < d.nseg; ++i) {
     const SkSeg& sg = c.h_segs[d.seg_off + i];
     const int tiles = (i + 1 < d.nseg ? c.h_segs[d.seg_off + i + 1].tile0 : d.ntiles) - sg.tile0;
     if (d.q4) {
-      pf_add(pf, sg.qw, (size_t)8 * d.K, tiles, sg.tile0, 0);  // 16 rows x K/8 words
-      pf_add(pf, sg.qs, (size_t)d.K, tiles, sg.tile0, 0);      // 16 rows x K/32 scales
+      pf_add(pf, sg.qw, sl * 8 * d.K, tiles, sg.tile0, 0);  // 16 rows x K/8 words per slab
+      pf_add(pf, sg.qs, sl * d.K, tiles, sg.tile0, 0);      // 16 rows x K/32 scales per slab
     } else {
-      pf_add(pf, sg.w, (size_t)32 * d.K, tiles, sg.tile0, 0);  // 16 rows x K halfs
+      pf_add(pf, sg.w, sl * 32 * d.K, tiles, sg.tile0, 0);  // 16 rows x K halfs per slab
     }
   }
 }
-// the prefix K / V of layer L (or its chunk images), read by the attention on every XCD
-void pf_kv(const Ctx& c, Prefetch& pf, int L, const float* keys, const _Float16* values) {
-  if (!(c.prefetch & PF_QKV_KV) || !c.frag || keys == nullptr) return;
+// the prefix K / V of layer L (or its chunk images), read by the attention (every XCD
+// reads every split's keys: every_xcd fills each XCD's L2, otherwise each line is read once)
+void pf_kv(const Ctx& c, Prefetch& pf, int L, const float* keys, const _Float16* values, unsigned bit,
+           int every_xcd) {
+  if (!(c.prefetch & bit) || !c.frag || keys == nullptr) return;
   pf.nblocks = c.pf_blocks;
   if (c.use_img) {
     const int chunks = (c.P + 31) / 32;
     pf_add(pf, c.kvimg + (size_t)L * c.img_layer_bytes, c.img_layer_bytes / ((size_t)c.KV * chunks), c.KV * chunks,
-           0, 1);
+           0, every_xcd);
   } else {
     const int slabs = (int)(kv_slice(c) / ((size_t)8 * c.HD));  // 8 keys per slab
-    pf_add(pf, keys + L * kv_slice(c), (size_t)8 * c.HD * sizeof(float), slabs, 0, 1);
-    pf_add(pf, values + L * kv_slice(c), (size_t)8 * c.HD * sizeof(_Float16), slabs, 0, 1);
+    pf_add(pf, keys + L * kv_slice(c), (size_t)8 * c.HD * sizeof(float), slabs, 0, every_xcd);
+    pf_add(pf, values + L * kv_slice(c), (size_t)8 * c.HD * sizeof(_Float16), slabs, 0, every_xcd);
   }
 }
 
@@ -344,7 +354,7 @@ int enqueue_qkv(Ctx& c, int L, const _Float16* modp, hipStream_t st, const float
                 const _Float16* values = nullptr) {  // adaRMS (input) + q/k/v
   const _Float16* m_in = mod_of(c, modp, 2 * L);
   SkOp op = make_op(c, c.layer_ops[4 * L + 0], c.prescaled ? c.xu : c.x16, c.W1, c.T);
-  pf_kv(c, op.pf, L, keys, values);
+  pf_kv(c, op.pf, L, keys, values, PF_QKV_KV, 1);
   set_norm(c, op, m_in);
   op.rope_cos = c.cos;
   op.rope_sin = c.sin;
@@ -401,6 +411,7 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   pf_weights(c, a.pf, c.layer_ops[4 * L + 2], PF_ATTN_GU);
   pf_weights(c, a.pf, c.layer_ops[4 * L + 3], PF_ATTN_DOWN);
   if (L + 1 < c.D) pf_weights(c, a.pf, c.layer_ops[4 * (L + 1)], PF_ATTN_QKV);
+  if (L + 1 < c.D) pf_kv(c, a.pf, L + 1, keys, values, PF_ATTN_KV, 0);
   return attn_launch(a, st);
 }
 
@@ -674,14 +685,13 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
                "depth / lengths / steps must be positive");
   MLCV_REQUIRE(cfg->num_steps <= 64, "num_steps must be <= 64");
 
-  static std::once_flag tiling_once;
-  std::call_once(tiling_once, read_tiling_override);
   auto* h = new (std::nothrow) mlcv_ctx();
   if (!h) {
     set_error("out of host memory");
     return -1;
   }
   Ctx& c = h->c;
+  c.tilings = read_tilings();
   c.cfg = *cfg;
   c.q4 = cfg->quant == MLCV_QUANT_Q4F16_1;
   c.W0 = cfg->vlm_width;

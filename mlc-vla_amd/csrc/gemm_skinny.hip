@@ -151,14 +151,23 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   // barrier between loads and MFMAs: each MFMA waits only for its own operands)
   constexpr bool DIRECT = XM != 0;
   constexpr int XMT = XM == 2 ? 1 : 4;  // m tiles loaded and multiplied by the direct path
-  constexpr int XS_HALFS = DIRECT ? KG * SLABS * 4 * 64 * 8 : MB * XLD;
+  // fragment-major tiles of several slabs: the 4 waves split K as in a 16-row tile and
+  // every wave multiplies its X fragments by all the slabs' weights (X is loaded once per
+  // workgroup); the 4 k-group partials of each slab are summed before the epilogue, which
+  // keeps the (slab, kg) wave roles
+  constexpr bool MSD = XM == 1 && SLABS > 1;
+  constexpr int SW = MSD ? SLABS : 1;   // slabs per wave in the product
+  constexpr int LKG = MSD ? 4 : KG;     // k groups of the product
+  constexpr int LCPW = NC / LKG;        // chunks per wave per round in the product
+  static_assert(!MSD || (LCPW >= 1 && LCPW * LKG == NC), "multi-slab tiles need NC >= 4");
+  constexpr int XS_HALFS = DIRECT ? LKG * SLABS * 4 * 64 * 8 : MB * XLD;
   __shared__ __attribute__((aligned(16))) _Float16 xs[XS_HALFS];
   __shared__ float denom[4][MB];     // NORM 1: 1 / sqrt(mean(x^2) + eps) per row, per wave;
                                      // NORM 2: each wave's partial sum of squares per row
   __shared__ f4 shiftacc[SLABS * 4]; // NORM 2: the shift row's product, per slab and lane group
   __shared__ int is_last;
-  static_assert(KG == 1 || (size_t)KG * SLABS * 4 * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
-  f4* red = reinterpret_cast<f4*>(xs);  // [KG][SLABS][4 m tiles][64 lanes] after the last round
+  static_assert(LKG == 1 || (size_t)LKG * SLABS * 4 * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
+  f4* red = reinterpret_cast<f4*>(xs);  // [LKG][SLABS][4 m tiles][64 lanes] after the last round
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
@@ -258,9 +267,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int j = 0; j < 4; ++j) part[j] = load_global(reinterpret_cast<const f4*>(rr + min(4 * (w + 4 * j), op.rowss_tiles - 4)));
   }
 
-  f4 acc[4];
+  f4 acc[SW][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = (f4){0.f, 0.f, 0.f, 0.f};
+  for (int sl = 0; sl < SW; ++sl)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[sl][i] = (f4){0.f, 0.f, 0.f, 0.f};
+  const int lkg = MSD ? w : kg;  // this wave's k group in the product
 
   // one round: rounds after the first run in a loop, the first is peeled so that the
   // prefetched loads above stay in flight (a loop header would wait for all of them)
@@ -274,12 +286,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     // of the weight fragments (q4: the dequantized nibble order, so the X fragment is
     // permuted after the load).
     const int KS = K >> 5, KCN = K >> 7;
-    h8 xf[CPW][4][XMT];
+    h8 xf[LCPW][4][XMT];
 #pragma unroll
-    for (int c = 0; c < CPW; ++c)
+    for (int c = 0; c < LCPW; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int kcs = kr + (kg * CPW + c) * KC;
+        const int kcs = kr + (lkg * LCPW + c) * KC;
         if constexpr (XM == 1) {
           const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
           const int piece = Q4 ? 16 * j + r16 : lane;
@@ -291,34 +303,41 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
           xf[c][j][0] = load_global(reinterpret_cast<const h8*>(op.x + (size_t)min(r16, mlast) * op.ldx + kx));
         }
       }
-    WRaw<Q4> wr[CPW];
+    WRaw<Q4> wr[SW][LCPW];
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int kcs = kr + (kg * CPW + c) * KC;
-      if constexpr (!Q4) {
+    for (int sl = 0; sl < SW; ++sl)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wr[c].v[j] = load_global(reinterpret_cast<const h8*>(
-              seg.w + (((size_t)lt * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
-      } else {
-        const size_t blk = ((size_t)lt * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
-        wr[c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
-        wr[c].s = load_global(seg.qs + blk);
+      for (int c = 0; c < LCPW; ++c) {
+        const int kcs = kr + (lkg * LCPW + c) * KC;
+        const size_t wsl = (size_t)SLABS * lt + sl;  // 16-row slab of the shuffled weights
+        if constexpr (!Q4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            wr[sl][c].v[j] = load_global(reinterpret_cast<const h8*>(
+                seg.w + ((wsl * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
+        } else {
+          const size_t blk = (wsl * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
+          wr[sl][c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
+          wr[sl][c].s = load_global(seg.qs + blk);
+        }
       }
-    }
     // every load of the round in flight before the first MFMA (the scheduler would
     // otherwise interleave them and keep only a few outstanding)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < CPW; ++c)
+    for (int c = 0; c < LCPW; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // k past the slice: the weight fragment is zeroed (X there is finite data of the
         // same rows, so the products vanish)
-        const bool kok = kr + (kg * CPW + c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g) < kend;
-        h8 a = wfrag<Q4>(wr[c], j);
+        const bool kok = kr + (lkg * LCPW + c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g) < kend;
+        h8 a[SW];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = kok ? a[e] : (_Float16)0.0f;
+        for (int sl = 0; sl < SW; ++sl) {
+          a[sl] = wfrag<Q4>(wr[sl][c], j);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[sl][e] = kok ? a[sl][e] : (_Float16)0.0f;
+        }
 #pragma unroll
         for (int mt = 0; mt < XMT; ++mt) {
           h8 b = xf[c][j][mt];
@@ -327,7 +346,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
             for (int e = 0; e < 8; ++e) b[e] = r16 < op.M ? b[e] : (_Float16)0.0f;
           }
           if constexpr (Q4) b = perm8(b);
-          acc[mt] = mfma16x16x32(a, b, acc[mt]);
+#pragma unroll
+          for (int sl = 0; sl < SW; ++sl) acc[sl][mt] = mfma16x16x32(a[sl], b, acc[sl][mt]);
         }
       }
   };
@@ -397,7 +417,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
           const h8 b = *reinterpret_cast<const h8*>(&xs[(mt * 16 + r16) * XLD + ko]);
-          acc[mt] = mfma16x16x32(a, b, acc[mt]);
+          acc[0][mt] = mfma16x16x32(a, b, acc[0][mt]);
         }
       }
     }
@@ -425,19 +445,23 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 
   // ---- k groups of a slab summed in k-group order; wave keeps m tiles kg + i*KG ----------
   f4 own[NOWN];
-  if constexpr (KG == 1) {
+  if constexpr (LKG == 1) {
 #pragma unroll
-    for (int i = 0; i < NOWN; ++i) own[i] = acc[i];
+    for (int i = 0; i < NOWN; ++i) own[i] = acc[0][i];
   } else {
+    // product k group q of slab sl at red[q][sl]: MSD waves write every slab of their k group
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) red[((kg * SLABS + slab) * 4 + mt) * 64 + lane] = acc[mt];
+    for (int sl = 0; sl < SW; ++sl)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        red[((lkg * SLABS + (MSD ? sl : slab)) * 4 + mt) * 64 + lane] = acc[sl][mt];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NOWN; ++i) {
       const int mt = kg + i * KG;
       f4 sum = red[((0 * SLABS + slab) * 4 + mt) * 64 + lane];
 #pragma unroll
-      for (int q = 1; q < KG; ++q) sum += red[((q * SLABS + slab) * 4 + mt) * 64 + lane];
+      for (int q = 1; q < LKG; ++q) sum += red[((q * SLABS + slab) * 4 + mt) * 64 + lane];
       own[i] = sum;
     }
   }
@@ -740,8 +764,9 @@ __global__ void wf_shuffle_q4_kernel(const uint32_t* __restrict__ qw, const _Flo
 template <int NORM, int EPI, bool TABLE, int TR, int XM>
 constexpr bool sk_combo() {
   if (XM == 1)
-    return TR == 16 && !TABLE &&
-           ((NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) || (NORM == 0 && EPI == EPI_GATED_RES));
+    return !TABLE && ((TR == 16 && ((NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) ||
+                                    (NORM == 0 && EPI == EPI_GATED_RES))) ||
+                      (TR == 32 && ((NORM == 2 && EPI == EPI_GEGLU) || (NORM == 0 && EPI == EPI_GATED_RES))));
   if (XM == 2) return TR == 16 && NORM == 0 && (EPI == EPI_STORE || (EPI == EPI_STORE_SILU && !TABLE));
   if (TABLE) return TR == 64 && NORM == 0 && EPI == EPI_STORE;
   if (TR == 16) return NORM == 1 && EPI == EPI_STORE;
@@ -754,7 +779,8 @@ int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   if constexpr (!sk_combo<NORM, EPI, TABLE, TR, XM>()) {
     MLCV_REQUIRE(false, "skinny GEMM: tile rows / prologue / epilogue combination not built");
   } else {
-    constexpr int KG = 4 / (TR / 16);
+    constexpr bool MSD = XM == 1 && TR > 16;  // multi-slab fragment-major tiles: 4 k groups
+    constexpr int KG = MSD ? 4 : 4 / (TR / 16);
     if (nc < KG) nc = KG;
     switch (nc) {
       case 1:
@@ -871,7 +897,8 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   int nc = cps >= 5 ? 8 : cps >= 3 ? 4 : cps;
   const bool direct = op.frag || op.xrow;  // operands straight into registers, little LDS
   MLCV_REQUIRE(!(op.frag && op.xrow), "fragment-major and row-major X at once");
-  MLCV_REQUIRE(!direct || op.tr == 16, "register-direct operands need 16-row tiles");
+  MLCV_REQUIRE(!direct || op.tr == 16 || (op.frag && op.tr == 32),
+               "register-direct operands need 16-row tiles (fragment-major X: 16 or 32)");
   MLCV_REQUIRE(!op.xrow || (op.M <= 16 && op.K % 128 == 0 && norm == 0),
                "row-major direct X needs M <= 16, K % 128 == 0 and no prologue");
   MLCV_REQUIRE(!op.frag || (op.M < MB && op.K % 128 == 0 && op.nseg <= 3),

@@ -234,6 +234,30 @@ def test_q4_path_vs_oracle_and_vs_fp(tiny):
     _tol(vel_q, ref)
 
 
+@pytest.mark.parametrize("kw", [TINY_KWARGS, DUMMY_KWARGS], ids=["tiny", "dummy"])
+def test_multi_slab_tiles_bit_identical(kw, monkeypatch):
+    """32-row fragment-major tiles (every wave multiplies its X fragments by both 16-row
+    weight slabs) split K over the same 4 waves and sum the k groups in the same order as
+    16-row tiles: with equal K slices the step and the graph loop are bit-identical."""
+    ref = Model(kw)
+    monkeypatch.setenv("MLCV_TILING", "o=32:2,gu=32:1,down=32:4")
+    alt = Model(kw)
+    monkeypatch.delenv("MLCV_TILING")
+    pm = make_prefix_mask_np(ref.cfg.prefix_len)
+    cos, sin = make_rope_np(ref.cfg.suffix_len, ref.cfg.vlm.head_dim, ref.cfg.rope_theta,
+                            offset=ref.cfg.prefix_len)
+    te = make_time_embs(ref.cfg.num_denoise_steps, ref.cfg.action_expert.width)[2].astype(np.float16)
+    outs = []
+    for m in (ref, alt):
+        k, v = _prefill(m, pm)
+        step = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                              m.params).numpy()
+        outs.append((step, m.runner.sample_graph(m.params, m.prefix, noise=m.noise)))
+    assert np.all(np.isfinite(outs[0][0])) and np.all(np.isfinite(outs[0][1]))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1], outs[0][1])
+
+
 def test_full_size_step_vs_oracle():
     """One fp16 denoise_step_kv at the full pi0.5 shape (18 layers, width 1024, P=968, T=50)
     against the float32 oracle, with N(0,1) stand-in prefix K/V."""
