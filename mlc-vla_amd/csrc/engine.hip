@@ -44,15 +44,15 @@ struct OpDesc {
 };
 
 // Tiling of the step's layer GEMMs.  With fragment-major operands (M < 64): 16-row tiles
-// whose waves load their operand fragments straight into registers; q/k/v and gate_up
-// take the whole K per workgroup (no split-K exchange), o_proj and down split K.
+// whose waves load their operand fragments straight into registers; q/k/v, o_proj and
+// gate_up take the whole K per workgroup (no split-K exchange), down splits K in 4.
 // Otherwise (M >= 64) the row-major kernels stage X through LDS with 16/32-row tiles.
 // Everything else uses 64-row tiles and the planner's split.
 struct Tiling {
   int tr, splits;
 };
 struct LayerTilings {
-  Tiling qkv = {16, 1}, o = {16, 2}, gu = {16, 1}, down = {16, 4};
+  Tiling qkv = {16, 1}, o = {16, 1}, gu = {16, 1}, down = {16, 4};
 };
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
