@@ -169,9 +169,12 @@ struct Ctx {
   // prefix K/V chunk images of every layer (built once per call from keys / values)
   char* kvimg = nullptr;
   size_t img_layer_bytes = 0;
-  // the enqueued sequence built the images (the loop: one build serves every step); a
-  // single step reads the f32 keys directly (a build would cost about what it saves)
+  // the enqueued sequence built the images and the attention reads them
   bool use_img = false;
+  // MLCV_LOOP_IMG=1: the loop builds the images once and every step reads them.  Off by
+  // default: the chunk copy from an image costs about what the conversion of the f32
+  // keys costs (both are bound by the chunk's bytes), so the build is pure overhead
+  bool loop_img = false;
   size_t attn_ws_floats_n = 0;
   int st_nsplit = 1, st_kps = 32, pf_nsplit = 1, pf_kps = 32;
 
@@ -575,8 +578,8 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
 int enqueue_loop(Ctx& c, const float* keys, const _Float16* values, hipStream_t st) {
   const size_t modstep = (size_t)c.NM * 3 * c.W1;
   MLCV_TRY(euler_init_launch(c.x0, c.x32, c.xin16, c.T * c.A, st));
-  MLCV_TRY(enqueue_kv_prep(c, keys, values, st));
-  c.use_img = true;
+  if (c.loop_img) MLCV_TRY(enqueue_kv_prep(c, keys, values, st));
+  c.use_img = c.loop_img;
   if (c.hoist) MLCV_TRY(enqueue_time_mod(c, c.te, c.NS, st, c.fork_mod));
   for (int i = 0; i < c.NS; ++i) {
     if (c.hoist) {
@@ -829,6 +832,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // measured: the forked modulation slows the layer chain more than it hides, so it is
   // off unless MLCV_FORK_MOD=1 (tuning)
   c.fork_mod = std::getenv("MLCV_FORK_MOD") != nullptr && std::atoi(std::getenv("MLCV_FORK_MOD")) != 0;
+  if (const char* e = std::getenv("MLCV_LOOP_IMG")) c.loop_img = std::atoi(e) != 0;
   if (const char* e = std::getenv("MLCV_PREFETCH")) c.prefetch = (unsigned)std::strtoul(e, nullptr, 0);
   if (const char* e = std::getenv("MLCV_PF_BLOCKS")) c.pf_blocks = std::max(8, std::atoi(e));
   bool ev_ok = hipEventCreateWithFlags(&c.cond_ev, hipEventDisableTiming) == hipSuccess;

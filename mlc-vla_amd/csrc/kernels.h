@@ -6,9 +6,10 @@
 namespace mlcv {
 
 // ---------------------------------------------------------------------------
-// L2 prefetch by spare workgroups.  A launch can append `nblocks` workgroups that only
-// read the regions a later kernel of the sequence will read, so that the later kernel
-// finds them in the L2 of the XCD its workgroups run on (workgroups are dealt to the 8
+// Prefetch by spare workgroups.  A launch can append `nblocks` workgroups that only read
+// the regions a later kernel of the sequence will read, so that the later kernel finds
+// them in the memory-side cache (and, where the XCD's L2 keeps them across the launch
+// boundary, in the L2 of the XCD its workgroups run on: workgroups are dealt to the 8
 // XCDs round-robin by linear id, and a consumer tile t of a grid whose x extent is a
 // multiple of 8 runs on XCD t % 8).  The loads touch one dword per 64-byte line and
 // change nothing; a wrong guess of the placement costs only the extra reads.
@@ -30,14 +31,14 @@ struct Prefetch {
 
 // In a prefetch workgroup: `lin` = its linear workgroup id, `lin0` = the linear id of the
 // launch's first prefetch workgroup.  The lines of the slabs this XCD reads are spread
-// over the XCD's prefetch workgroups, 16 loads in flight per lane.
+// over the XCD's prefetch workgroups, 16 loads in flight per lane (any workgroup size).
 __device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
   const int xcd = lin & 7;
   const int p = lin - lin0;
   const int p0 = (xcd - lin0) & 7;  // the first prefetch workgroup on this XCD
   const int rank = (p - p0) >> 3;
   const int nrank = (pf.nblocks - p0 + 7) >> 3;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nt = blockDim.x;
   unsigned acc = 0;
   for (int ri = 0; ri < pf.nreg; ++ri) {
     const PfRegion R = pf.r[ri];
@@ -46,8 +47,8 @@ __device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
     const int step = R.every_xcd ? 1 : 8;
     const int nsl = R.every_xcd ? R.nslabs : (R.nslabs - first + 7) >> 3;
     const int nlines = nsl * lps;
-    const int gstep = nrank * 256;
-    for (int g = rank * 256 + tid; g < nlines; g += 16 * gstep) {
+    const int gstep = nrank * nt;
+    for (int g = rank * nt + tid; g < nlines; g += 16 * gstep) {
       unsigned v[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
