@@ -23,6 +23,7 @@
 // A read touches start on distinct banks); V transposed [d][key] with a pitch of 40
 // halfs, written as packed key pairs (ds_write_b32) -- lanes of one store cover 16
 // key pairs x 4 dims and a wave's MFMA reads of 16 d-rows land on disjoint banks.
+#include <algorithm>
 #include <type_traits>
 
 #include "kernels.h"
@@ -797,7 +798,43 @@ __global__ void euler_init_kernel(const float* __restrict__ x0, float* __restric
   }
 }
 
+struct CopyList {
+  CopyJob j[COPY_MAX];
+};
+// job blockIdx.y; 16-byte pieces when both ends and the size are 16-byte aligned, bytes otherwise
+__global__ void copy_list_kernel(CopyList L) {
+  const CopyJob jb = L.j[blockIdx.y];
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (size_t)gridDim.x * blockDim.x;
+  if (((reinterpret_cast<uintptr_t>(jb.src) | reinterpret_cast<uintptr_t>(jb.dst) | jb.bytes) & 15) == 0) {
+    const u4* s = static_cast<const u4*>(jb.src);
+    u4* d = static_cast<u4*>(jb.dst);
+    for (size_t i = t; i < jb.bytes / 16; i += nt) d[i] = s[i];
+  } else {
+    const char* s = static_cast<const char*>(jb.src);
+    char* d = static_cast<char*>(jb.dst);
+    for (size_t i = t; i < jb.bytes; i += nt) d[i] = s[i];
+  }
+}
+
 }  // namespace
+
+int copy_list_launch(const CopyJob* jobs, int n, hipStream_t st) {
+  MLCV_REQUIRE(n >= 0 && n <= COPY_MAX, "at most 8 copies per batch");
+  CopyList L{};
+  size_t most = 0;
+  int k = 0;
+  for (int i = 0; i < n; ++i) {
+    if (jobs[i].bytes == 0) continue;
+    MLCV_REQUIRE(jobs[i].src && jobs[i].dst, "null copy buffer");
+    L.j[k++] = jobs[i];
+    most = std::max(most, jobs[i].bytes);
+  }
+  if (k == 0) return 0;
+  const unsigned bx = (unsigned)std::min<size_t>(256, (most / 16 + 255) / 256 + 1);
+  copy_list_kernel<<<dim3(bx, k), 256, 0, st>>>(L);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
 
 void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps) {
   // prefix splits of whole 32-key chunks, plus one split for the suffix block

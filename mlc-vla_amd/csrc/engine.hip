@@ -1046,22 +1046,21 @@ int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mas
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  MLCV_HIP(hipMemcpyAsync(c.px, prefix_embs, (size_t)c.P * c.W0 * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.mask, prefix_mask, (size_t)c.P * 4, hipMemcpyDeviceToDevice, st));
+  const CopyJob in[] = {{prefix_embs, c.px, (size_t)c.P * c.W0 * 2}, {prefix_mask, c.mask, (size_t)c.P * 4}};
+  MLCV_TRY(copy_list_launch(in, 2, st));
   MLCV_TRY(run_graph(c, c.g_prefill, {}, [&](hipStream_t s) { return enqueue_prefill(c, c.pkeys, c.pvalues, s); },
                      st));
   const size_t n = (size_t)c.D * kv_slice(c);
-  MLCV_HIP(hipMemcpyAsync(keys, c.pkeys, n * 4, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(values, c.pvalues, n * 2, hipMemcpyDeviceToDevice, st));
-  return 0;
+  const CopyJob out[] = {{c.pkeys, keys, n * 4}, {c.pvalues, values, n * 2}};
+  return copy_list_launch(out, 2, st);
 }
 
-static int copy_suffix_inputs(Ctx& c, const float* cos, const float* sin, const float* mask, hipStream_t st) {
+// the suffix RoPE tables and the prefix mask, staged with the entry point's other inputs
+static void suffix_jobs(const Ctx& c, const float* cos, const float* sin, const float* mask, std::vector<CopyJob>& jobs) {
   const size_t half = c.HD / 2;
-  MLCV_HIP(hipMemcpyAsync(c.cos, cos, (size_t)c.T * half * 4, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.sin, sin, (size_t)c.T * half * 4, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.mask, mask, (size_t)c.P * 4, hipMemcpyDeviceToDevice, st));
-  return 0;
+  jobs.push_back({cos, c.cos, (size_t)c.T * half * 4});
+  jobs.push_back({sin, c.sin, (size_t)c.T * half * 4});
+  jobs.push_back({mask, c.mask, (size_t)c.P * 4});
 }
 
 int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, const void* x_t, const void* time_emb,
@@ -1072,9 +1071,9 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  MLCV_HIP(hipMemcpyAsync(c.xin16, x_t, (size_t)c.T * c.A * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.te, time_emb, (size_t)c.W1 * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  std::vector<CopyJob> jobs = {{x_t, c.xin16, (size_t)c.T * c.A * 2}, {time_emb, c.te, (size_t)c.W1 * 2}};
+  suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
+  MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
   MLCV_TRY(run_graph(c, c.g_step, {keys, values},
                      [&](hipStream_t s) {
@@ -1095,9 +1094,9 @@ int mlcv_denoise_loop_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  MLCV_HIP(hipMemcpyAsync(c.x0, x0, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.te, time_embs, (size_t)c.NS * c.W1 * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  std::vector<CopyJob> jobs = {{x0, c.x0, (size_t)c.T * c.A * 4}, {time_embs, c.te, (size_t)c.NS * c.W1 * 2}};
+  suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
+  MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
   MLCV_TRY(run_graph(c, c.g_loop, {keys, values}, [&](hipStream_t s) { return enqueue_loop(c, keys, vals, s); },
                      st));
@@ -1112,10 +1111,11 @@ int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask,
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  MLCV_HIP(hipMemcpyAsync(c.px, prefix_embs, (size_t)c.P * c.W0 * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.x0, x0, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
-  MLCV_HIP(hipMemcpyAsync(c.te, time_embs, (size_t)c.NS * c.W1 * 2, hipMemcpyDeviceToDevice, st));
-  MLCV_TRY(copy_suffix_inputs(c, suffix_cos, suffix_sin, prefix_mask, st));
+  std::vector<CopyJob> jobs = {{prefix_embs, c.px, (size_t)c.P * c.W0 * 2},
+                               {x0, c.x0, (size_t)c.T * c.A * 4},
+                               {time_embs, c.te, (size_t)c.NS * c.W1 * 2}};
+  suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
+  MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
   MLCV_TRY(run_graph(c, c.g_chunk, {},
                      [&](hipStream_t s) {
                        MLCV_TRY(enqueue_prefill(c, c.pkeys, c.pvalues, s));

@@ -242,4 +242,14 @@ int tg_launch(const TgArgs& a, hipStream_t st);
 
 int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStream_t st);
 
+// a batch of device-to-device copies in one launch (the entry points stage their inputs
+// into the context's buffers with one kernel instead of one copy launch per buffer)
+struct CopyJob {
+  const void* src;
+  void* dst;
+  size_t bytes;
+};
+constexpr int COPY_MAX = 8;
+int copy_list_launch(const CopyJob* jobs, int n, hipStream_t st);
+
 }  // namespace mlcv
