@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--summarize-pmc", metavar="COUNTER_CSV",
                     help="print the mean of each counter per dispatch of a rocprofv3 --pmc CSV, by kernel and "
                          "launch shape, and exit")
-    ap.add_argument("--only-op", choices=sorted(OPS_PER_STEP), default=None,
+    ap.add_argument("--only-op", choices=sorted(list(OPS_PER_STEP) + ["attention_only", "prefill"]), default=None,
                     help="after set-up, run --op-iters launches of one op of the step and exit (for --pmc runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run --op-iters device copies of this many MiB and exit (counter calibration)")
@@ -163,7 +163,7 @@ def op_bytes_flops(cfg, op):
         return nm * (3 * W * W + 3 * W) * 2 + W * 2 + nm * 3 * W * 2, 2 * nm * 3 * W * W
     if op == "qkv":
         return (nq + 2 * nkv) * W * 2 + T * W * 2 + 2 * W * 2 + T * (nq + 2 * nkv) * 2, 2 * T * W * (nq + 2 * nkv)
-    if op == "attention":
+    if op in ("attention", "attention_only"):
         return (KV * P * hd * 6 + T * nq * 2 + 2 * T * nkv * 2 + T * nq * 2 + P * 4 + T * hd * 4,
                 4 * H * T * (P + T) * hd)
     if op == "o_proj":
@@ -180,10 +180,30 @@ def op_bytes_flops(cfg, op):
 OPS_PER_STEP = {"modulation": 1, "qkv": 18, "attention": 18, "o_proj": 18, "gate_up": 18, "down": 18, "head": 1}
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _pct(ts, q):
+    ts = sorted(ts)
+    return ts[min(len(ts) - 1, int(q * len(ts)))]
+
+
 def cpu_baseline(cfg, seconds):
-    """The numpy float32 oracle of one denoise_step_kv on the host cores (bounded sample)."""
+    """CPU restatement baseline (the numpy float32 oracle on the host cores; the reference's
+    TVM llvm/c build is not available): 3 warm-ups, then at least 10 timed denoise_step_kv
+    at the full shape within a bounded sample, and the config-1 run (the 2-layer model,
+    prefill + 10 Euler steps) the same way."""
     import numpy as np
 
+    from mlc_vla.model.pi0 import Pi0Config
     from oracle import pi0_oracle as O
 
     threads = len(os.sched_getaffinity(0))
@@ -195,6 +215,18 @@ def cpu_baseline(cfg, seconds):
             threads = max(t["num_threads"] for t in blas)
     except Exception:  # noqa: BLE001
         pass
+
+    def timed_cpu(fn, budget, min_iters=10, warm=3):
+        for _ in range(warm):
+            fn()
+        ts, t0 = [], time.perf_counter()
+        while len(ts) < min_iters or (time.perf_counter() - t0 < budget and len(ts) < 5000):
+            t1 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t1) * 1e6)
+        return ts, time.perf_counter() - t0
+
+    P = O.Prec("f32")
     d = O.dims_from_config(cfg)
     keep = lambda n: not (".experts.0." in n or ".mlp.0." in n)  # noqa: E731
     params = O.make_params([(n, s) for n, s in O.param_specs(d) if keep(n)], 0, "float32")
@@ -205,18 +237,24 @@ def cpu_baseline(cfg, seconds):
     te = O.sinusoidal_time_emb(1.0, d.ae_width)
     cos, sin = O.make_rope_np(d.suffix_len, d.head_dim, d.theta, offset=d.prefix_len)
     pm = O.make_prefix_mask_np(d.prefix_len)
-    P = O.Prec("f32")
-    O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 5000:
-            break
-    return {"value": round(el / n * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": f"{n} float32 denoise_step_kv at the full pi0.5 shape (18 layers, P=968, T=50) "
-                      f"with the numpy oracle after 1 warm-up ({el:.1f} s)"}
+    ts, el = timed_cpu(lambda: O.denoise_step_kv(params, d, keys, values, x_t, te, cos, sin, pm, P), seconds)
+
+    # config 1: the 2-layer model (prefix 32, horizon 8, fp32), prefill + 10 host Euler steps
+    c1 = Pi0Config(paligemma_variant="tiny_vlm", action_expert_variant="tiny_action", image_keys=(), max_token_len=32,
+                   action_horizon=8, action_dim=32, num_denoise_steps=10, dtype="float32")
+    d1 = O.dims_from_config(c1)
+    p1 = O.make_params(O.param_specs(d1), 0, "float32")
+    prefix = np.random.default_rng(1).standard_normal((1, d1.prefix_len, d1.vlm_width)).astype(np.float32)
+    noise = np.random.default_rng(0).standard_normal((1, d1.suffix_len, d1.action_dim)).astype(np.float32)
+    ts1, el1 = timed_cpu(lambda: O.sample(p1, d1, prefix, noise, P, num_steps=10), min(5.0, seconds / 4))
+    return {"value": round(sum(ts) / len(ts), 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "p50_us": round(_pct(ts, 0.5), 1), "p90_us": round(_pct(ts, 0.9), 1), "cpu_model": _cpu_model(),
+            "label": "CPU restatement baseline (numpy float32 oracle), not the reference TVM build",
+            "sample": f"{len(ts)} float32 denoise_step_kv at the full pi0.5 shape (18 layers, P=968, T=50) "
+                      f"with the numpy oracle after 3 warm-ups ({el:.1f} s)",
+            "config1_chunk": {"p50_us": round(_pct(ts1, 0.5), 1), "p90_us": round(_pct(ts1, 0.9), 1),
+                              "iters": len(ts1), "unit": "us/chunk",
+                              "sample": "2-layer model (prefix 32, horizon 8, fp32): prefill + 10 Euler steps"}}
 
 
 def main():
@@ -293,6 +331,42 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / iters, (time.perf_counter() - w0) * 1e3 / iters
 
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    scratch = torch.empty(512 << 18, device="cuda", dtype=torch.float32)  # 512 MiB for the cold protocol
+
+    def per_step(fn, iters):
+        """GPU time of each of `iters` back-to-back calls (events between them: the host stays ahead)."""
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+        fn()
+        ev[0].record()
+        for i in range(iters):
+            fn()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        return [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(iters)]
+
+    def per_cold(fn, iters):
+        """Cold protocol: 512 MiB written between calls (outside the timed region), then a spin
+        on the GPU so that the host has queued the call before its start event runs."""
+        ts = []
+        for i in range(iters):
+            scratch.fill_(float(i))
+            if hasattr(torch.cuda, "_sleep"):
+                torch.cuda._sleep(1_000_000)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return ts
+
+    if args.only_op == "prefill":  # the prefill graph alone (MFMA counters of the prefill GEMMs)
+        for _ in range(args.op_iters):
+            vm["prefill"](prefix, pm_800, params)
+        torch.cuda.synchronize()
+        print(json.dumps({"only_op": "prefill", "launches": args.op_iters}))
+        return
     if args.only_op:
         op = N.OPS[args.only_op]
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -315,8 +389,19 @@ def main():
     chunk_nh_ms, _ = timed(chunk, args.chunk_iters, 3)
     vm.set_hoist(True)
 
+    # ---- single steps: percentiles warm, and the cold-cache protocol -----------
+    warm_ts = per_step(step, max(20, min(args.steps, 200)))
+    cold_ts = per_cold(step, 30)
+
+    # ---- isolated attention (one layer; 18 layers back to back), cold -----------
+    a_op = N.OPS["attention_only"]
+    attn_one = lambda L: N.call("mlcv_bench_op", vm._ctx, a_op, L, 1, runtime._ptr(keys),  # noqa: E731
+                                runtime._ptr(values), stream())
+    a_single = per_cold(lambda: attn_one(0), 30)
+    a_stack = per_cold(lambda: [attn_one(L) for L in range(18)], 10)
+    a_bytes, _ = op_bytes_flops(cfg, "attention")
+
     # ---- per-op launch times (the step's kernels one op at a time) ------------
-    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
     per_op = {}
     for name, cnt in OPS_PER_STEP.items():
         op = N.OPS[name]
@@ -356,6 +441,17 @@ def main():
         "step_wall_us": round(step_wall_ms * 1e3, 1),
         "chunk_ms": round(chunk_ms, 3),
         "chunk_ms_per_step_modulation": round(chunk_nh_ms, 3),
+        "step_percentiles": {"p50_us": round(_pct(warm_ts, 0.5), 1), "p90_us": round(_pct(warm_ts, 0.9), 1),
+                             "iters": len(warm_ts)},
+        "step_cold": {"p50_us": round(_pct(cold_ts, 0.5), 1), "p90_us": round(_pct(cold_ts, 0.9), 1),
+                      "iters": len(cold_ts), "protocol": "512 MiB scratch written between steps, outside the timed region"},
+        "attention_isolated": {
+            "workload": "joint attention of one layer, P=968 prefix keys (fp32) + 50 suffix keys, 8 q heads, hd 256",
+            "single_cold_p50_us": round(_pct(a_single, 0.5), 2),
+            "stacked18_cold_us_per_layer": round(_pct(a_stack, 0.5) / 18, 2),
+            "bytes_per_launch": int(a_bytes),
+            "single_GBps": round(a_bytes / (_pct(a_single, 0.5) * 1e-6) / 1e9, 1),
+            "stacked18_GBps": round(a_bytes * 18 / (_pct(a_stack, 0.5) * 1e-6) / 1e9, 1)},
         "prefill_ms": round(prefill_ms, 3),
         "loop_ms": round(loop_ms, 3),
         "step_roofline": {"bound": "hbm", "achieved": round(sbytes / (step_us * 1e-6) / 1e9, 1),
@@ -388,14 +484,16 @@ def main():
                 qparams.append(by_name[n])
         del cache
         vq = vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams)
-        q_ms, _ = timed(lambda: vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams),
-                        args.steps, args.warmup)
+        qstep = lambda: vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams)  # noqa: E731
+        q_ms, _ = timed(qstep, args.steps, args.warmup)
+        q_cold = per_cold(qstep, 30)
         qbytes = step_bytes(cfg, q4=True)
         v16 = step().numpy()
         cosq = float(np.dot(vq.numpy().ravel(), v16.ravel()) / (np.linalg.norm(vq.numpy()) * np.linalg.norm(v16)))
         out["q4f16_1_step"] = {"us": round(q_ms * 1e3, 1), "bytes_per_step": int(qbytes),
                                "frac": round(qbytes / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                               "cos_vs_fp16": round(cosq, 5)}
+                               "cos_vs_fp16": round(cosq, 5), "cold_p50_us": round(_pct(q_cold, 0.5), 1),
+                               "cold_p90_us": round(_pct(q_cold, 0.9), 1)}
         del vmq, qparams
 
     if not args.no_cpu_baseline:

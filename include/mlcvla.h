@@ -144,6 +144,7 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
 #define MLCV_OP_GATEUP 5     /* adaRMS + gate_up + GeGLU */
 #define MLCV_OP_DOWN 6       /* down + gated residual */
 #define MLCV_OP_HEAD 7       /* final adaRMS + action_out_proj */
+#define MLCV_OP_ATTENTION_ONLY 8 /* MLCV_OP_ATTENTION without the workgroups that prefetch the next ops' weights */
 int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
                   void* stream);
 

@@ -1134,7 +1134,7 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
   MLCV_REQUIRE(layer >= 0 && layer < c.D, "layer out of range");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
-  if (op == MLCV_OP_ATTENTION) MLCV_REQUIRE(keys && values, "attention needs keys and values");
+  if (op == MLCV_OP_ATTENTION || op == MLCV_OP_ATTENTION_ONLY) MLCV_REQUIRE(keys && values, "attention needs keys and values");
   for (int i = 0; i < iters; ++i) {
     switch (op) {
       case MLCV_OP_TIME_MOD: MLCV_TRY(enqueue_time_mod(c, c.te, 1, st, false)); break;
@@ -1146,6 +1146,15 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
         c.use_img = false;
         MLCV_TRY(enqueue_attn(c, layer, keys, vals, st));
         break;
+      case MLCV_OP_ATTENTION_ONLY: {
+        c.use_img = false;
+        const unsigned pf = c.prefetch;
+        c.prefetch = 0;
+        const int r = enqueue_attn(c, layer, keys, vals, st);
+        c.prefetch = pf;
+        MLCV_TRY(r);
+        break;
+      }
       case MLCV_OP_OPROJ: MLCV_TRY(enqueue_oproj(c, layer, c.mod, st)); break;
       case MLCV_OP_GATEUP: MLCV_TRY(enqueue_gateup(c, layer, c.mod, st)); break;
       case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;

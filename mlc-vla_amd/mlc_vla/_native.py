@@ -56,7 +56,8 @@ SIGNATURES = {
     "mlcv_bench_op": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
 }
 
-OPS = {"time_mod": 0, "modulation": 1, "qkv": 2, "attention": 3, "o_proj": 4, "gate_up": 5, "down": 6, "head": 7}
+OPS = {"time_mod": 0, "modulation": 1, "qkv": 2, "attention": 3, "o_proj": 4, "gate_up": 5, "down": 6, "head": 7,
+       "attention_only": 8}
 
 _lock = threading.Lock()
 _lib = None
