@@ -53,12 +53,12 @@ struct Tiling {
 };
 struct LayerTilings {
   Tiling qkv = {16, 1}, o = {16, 1}, gu = {16, 1}, down = {16, 4};
+  Tiling head = {16, 1}, tmlp = {16, 1};  // action_out and the time MLP (16-row tiles)
 };
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
 constexpr int ATTN_TARGET = 128;  // workgroups of the step's attention (row blocks x key splits)
 constexpr int MOD_SPLITS = 1;   // modulation pieces (16-row tiles: 384 workgroups each)
-constexpr int TMLP_SPLITS = 2;  // time MLP (16-row tiles: 128 workgroups)
 // prefetch assignments (which launch of a layer fetches which later operand into the
 // memory-side cache): the attention runs on half the CUs for the longest span of the layer
 enum : unsigned {
@@ -73,9 +73,10 @@ enum : unsigned {
 };
 constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 
-// MLCV_TILING="qkv=16:S,o=TR:S,gu=TR:S,down=TR:S" overrides the tile rows (16, or 32 for
-// o / gate_up / down) and K slices of the fragment-major layer GEMMs for tuning (read at
-// context creation; 0 = planner).
+// MLCV_TILING="qkv=16:S,o=TR:S,gu=TR:S,down=TR:S,head=16:S,tmlp=16:S" overrides the tile
+// rows (16, or 32 for o / gate_up / down) and K slices of the fragment-major GEMMs (the
+// time MLP's K slices apply to its small-M tiles) for tuning (read at context creation;
+// 0 = planner).
 LayerTilings read_tilings() {
   LayerTilings lt;
   const char* e = std::getenv("MLCV_TILING");
@@ -91,9 +92,11 @@ LayerTilings read_tilings() {
       const std::string name = item.substr(0, eq);
       const int tr = std::atoi(item.substr(eq + 1, colon - eq - 1).c_str());
       const int sp = std::atoi(item.substr(colon + 1).c_str());
-      if (tr == 16 || (tr == 32 && name != "qkv")) {
+      if (tr == 16 || (tr == 32 && (name == "o" || name == "gu" || name == "down"))) {
         Tiling t{tr, sp};
         if (name == "qkv") lt.qkv = t;
+        else if (name == "head") lt.head = t;
+        else if (name == "tmlp") lt.tmlp = t;
         else if (name == "o") lt.o = t;
         else if (name == "gu") lt.gu = t;
         else if (name == "down") lt.down = t;
@@ -289,7 +292,7 @@ Tiling tile_qkv(const Ctx& c) { return c.frag ? c.tilings.qkv : ROWMAJOR_QKV; }
 Tiling tile_o(const Ctx& c) { return c.frag ? c.tilings.o : ROWMAJOR_O; }
 Tiling tile_gu(const Ctx& c) { return c.frag ? c.tilings.gu : ROWMAJOR_GU; }
 Tiling tile_down(const Ctx& c) { return c.frag ? c.tilings.down : ROWMAJOR_DOWN; }
-Tiling tile_head(const Ctx& c) { return c.frag ? Tiling{16, 2} : Tiling{64, 0}; }
+Tiling tile_head(const Ctx& c) { return c.frag ? c.tilings.head : Tiling{64, 0}; }
 
 // ---- the ops of one decoder layer of the suffix path (modulations in modp) ------
 const _Float16* mod_of(const Ctx& c, const _Float16* modp, int idx) { return modp + (size_t)idx * 3 * c.W1; }
@@ -802,7 +805,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       {tiles(W1, tile_o(c).tr), nq, mb_t, tile_o(c).tr, tile_o(c).splits},
       {tiles(c.F1, tile_gu(c).tr / 2), W1, mb_t, tile_gu(c).tr, tile_gu(c).splits},
       {tiles(W1, tile_down(c).tr), c.F1, mb_t, tile_down(c).tr, tile_down(c).splits},
-      {tiles(W1, 16), W1, mb_s, 16, TMLP_SPLITS},                                // time mlp
+      {tiles(W1, 16), W1, mb_s, 16, c.tilings.tmlp.splits},                      // time mlp
       {tiles(W1, 64), W1, mb_s, 64, 0},
       {std::max(2, c.NM - 2) * tiles(3 * W1, 64), W1, mb_s, 64, 0},              // modulation pieces
       {std::max(2, c.NM - 2) * tiles(3 * W1, 16), W1, mb_s, 16, MOD_SPLITS},
@@ -1001,8 +1004,9 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     const int gtr = c.small_m ? 16 : 64;
     const Lin ftin = gemv_copy(c.tin), ftout = gemv_copy(c.tout);
     MLCV_REQUIRE(ftin.N >= 0 && ftout.N >= 0, get_error());
-    seg_ops(c, c.op_tin, {seg_of(ftin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, c.small_m ? TMLP_SPLITS : 0);
-    seg_ops(c, c.op_tout, {seg_of(ftout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, c.small_m ? TMLP_SPLITS : 0);
+    const int tsp = c.small_m ? c.tilings.tmlp.splits : 0;
+    seg_ops(c, c.op_tin, {seg_of(ftin, c.tmp, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, tsp);
+    seg_ops(c, c.op_tout, {seg_of(ftout, c.cond, W1, W1)}, W1, EPI_STORE_SILU, c.q4, gtr, tsp);
     c.op_tin.xrow = c.op_tout.xrow = c.small_m;
     const int ldo = c.NM * 3 * W1;
     std::vector<SkSeg> first, rest;
