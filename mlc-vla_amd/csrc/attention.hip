@@ -367,15 +367,16 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
   const size_t pr0 = (size_t)kvh * a.nsplit * a.rpad + row;
   const int ns = a.nsplit;
   const int sl = min(lane, ns - 1);
-  const float m_l = a.part_ml[(pr0 + (size_t)sl * a.rpad) * 2];
-  const float l_l = a.part_ml[(pr0 + (size_t)sl * a.rpad) * 2 + 1];
+  // the partials were written by the attention kernel just before: device-scope loads
+  const uint32_t nrow = (uint32_t)a.KV * ns * a.rpad;
+  const __amdgpu_buffer_rsrc_t rml = dev_rsrc(a.part_ml, nrow * 8), ro = dev_rsrc(a.part_o, nrow * hd * 2);
+  const float m_l = load_dev<float>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8));
+  const float l_l = load_dev<float>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8 + 4));
   // the O loads of the first 256 dims go out with the m / l loads (partials: fp16 O_s / l_s)
-  const _Float16* po = reinterpret_cast<const _Float16*>(a.part_o);
   const int d0 = min(lane * 4, hd - 4);
   h4 o[MAXS];
 #pragma unroll
-  for (int s = 0; s < MAXS; ++s)
-    o[s] = *reinterpret_cast<const h4*>(po + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0);
+  for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0) * 2));
   // out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s with w_s = exp(m_s - max)
   float ms[MAXS], wv[MAXS];
   float mmax = -INFINITY;
@@ -395,8 +396,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
   for (int d = lane * 4; d < hd; d += 256) {
     if (d != d0) {  // head dims past 256
 #pragma unroll
-      for (int s = 0; s < MAXS; ++s)
-        o[s] = *reinterpret_cast<const h4*>(po + (pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d);
+      for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d) * 2));
     }
     f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -551,12 +551,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     load(0, R0);
     if (nch > 1) load(1, R1);
     if constexpr (QF) {
-      const size_t tile = (size_t)kvh * (a.rpad / 16) + (blockIdx.x * ROWS + 16 * w) / 16;
+      // q fragments from the q/k/v epilogue of the previous kernel: device-scope loads
+      const __amdgpu_buffer_rsrc_t rq = dev_rsrc(a.qf, (uint32_t)a.KV * a.rpad * NKS * 128);
+      const int tile = kvh * (a.rpad / 16) + (blockIdx.x * ROWS + 16 * w) / 16;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const _Float16* qb = a.qf + ((tile * NKS + ks) * 2) * 512 + lane * 8;
-        qh[ks] = load_global(reinterpret_cast<const h8*>(qb));
-        ql[ks] = load_global(reinterpret_cast<const h8*>(qb + 512));
+        const int qb = (((tile * NKS + ks) * 2) * 512 + lane * 8) * 2;
+        qh[ks] = load_dev<h8>(rq, qb);
+        ql[ks] = load_dev<h8>(rq, qb + 1024);
       }
     } else {
       QRaw<HD> qa, qb;

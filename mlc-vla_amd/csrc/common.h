@@ -70,6 +70,20 @@ __device__ __forceinline__ T load_global(const T* p) {
   return *(gT*)p;
 }
 
+// Device-scope loads (buffer loads with sc1) of data the previous kernel wrote: they read
+// at the memory side instead of missing in this XCD's L2 and filling it with lines no later
+// launch reuses.  Offsets are in bytes; past `bytes` the load returns zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+template <class T>
+__device__ __forceinline__ T load_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "4, 8 or 16 bytes");
+  if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+  else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 16));
+  else return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 16));
+}
+
 // fp16 <-> fp32 with IEEE round-to-nearest-even (v_cvt_f16_f32 / v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }
 __device__ __forceinline__ _Float16 f2h(float f) { return (_Float16)f; }

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     // X is the previous kernel's output: device-scope loads (sc1) read it at the memory
     // side instead of filling this XCD's L2 with lines the next launch cannot reuse
     __amdgpu_buffer_rsrc_t xr;
-    if constexpr (XM == 1) xr = __builtin_amdgcn_make_buffer_rsrc((void*)op.x, 0, MB * K * 2, 0x00020000);
+    if constexpr (XM == 1) xr = dev_rsrc(op.x, MB * K * 2);
     h8 xf[LCPW][4][XMT];
 #pragma unroll
     for (int c = 0; c < LCPW; ++c)
@@ -301,8 +301,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
           const int piece = Q4 ? 16 * j + r16 : lane;
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt)
-            xf[c][j][mt] = __builtin_bit_cast(
-                h8, __builtin_amdgcn_raw_buffer_load_b128(xr, ((ks * 4 + mt) * 64 + piece) * 16, 0, 16));
+            xf[c][j][mt] = load_dev<h8>(xr, ((ks * 4 + mt) * 64 + piece) * 16);
         } else {
           const int kx = min(kcs + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g), K - 8);
           xf[c][j][0] = load_global(reinterpret_cast<const h8*>(op.x + (size_t)min(r16, mlast) * op.ldx + kx));
