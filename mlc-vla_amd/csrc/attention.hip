@@ -89,8 +89,8 @@ __device__ __forceinline__ void cvt8(const h8 x, float* o) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = h2f(x[e]);
 }
-__device__ __forceinline__ void ld8f(const float* p, float* o) {
-  const f4 a = load_global(reinterpret_cast<const f4*>(p)), b = load_global(reinterpret_cast<const f4*>(p + 4));
+__device__ __forceinline__ void ld8f(__amdgpu_buffer_rsrc_t r, int byte_off, float* o) {
+  const f4 a = load_dev<f4, KV_AUX>(r, byte_off), b = load_dev<f4, KV_AUX>(r, byte_off + 16);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     o[e] = a[e];
@@ -102,29 +102,30 @@ __device__ __forceinline__ void ld8f(const float* p, float* o) {
 template <int HD, bool KF32>
 __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
-  const size_t base = (size_t)kvh * a.Sp * HD;
+  // this kv head's keys and values (element offsets below are within one head: < 2^31 bytes)
+  const size_t head = (size_t)kvh * a.Sp * HD, hbytes = (size_t)a.Sp * HD;
+  const __amdgpu_buffer_rsrc_t rk = dev_rsrc(static_cast<const char*>(a.kp) + head * (KF32 ? 4 : 2),
+                                             (uint32_t)(hbytes * (KF32 ? 4 : 2)));
+  const __amdgpu_buffer_rsrc_t rv = dev_rsrc(a.vp + head, (uint32_t)(hbytes * 2));
 #pragma unroll
   for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
     int j, dp;
     kitem<HD>(i, tid, j, dp);
-    const size_t off = base + (size_t)min(c0 + j, kend - 1) * HD + dp;
+    const int off = min(c0 + j, kend - 1) * HD + dp;
     if constexpr (KF32) {
-      const float* kp = reinterpret_cast<const float*>(a.kp);
-      ld8f(kp + off, r.k[i]);
-      ld8f(kp + off + HALF, r.k[i] + 8);
+      ld8f(rk, off * 4, r.k[i]);
+      ld8f(rk, (off + HALF) * 4, r.k[i] + 8);
     } else {
-      const _Float16* kp = reinterpret_cast<const _Float16*>(a.kp);
-      cvt8(load_global(reinterpret_cast<const h8*>(kp + off)), r.k[i]);
-      cvt8(load_global(reinterpret_cast<const h8*>(kp + off + HALF)), r.k[i] + 8);
+      cvt8(load_dev<h8, KV_AUX>(rk, off * 2), r.k[i]);
+      cvt8(load_dev<h8, KV_AUX>(rk, (off + HALF) * 2), r.k[i] + 8);
     }
   }
 #pragma unroll
   for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
     int jp, d0;
     vitem<HD>(i, tid, jp, d0);
-    const _Float16* vb = a.vp + base + d0;
-    r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * HD));
-    r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * HD));
+    r.v[i][0] = load_dev<h8, KV_AUX>(rv, (min(c0 + 2 * jp, kend - 1) * HD + d0) * 2);
+    r.v[i][1] = load_dev<h8, KV_AUX>(rv, (min(c0 + 2 * jp + 1, kend - 1) * HD + d0) * 2);
   }
   // a global-space load whose value is untouched until store time: a flat load, or
   // arithmetic on the loaded value here, would make the compiler wait for every load in
@@ -183,21 +184,23 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
 template <int HD>
 __device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
+  // the previous kernel's output: device-scope loads
+  const __amdgpu_buffer_rsrc_t rk = dev_rsrc(a.ks32, (uint32_t)kend * a.ks_ld * 4);
+  const __amdgpu_buffer_rsrc_t rv = dev_rsrc(a.vs, (uint32_t)kend * a.vs_ld * 2);
 #pragma unroll
   for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
     int j, dp;
     kitem<HD>(i, tid, j, dp);
-    const float* kr = a.ks32 + (size_t)min(c0 + j, kend - 1) * a.ks_ld + (size_t)kvh * HD + dp;
-    ld8f(kr, r.k[i]);
-    ld8f(kr + HALF, r.k[i] + 8);
+    const int off = min(c0 + j, kend - 1) * a.ks_ld + kvh * HD + dp;
+    ld8f(rk, off * 4, r.k[i]);
+    ld8f(rk, (off + HALF) * 4, r.k[i] + 8);
   }
 #pragma unroll
   for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
     int jp, d0;
     vitem<HD>(i, tid, jp, d0);
-    const _Float16* vb = a.vs + (size_t)kvh * HD + d0;
-    r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * a.vs_ld));
-    r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld));
+    r.v[i][0] = load_dev<h8>(rv, (min(c0 + 2 * jp, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
+    r.v[i][1] = load_dev<h8>(rv, (min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
   }
   r.msk = 0.f;
   r.mok = c0 + (tid & (KCH - 1)) < kend;

@@ -70,19 +70,34 @@ __device__ __forceinline__ T load_global(const T* p) {
   return *(gT*)p;
 }
 
-// Device-scope loads (buffer loads with sc1) of data the previous kernel wrote: they read
-// at the memory side instead of missing in this XCD's L2 and filling it with lines no later
-// launch reuses.  Offsets are in bytes; past `bytes` the load returns zeros.
+// Buffer loads with explicit cache-policy bits (AUX: 16 = device scope, sc1).  Device-scope
+// loads of data the previous kernel wrote read it at the memory side instead of missing in
+// this XCD's L2 and filling it with lines no later launch reuses.  Offsets are in bytes;
+// past `bytes` the load returns zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
-template <class T>
+template <class T, int AUX = 16>
 __device__ __forceinline__ T load_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
   static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "4, 8 or 16 bytes");
-  if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
-  else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 16));
-  else return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 16));
+  if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, AUX));
+  else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, AUX));
+  else return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, AUX));
 }
+// cache policy of the streamed operands (measured on the step at P=968, T=50):
+// prefix / suffix keys and values: device scope, 4 us per step faster than plain loads;
+// weights (layer GEMMs, and the row-major time-MLP / modulation GEMVs): non-temporal (2),
+// 15 us per step faster with a cold memory-side cache, 9-25 us with a warm one
+#ifndef MLCV_KV_AUX
+#define MLCV_KV_AUX 16
+#endif
+#ifndef MLCV_W_AUX
+#define MLCV_W_AUX 2
+#endif
+#ifndef MLCV_WROW_AUX
+#define MLCV_WROW_AUX 2
+#endif
+constexpr int KV_AUX = MLCV_KV_AUX, W_AUX = MLCV_W_AUX, WROW_AUX = MLCV_WROW_AUX;
 
 // fp16 <-> fp32 with IEEE round-to-nearest-even (v_cvt_f16_f32 / v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }

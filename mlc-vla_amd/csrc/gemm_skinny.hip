@@ -315,10 +315,10 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
         const int kcs = kr + (lkg * LCPW + c) * KC;
         const size_t wsl = (size_t)SLABS * lt + sl;  // 16-row slab of the shuffled weights
         if constexpr (!Q4) {
+          const __amdgpu_buffer_rsrc_t rw = dev_rsrc(seg.w + wsl * KS * 512, (uint32_t)KS * 1024);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            wr[sl][c].v[j] = load_global(reinterpret_cast<const h8*>(
-                seg.w + ((wsl * KS + min((kcs >> 5) + j, KS - 1)) * 64 + lane) * 8));
+            wr[sl][c].v[j] = load_dev<h8, XM == 2 ? WROW_AUX : W_AUX>(rw, (min((kcs >> 5) + j, KS - 1) * 64 + lane) * 16);
         } else {
           const size_t blk = (wsl * KCN + min(kcs >> 7, KCN - 1)) * 64 + lane;
           wr[sl][c].words = load_global(reinterpret_cast<const u4*>(seg.qw + blk * 4));
