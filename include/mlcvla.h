@@ -132,6 +132,19 @@ int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, i
 int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,
                 const void* bias, void* y, int32_t N, void* stream);
 
+/* Prefill linear on the long-M tile GEMM (testing / benchmarking; no counterpart in the
+ * reference): x [M,K] f16, w [N,K] f16 (MLCV_TILE_GEGLU: [2N,K], gate rows then up rows),
+ * y [M,N] f16 with f32 accumulation:
+ *   MLCV_TILE_STORE     y = x . w^T
+ *   MLCV_TILE_RESIDUAL  y = fp16(y + fp16(x . w^T))
+ *   MLCV_TILE_GEGLU     y = fp16(fp16(gelu_tanh(fp16(x . wg^T))) * fp16(x . wu^T))
+ * small_tiles = 1 runs the 128 x 128 tile kernel instead of the 256-row one.  Synchronous. */
+#define MLCV_TILE_STORE 0
+#define MLCV_TILE_RESIDUAL 1
+#define MLCV_TILE_GEGLU 2
+int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
+                     int32_t small_tiles, void* stream);
+
 /* Enqueue `iters` launches of one operation of denoise_step_kv on `stream`, on the
  * context's current buffers (benchmarking / profiling only; no counterpart in the
  * reference).  `layer` selects the decoder layer; `keys` / `values` are needed for

@@ -194,6 +194,27 @@ __device__ __forceinline__ void counter_reset(unsigned* p) {
   __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Meeting point of the n workgroups of one group (one thread of each calls it once, after
+// its stores have completed).  ctr[0] counts the arrivals of the current meeting, ctr[1]
+// is its generation: the last to arrive resets the count and advances the generation, the
+// others poll the generation.  The count is zero after every meeting, so launches with a
+// different n may reuse the counters; meetings over the same counters must be ordered.
+// The poll is bounded: false after `limit` polls (the group did not meet).
+__device__ __forceinline__ bool group_meet_gen(unsigned* ctr, unsigned n, unsigned limit) {
+  const unsigned gen = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_all_memory();  // the generation is read before this arrival can complete the meeting
+  if (counter_add(ctr, 1u) == n - 1) {
+    counter_reset(ctr);
+    counter_add(ctr + 1, 1u);
+    return true;
+  }
+  for (unsigned i = 0; i < limit; ++i) {
+    if (__hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) return true;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return false;
+}
+
 // Split an fp32 value into fp16 hi + lo with hi + lo ~= x to ~2^-22 relative
 // (absolute floor: fp16 subnormal spacing 2^-24 on the lo part).
 __device__ __forceinline__ void split_f32(float x, _Float16& hi, _Float16& lo) {

@@ -169,6 +169,12 @@ struct Ctx {
   unsigned* counters = nullptr;
   size_t ncounters = 0;
   float* attn_ws = nullptr;
+  // split-K partials and meeting counters of the prefill GEMMs (256-row tiles)
+  float* gemm_ws = nullptr;
+  size_t gemm_ws_floats = 0;
+  unsigned* gemm_sync = nullptr;
+  size_t gemm_sync_words = 0;
+  bool gemm_small = false;  // MLCV_PREFILL_SMALL_TILES=1: the 128 x 128 tile kernel only
   // prefix K/V chunk images of every layer (built once per call from keys / values)
   char* kvimg = nullptr;
   size_t img_layer_bytes = 0;
@@ -481,6 +487,15 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
   return enqueue_head(c, modp, euler, st);
 }
 
+// the prefill GEMMs' split-K workspace (shared: the launches are ordered on one stream)
+void gemm_ws_args(const Ctx& c, TgArgs& g) {
+  g.ws = c.gemm_ws;
+  g.ws_floats = c.gemm_ws_floats;
+  g.sync = c.gemm_sync;
+  g.sync_tiles = (int)(c.gemm_sync_words / 32);
+  g.small_tiles = c.gemm_small ? 1 : 0;
+}
+
 // ---- prefill: expert-0 over the prefix, K/V written per layer ----------------
 int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
   const int W0 = c.W0, P = c.P, HD = c.HD;
@@ -505,6 +520,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     g.N = nqkv;
     g.K = W0;
     g.epi = TG_STORE;
+    gemm_ws_args(c, g);
     MLCV_TRY(tg_launch(g, st));
     MLCV_TRY(kv_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.KV, HD, kL, vL, st));
     if (L == c.D - 1) break;  // the last layer's attention / MLP feed no output
@@ -545,6 +561,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     o.N = W0;
     o.K = nq;
     o.epi = TG_RESIDUAL;
+    gemm_ws_args(c, o);
     MLCV_TRY(tg_launch(o, st));
     MLCV_TRY(rmsnorm_launch(c.px, ly.ln_post0, c.pxn, P, W0, c.cfg.rms_norm_eps, st));
     TgArgs gu{};
@@ -560,6 +577,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     gu.K = W0;
     gu.epi = TG_GEGLU;
     gu.F = c.F0;
+    gemm_ws_args(c, gu);
     MLCV_TRY(tg_launch(gu, st));
     TgArgs dn{};
     dn.a = c.ph;
@@ -573,6 +591,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     dn.N = W0;
     dn.K = c.F0;
     dn.epi = TG_RESIDUAL;
+    gemm_ws_args(c, dn);
     MLCV_TRY(tg_launch(dn, st));
   }
   return 0;
@@ -791,6 +810,10 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
                                 attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
   ALLOC(c.attn_ws, c.attn_ws_floats_n);
+  c.gemm_ws_floats = tg_ws_floats();
+  c.gemm_sync_words = tg_sync_words();
+  ALLOC(c.gemm_ws, c.gemm_ws_floats);
+  ALLOC(c.gemm_sync, c.gemm_sync_words);
   c.img_layer_bytes = attn_img_bytes(c.KV, c.P, hd);
   ALLOC(c.kvimg, (size_t)c.D * c.img_layer_bytes);
 
@@ -836,6 +859,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // off unless MLCV_FORK_MOD=1 (tuning)
   c.fork_mod = std::getenv("MLCV_FORK_MOD") != nullptr && std::atoi(std::getenv("MLCV_FORK_MOD")) != 0;
   if (const char* e = std::getenv("MLCV_LOOP_IMG")) c.loop_img = std::atoi(e) != 0;
+  if (const char* e = std::getenv("MLCV_PREFILL_SMALL_TILES")) c.gemm_small = std::atoi(e) != 0;
   if (const char* e = std::getenv("MLCV_PREFETCH")) c.prefetch = (unsigned)std::strtoul(e, nullptr, 0);
   if (const char* e = std::getenv("MLCV_PF_BLOCKS")) c.pf_blocks = std::max(8, std::atoi(e));
   bool ev_ok = hipEventCreateWithFlags(&c.cond_ev, hipEventDisableTiming) == hipSuccess;
@@ -845,6 +869,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
     return fail(-1);
   }
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(c.gemm_sync, 0, c.gemm_sync_words * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.counters_side, 0, c.ncounters_side * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.xu, 0, (size_t)64 * W1 * 2) != hipSuccess ||
       hipMemset(c.qf, 0, qf_halfs * 2) != hipSuccess ||
@@ -1261,6 +1286,49 @@ int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, i
   MLCV_REQUIRE(w && q_weight && q_scale && N > 0 && K > 0, "bad argument");
   return q4_dequant_launch(q_weight, reinterpret_cast<const _Float16*>(q_scale), reinterpret_cast<_Float16*>(w), N,
                            K, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
+                     int32_t small_tiles, void* stream) {
+  MLCV_REQUIRE(x && w && y && M > 0 && K > 0 && N > 0, "bad argument");
+  MLCV_REQUIRE(epi == TG_STORE || epi == TG_RESIDUAL || epi == TG_GEGLU, "unknown epilogue");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // split-K workspace and meeting counters of this entry point (per device, kept; calls on
+  // one device are serialized by the lock)
+  static std::mutex mu;
+  static float* ws[64] = {};
+  static unsigned* sync[64] = {};
+  std::lock_guard<std::mutex> lk(mu);
+  int dev = 0;
+  MLCV_HIP(hipGetDevice(&dev));
+  MLCV_REQUIRE(dev >= 0 && dev < 64, "device index");
+  if (!ws[dev]) {
+    MLCV_HIP(hipMalloc(&ws[dev], tg_ws_floats() * sizeof(float)));
+    MLCV_HIP(hipMalloc(&sync[dev], tg_sync_words() * sizeof(unsigned)));
+    MLCV_HIP(hipMemset(sync[dev], 0, tg_sync_words() * sizeof(unsigned)));
+  }
+  TgArgs g{};
+  g.a = reinterpret_cast<const _Float16*>(x);
+  g.lda = K;
+  g.b0 = g.b1 = g.b2 = reinterpret_cast<const _Float16*>(w);
+  g.n1 = g.n2 = epi == TG_GEGLU ? 2 * N : N;
+  g.ldb = K;
+  g.c = reinterpret_cast<_Float16*>(y);
+  g.ldc = N;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.epi = epi;
+  g.F = N;
+  g.ws = ws[dev];
+  g.ws_floats = tg_ws_floats();
+  g.sync = sync[dev];
+  g.sync_tiles = (int)(tg_sync_words() / 32);
+  g.small_tiles = small_tiles ? 1 : 0;
+  MLCV_HIP(hipStreamSynchronize(st));
+  MLCV_TRY(tg_launch(g, st));
+  MLCV_HIP(hipStreamSynchronize(st));
+  return 0;
 }
 
 int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,

@@ -9,6 +9,8 @@
 // one L2 only.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace mlcv {
 
 namespace {
@@ -142,10 +144,283 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(TgArgs a, int mtiles, in
   }
 }
 
+// ---- long-M GEMM: 256-row tiles, operands DMA'd straight into swizzled LDS ----------------
+//
+// Workgroup tile 256 (m) x BN (n) x 64 (k), 4 waves in 2 x 2: wave (wm, wn) owns m rows
+// [128 wm, +128) and n rows [BN/2 wn, +BN/2) as 4 x NBW blocks of 32 x 32 on
+// v_mfma_f32_32x32x16_f16 with the weights as the A operand, so D[n][m] leaves each lane
+// 4 consecutive n of one m row (8-byte stores).
+// LDS: per stage A 256 x 64 and B BN x 64 halfs.  One global_load_lds of 16 B per lane
+// moves 8 rows x 128 B (a row is 8 lanes, one whole line); row r's piece p (8 halfs) lands
+// in slot p ^ (r & 7) of the row, so the MFMA operand reads (8 consecutive lanes = 8 rows,
+// same piece) touch 8 distinct 16-byte slots of 8 different 128-byte rows: conflict-free.
+// Two stages: the DMA of k tile t + 1 runs while tile t is multiplied.
+// Split-K (SPLIT): the S workgroups of a tile run on one XCD (workgroups are dealt to the 8
+// XCDs round-robin by linear id); each writes its fp32 partial in the MFMA register order
+// (1 KB per store), they meet (group_meet_gen: the grid is launched only when it fits on
+// the CUs at once, so the meeting completes), and each reduces a share of the tile's blocks
+// in split order (deterministic) before the epilogue.
+constexpr int GBM = 256, GBK = 64;
+constexpr unsigned GMEET_POLLS = 1u << 22;
+
+struct GemmPlan {
+  int bn, splitk, kt_per;  // n tile, K slices, k tiles (of 64) per slice
+  int mtiles, ntiles;      // ntiles: n tiles of BN (GeGLU: of BN/2 outputs)
+  float* ws;               // split-K partials [tile][split][4 waves][blocks][4][64] f4
+  unsigned* sync;          // per tile: 32 words (arrivals, generation)
+};
+
+__device__ __forceinline__ int lds_swz(int r, int p) { return (r >> 3) * 1024 + (r & 7) * 128 + ((p ^ (r & 7)) << 4); }
+
+template <int BN, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
+  constexpr int NBW = BN / 64;                  // n blocks of 32 per wave
+  constexpr int ASZ = GBM * GBK * 2, BSZ = BN * GBK * 2;
+  constexpr int STG = ASZ + BSZ;
+  __shared__ __attribute__((aligned(16))) char lds[2 * STG];
+  typedef __attribute__((address_space(3))) void* lptr_t;
+  typedef const __attribute__((address_space(1))) void* gptr_t;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int wm = w >> 1, wn = w & 1;
+  // tile and K slice; the S slices of a tile share the XCD (id % 8)
+  const int id = blockIdx.x, xcd = id % NXCD, j = id / NXCD;
+  const int S = SPLIT ? p.splitk : 1;
+  const int s = j % S, tl = j / S;
+  const int tile = tl * NXCD + xcd;
+  const int ntile_all = p.mtiles * p.ntiles;
+  if (tile >= ntile_all) return;
+  const int tm = tile % p.mtiles, tn = tile / p.mtiles;
+  const int m0 = tm * GBM;
+  const int kt0 = s * p.kt_per, nkt = min(p.kt_per, a.K / GBK - kt0);
+
+  // per-lane global row pointers of this wave's DMA rows: A rows [64 w, +64), B rows
+  // [BN/4 w, +BN/4), 8 rows per instruction
+  constexpr int NAI = 8, NBI = BN / 32;
+  const int lr = lane >> 3, pc = (lane & 7) ^ lr;  // row in the 8, and its piece
+  const _Float16* ag[NAI];
+  const _Float16* bg[NBI];
+#pragma unroll
+  for (int i = 0; i < NAI; ++i) {
+    const int m = min(m0 + 64 * w + 8 * i + lr, a.M - 1);
+    ag[i] = a.a + (size_t)m * a.lda + pc * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < NBI; ++i) {
+    const int r = (BN / 4) * w + 8 * i + lr;  // B tile row
+    if constexpr (EPI == TG_GEGLU) {
+      // wave half wn holds 64 outputs as [gate 32, up 32, gate 32, up 32]
+      const int hw = r / (BN / 2), blk = (r % (BN / 2)) / 32, jj = r % 32;
+      const int jo = tn * (BN / 2) + hw * (BN / 4) + (blk >> 1) * 32 + jj;
+      bg[i] = a.b0 + (size_t)((blk & 1) ? a.F + jo : jo) * a.ldb + pc * 8;
+    } else {
+      const int n = min(tn * BN + r, a.N - 1);
+      bg[i] = brow_ptr(a, n) + pc * 8;
+    }
+  }
+  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+    char* sb = lds + stage * STG;
+    const int ko = (kt0 + kt) * GBK;
+#pragma unroll
+    for (int i = 0; i < NAI; ++i)
+      __builtin_amdgcn_global_load_lds((gptr_t)(ag[i] + ko), (lptr_t)(sb + (8 * w + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NBI; ++i)
+      __builtin_amdgcn_global_load_lds((gptr_t)(bg[i] + ko), (lptr_t)(sb + ASZ + ((BN / 32) * w + i) * 1024), 16, 0, 0);
+  };
+
+  f16v acc[NBW][4];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[nb][mb][e] = 0.f;
+
+  if (nkt > 0) dma(0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    wait_all_memory();  // this wave's DMA of tile kt has landed in LDS
+    __syncthreads();    // every wave's has; stage kt+1 is no longer read
+    if (kt + 1 < nkt) dma(kt + 1, (kt + 1) & 1);
+    const char* sa = lds + (kt & 1) * STG;
+    const char* sbb = sa + ASZ;
+#pragma unroll
+    for (int kb = 0; kb < GBK / 16; ++kb) {
+      const int pp = 2 * kb + lh;
+      h8 wf[NBW], xf[4];
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb)
+        wf[nb] = *reinterpret_cast<const h8*>(sbb + lds_swz(wn * (BN / 2) + nb * 32 + l32, pp));
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz(wm * 128 + mb * 32 + l32, pp));
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[nb], xf[mb], acc[nb][mb]);
+    }
+  }
+
+  // epilogue of one 32 x 32 block (wave role wm2 / wn2, blocks nb / mb): lane column
+  // m = l32, rows n = 8 (e / 4) + 4 lh + (e % 4)
+  auto store_block = [&](const f16v& v, int wm2, int wn2, int nb, int mb) __attribute__((always_inline)) {
+    const int m = m0 + wm2 * 128 + mb * 32 + l32;
+    if (m >= a.M) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = tn * BN + wn2 * (BN / 2) + nb * 32 + 8 * q + 4 * lh;
+      if (n >= a.N) continue;
+      _Float16* cp = a.c + (size_t)m * a.ldc + n;
+      h4 y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = f2h(v[4 * q + i]);
+      if constexpr (EPI == TG_RESIDUAL) {
+        const h4 c0 = *reinterpret_cast<const h4*>(cp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = hadd(c0[i], y[i]);
+      }
+      *reinterpret_cast<h4*>(cp) = y;
+    }
+  };
+
+  if constexpr (EPI == TG_GEGLU) {
+    // blocks (0, 1) and (2, 3) of the wave are gate / up of the same 32 outputs
+#pragma unroll
+    for (int hb = 0; hb < NBW / 2; ++hb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int m = m0 + wm * 128 + mb * 32 + l32;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int jo = tn * (BN / 2) + wn * (BN / 4) + hb * 32 + 8 * q + 4 * lh;
+          h4 y;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const _Float16 gv = f2h(acc[2 * hb][mb][4 * q + i]), uv = f2h(acc[2 * hb + 1][mb][4 * q + i]);
+            y[i] = hmul(f2h(gelu_tanh(h2f(gv))), uv);
+          }
+          *reinterpret_cast<h4*>(a.c + (size_t)m * a.ldc + jo) = y;
+        }
+      }
+    return;
+  } else if constexpr (!SPLIT) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) store_block(acc[nb][mb], wm, wn, nb, mb);
+    return;
+  } else {
+    // partial of this split: [wave][nb][mb][q][lane] f4
+    constexpr int BLK = NBW * 4;                // blocks per wave
+    constexpr size_t TILE_F4 = 4 * BLK * 4 * 64;  // f4 per split partial
+    f4* part = reinterpret_cast<f4*>(p.ws) + ((size_t)tile * S + s) * TILE_F4;
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4 v = {acc[nb][mb][4 * q], acc[nb][mb][4 * q + 1], acc[nb][mb][4 * q + 2], acc[nb][mb][4 * q + 3]};
+          part[((w * BLK + nb * 4 + mb) * 4 + q) * 64 + lane] = v;
+        }
+    __shared__ int met;
+    wait_all_memory();
+    __syncthreads();
+    if (tid == 0) met = group_meet_gen(p.sync + 32 * tile, (unsigned)S, GMEET_POLLS);
+    __syncthreads();
+    // blocks u = (wave role, nb, mb) of the tile, u % S == s, one wave each
+    const f4* base = reinterpret_cast<const f4*>(p.ws) + (size_t)tile * S * TILE_F4;
+    for (int u = s + S * w; u < 4 * BLK; u += 4 * S) {
+      const int w2 = u / BLK, b = u % BLK, nb = b / 4, mb = b % 4;
+      f16v v;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = 0.f;
+      for (int sp = 0; sp < S; ++sp) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4 x = base[(size_t)sp * TILE_F4 + ((size_t)u * 4 + q) * 64 + lane];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[4 * q + i] += x[i];
+        }
+      }
+      if (!met) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = __builtin_nanf("");
+      }
+      store_block(v, w2 >> 1, w2 & 1, nb, mb);
+    }
+  }
+}
+
+// compute units of the current device (cached per device)
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// 256-row tile plan; false = the shape needs the 128 x 128 kernel
+bool big_plan(const TgArgs& a, GemmPlan& p) {
+  if (a.small_tiles || a.K % GBK != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
+  if (a.epi == TG_GEGLU) {
+    if (a.F % 128 != 0) return false;
+    p.bn = 256;
+    p.ntiles = a.F / 128;
+  } else {
+    if (a.N % 4 != 0) return false;
+    p.bn = 128;
+    p.ntiles = (a.N + 127) / 128;
+  }
+  p.mtiles = (a.M + GBM - 1) / GBM;
+  const int tiles = p.mtiles * p.ntiles, kts = a.K / GBK;
+  const int slots = ((tiles + NXCD - 1) / NXCD) * NXCD;  // tile slots of the XCD-major grid
+  int S = 1;
+  if (a.epi != TG_GEGLU && a.ws && a.sync && tiles <= a.sync_tiles) {
+    // every workgroup of a split grid resident at once (one per CU), at least 4 k tiles each
+    S = std::min({8, device_cus() / slots, kts / 4});
+    const size_t part_floats = (size_t)4 * (p.bn / 64) * 4 * 4 * 64 * 4;
+    while (S > 1 && (size_t)tiles * S * part_floats > a.ws_floats) --S;
+    S = std::max(S, 1);
+  }
+  p.kt_per = (kts + S - 1) / S;
+  p.splitk = (kts + p.kt_per - 1) / p.kt_per;
+  p.ws = a.ws;
+  p.sync = a.sync;
+  return true;
+}
+
+int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
+  const int tiles = p.mtiles * p.ntiles;
+  const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
+  if (a.epi == TG_GEGLU) big_gemm_kernel<256, TG_GEGLU, false><<<blocks, 256, 0, st>>>(a, p);
+  else if (p.splitk > 1) {
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<128, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+  } else {
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, TG_RESIDUAL, false><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<128, TG_STORE, false><<<blocks, 256, 0, st>>>(a, p);
+  }
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
 }  // namespace
+
+size_t tg_sync_words() { return (size_t)std::max(device_cus(), 1) * 32; }
+// one 256 x 128 fp32 partial per CU
+size_t tg_ws_floats() { return (size_t)std::max(device_cus(), 1) * GBM * 128; }
 
 int tg_launch(const TgArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.K % 8 == 0 && a.lda % 8 == 0 && a.ldb % 8 == 0, "tile GEMM needs 16-byte aligned rows");
+  GemmPlan p{};
+  if (big_plan(a, p)) return big_launch(a, p, st);
   int ntiles;
   if (a.epi == TG_GEGLU) {
     MLCV_REQUIRE(a.F % 64 == 0, "GeGLU tile GEMM needs mlp_dim % 64 == 0");

@@ -237,7 +237,17 @@ struct TgArgs {
   int M, N, K;
   int epi;
   int F;                 // TG_GEGLU: up rows offset in b0
+  // split-K of the 256-row tile path (narrow N): partials workspace and per-tile meeting
+  // counters (32 words per tile, zero at allocation); null = no split-K
+  float* ws;
+  size_t ws_floats;
+  unsigned* sync;
+  int sync_tiles;
+  int small_tiles;       // 1: the 128 x 128 tile kernel only
 };
+// words of meeting counters and floats of partials the 256-row tile path can use
+size_t tg_sync_words();
+size_t tg_ws_floats();
 int tg_launch(const TgArgs& a, hipStream_t st);
 
 int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStream_t st);

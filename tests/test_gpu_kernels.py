@@ -73,6 +73,50 @@ def test_q4_dequant_bitexact(n, k):
     np.testing.assert_array_equal(_host(out).view(np.uint16), Q.dequantize(qw, qs).view(np.uint16))
 
 
+# (M, K, N, epilogue): the pi0.5 prefill GEMMs at P = 968 (q/k/v, o_proj + residual, gate_up
+# + GeGLU, down + residual), then ragged shapes (M and N tails, short K)
+TILE_SHAPES = [(968, 2048, 2560, 0), (968, 2048, 2048, 1), (968, 2048, 16384, 2), (968, 16384, 2048, 1),
+               (37, 192, 100, 0), (300, 1024, 260, 1), (300, 512, 384, 2), (1000, 4096, 512, 1), (5, 64, 128, 2)]
+
+
+@pytest.mark.parametrize("m,k,n,epi", TILE_SHAPES)
+@pytest.mark.parametrize("small", [0, 1], ids=["tile256", "tile128"])
+def test_tile_linear_vs_exact(m, k, n, epi, small):
+    """The prefill GEMM: exact fp16 products accumulated in fp32, one fp16 rounding (then the
+    residual add, or gelu_tanh(gate) * up, in fp16), against the float64 product on the
+    GPU.  The fp32 accumulation error is bounded by 8 eps32 sqrt(K) ||x_m * w_n||_2."""
+    print(f"tile linear M={m} K={k} N={n} epi={epi} small={small}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(m * 31 + k + n + epi)
+    rows = 2 * n if epi == 2 else n
+    x = torch.randn((m, k), generator=g, device="cuda").half()
+    w = (torch.randn((rows, k), generator=g, device="cuda") / k ** 0.5).half()
+    y0 = torch.randn((m, n), generator=g, device="cuda").half()
+    y = y0.clone() if epi == 1 else torch.empty((m, n), dtype=torch.float16, device="cuda")
+    N.call("mlcv_tile_linear", _p(x), m, k, _p(w), n, _p(y), epi, small, _st())
+    exact = x.double() @ w.double().T
+    slack = 8 * 2.0 ** -24 * k ** 0.5 * ((x.double() ** 2) @ (w.double() ** 2).T).sqrt()
+    got = y.double()
+    ulp = lambda t: torch.from_numpy(_ulp16(t.cpu().numpy())).cuda()  # noqa: E731
+    if epi == 2:
+        gate, up = exact[:, :n], exact[:, n:]
+        g16, u16 = gate.half(), up.half()
+        gl = torch.from_numpy(O.gelu_tanh(g16.float().cpu().numpy())).cuda().half()
+        ref = (gl.double() * u16.double()).half().double()
+        # one ulp of gate / up from the accumulation moves the result by about one ulp of
+        # each factor's share, plus the two fp16 roundings
+        bound = 2 * ulp(ref) + 2 * ulp(gl.double()) * up.abs() + 2 * ulp(g16.double()) * up.abs() * 1.2 + \
+            gl.double().abs() * (ulp(u16.double()) + slack[:, n:]) + up.abs() * 1.2 * slack[:, :n]
+        err = (got - ref).abs()
+    else:
+        pre16 = exact.half().double()
+        target = exact + (y0.double() if epi == 1 else 0.0)
+        bound = 0.5 * ulp(pre16) + slack + (0.5 * ulp(got) if epi == 1 else 0.0) + 0.5 * ulp(pre16)
+        err = (got - target).abs()
+    assert torch.isfinite(got).all()
+    assert bool((err <= bound).all()), float((err / bound).max())
+    assert cosine(got.cpu().numpy(), (ref if epi == 2 else target).cpu().numpy()) > 0.99999
+
+
 LIN_SHAPES = [(1, 1024, 3072), (50, 1024, 2560), (50, 2048, 1024), (50, 4096, 1024), (8, 32, 128), (50, 1024, 32),
               (100, 256, 64), (4, 64, 16)]
 
