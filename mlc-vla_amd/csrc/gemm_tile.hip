@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(TgArgs a, int mtiles, in
         const int j = tn * 64 + 32 * wn + l32;
         const _Float16 gv = f2h(acc[bm][0][e]);
         const _Float16 uv = f2h(acc[bm][1][e]);
-        a.c[(size_t)m * a.ldc + j] = hmul(f2h(gelu_tanh(h2f(gv))), uv);
+        a.c[(size_t)m * a.ldc + j] = hmul(f2h(gelu_tanh_hw(h2f(gv))), uv);
         continue;
       }
 #pragma unroll
@@ -184,12 +184,14 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l32 = lane & 31, lh = lane >> 5;
   const int wm = w >> 1, wn = w & 1;
-  // tile and K slice; the S slices of a tile share the XCD (id % 8)
+  // tile and K slice: XCD x (id % 8) owns the consecutive tiles [x per, (x + 1) per), all
+  // M tiles of an N tile together, so each weight tile is fetched into one L2; the S
+  // slices of a tile share the XCD
   const int id = blockIdx.x, xcd = id % NXCD, j = id / NXCD;
   const int S = SPLIT ? p.splitk : 1;
   const int s = j % S, tl = j / S;
-  const int tile = tl * NXCD + xcd;
-  const int ntile_all = p.mtiles * p.ntiles;
+  const int ntile_all = p.mtiles * p.ntiles, per = (ntile_all + NXCD - 1) / NXCD;
+  const int tile = xcd * per + tl;
   if (tile >= ntile_all) return;
   const int tm = tile % p.mtiles, tn = tile / p.mtiles;
   const int m0 = tm * GBM;
@@ -298,7 +300,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const _Float16 gv = f2h(acc[2 * hb][mb][4 * q + i]), uv = f2h(acc[2 * hb + 1][mb][4 * q + i]);
-            y[i] = hmul(f2h(gelu_tanh(h2f(gv))), uv);
+            y[i] = hmul(f2h(gelu_tanh_hw(h2f(gv))), uv);
           }
           *reinterpret_cast<h4*>(a.c + (size_t)m * a.ldc + jo) = y;
         }
