@@ -170,6 +170,16 @@ struct GemmPlan {
   unsigned* sync;          // per tile: 32 words (arrivals, generation)
 };
 
+// 16 bytes per lane from a buffer into LDS at lds + 16 lane.  The builtin is only given to
+// the device pass: in the host pass it makes clang drop the launch stubs of the kernels
+// that use it, without a diagnostic.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, __attribute__((address_space(3))) void* lds,
+                                                int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+#endif
+}
+
 __device__ __forceinline__ int lds_swz(int r, int p) { return (r >> 3) * 1024 + (r & 7) * 128 + ((p ^ (r & 7)) << 4); }
 
 template <int BN, int EPI, bool SPLIT>
@@ -179,9 +189,8 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   constexpr int STG = ASZ + BSZ;
   __shared__ __attribute__((aligned(16))) char lds[2 * STG];
   typedef __attribute__((address_space(3))) void* lptr_t;
-  typedef const __attribute__((address_space(1))) void* gptr_t;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, lh = lane >> 5;
   const int wm = w >> 1, wn = w & 1;
   // tile and K slice: XCD x (id % 8) owns the consecutive tiles [x per, (x + 1) per), all
@@ -197,39 +206,51 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   const int m0 = tm * GBM;
   const int kt0 = s * p.kt_per, nkt = min(p.kt_per, a.K / GBK - kt0);
 
-  // per-lane global row pointers of this wave's DMA rows: A rows [64 w, +64), B rows
-  // [BN/4 w, +BN/4), 8 rows per instruction
+  // DMA of this wave's rows: A rows [64 w, +64), B rows [BN/4 w, +BN/4), 8 rows per
+  // instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in the
+  // scalar offset; rows past the operand read zeros (the buffer's size)
   constexpr int NAI = 8, NBI = BN / 32;
   const int lr = lane >> 3, pc = (lane & 7) ^ lr;  // row in the 8, and its piece
-  const _Float16* ag[NAI];
-  const _Float16* bg[NBI];
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(a.a), 0, (int)min((size_t)a.M * a.lda * 2, (size_t)0x7fffffff), 0x00020000);
+  int aoff[NAI];
 #pragma unroll
-  for (int i = 0; i < NAI; ++i) {
-    const int m = min(m0 + 64 * w + 8 * i + lr, a.M - 1);
-    ag[i] = a.a + (size_t)m * a.lda + pc * 8;
-  }
+  for (int i = 0; i < NAI; ++i) aoff[i] = ((m0 + 64 * w + 8 * i + lr) * a.lda + pc * 8) * 2;
+  const _Float16* bbase[NBI];  // per instruction (wave-uniform): segment base and bytes
+  int bbytes[NBI], boff[NBI];
 #pragma unroll
   for (int i = 0; i < NBI; ++i) {
-    const int r = (BN / 4) * w + 8 * i + lr;  // B tile row
+    const int r0 = (BN / 4) * w + 8 * i;  // first B tile row of the instruction (uniform)
+    const _Float16* base;
+    int rows, row;
     if constexpr (EPI == TG_GEGLU) {
       // wave half wn holds 64 outputs as [gate 32, up 32, gate 32, up 32]
-      const int hw = r / (BN / 2), blk = (r % (BN / 2)) / 32, jj = r % 32;
-      const int jo = tn * (BN / 2) + hw * (BN / 4) + (blk >> 1) * 32 + jj;
-      bg[i] = a.b0 + (size_t)((blk & 1) ? a.F + jo : jo) * a.ldb + pc * 8;
+      const int hw = r0 / (BN / 2), blk = (r0 % (BN / 2)) / 32;
+      const int jo = tn * (BN / 2) + hw * (BN / 4) + (blk >> 1) * 32 + (r0 % 32);
+      base = a.b0;
+      rows = 2 * a.F;
+      row = ((blk & 1) ? a.F + jo : jo) + lr;
     } else {
-      const int n = min(tn * BN + r, a.N - 1);
-      bg[i] = brow_ptr(a, n) + pc * 8;
+      const int n0 = tn * BN + r0;  // segment boundaries are multiples of 8
+      const int seg0 = n0 < a.n1 ? 0 : n0 < a.n2 ? a.n1 : a.n2;
+      base = n0 < a.n1 ? a.b0 : n0 < a.n2 ? a.b1 : a.b2;
+      rows = (n0 < a.n1 ? a.n1 : n0 < a.n2 ? a.n2 : a.N) - seg0;
+      row = n0 - seg0 + lr;
     }
+    bbase[i] = base;
+    bbytes[i] = (int)min((size_t)rows * a.ldb * 2, (size_t)0x7fffffff);
+    boff[i] = (row * a.ldb + pc * 8) * 2;
   }
   auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
     char* sb = lds + stage * STG;
-    const int ko = (kt0 + kt) * GBK;
+    const int ko = (kt0 + kt) * GBK * 2;
 #pragma unroll
     for (int i = 0; i < NAI; ++i)
-      __builtin_amdgcn_global_load_lds((gptr_t)(ag[i] + ko), (lptr_t)(sb + (8 * w + i) * 1024), 16, 0, 0);
+      buffer_to_lds16(rA, (lptr_t)(sb + (8 * w + i) * 1024), aoff[i], ko);
 #pragma unroll
     for (int i = 0; i < NBI; ++i)
-      __builtin_amdgcn_global_load_lds((gptr_t)(bg[i] + ko), (lptr_t)(sb + ASZ + ((BN / 32) * w + i) * 1024), 16, 0, 0);
+      buffer_to_lds16(__builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i]), 0, bbytes[i], 0x00020000),
+                      (lptr_t)(sb + ASZ + ((BN / 32) * w + i) * 1024), boff[i], ko);
   };
 
   f16v acc[NBW][4];
@@ -240,26 +261,34 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[nb][mb][e] = 0.f;
 
+  // operand fragments of k step kb (16 k): weights of the wave's n blocks, X of its m blocks
+  auto ldfrag = [&](const char* sa, int kb, h8* wf, h8* xf) __attribute__((always_inline)) {
+    const int pp = 2 * kb + lh;
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb)
+      wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz(wn * (BN / 2) + nb * 32 + l32, pp));
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz(wm * 128 + mb * 32 + l32, pp));
+  };
+
   if (nkt > 0) dma(0, 0);
   for (int kt = 0; kt < nkt; ++kt) {
     wait_all_memory();  // this wave's DMA of tile kt has landed in LDS
     __syncthreads();    // every wave's has; stage kt+1 is no longer read
     if (kt + 1 < nkt) dma(kt + 1, (kt + 1) & 1);
     const char* sa = lds + (kt & 1) * STG;
-    const char* sbb = sa + ASZ;
+    // the fragments of k step kb + 1 are read while step kb multiplies
+    h8 wf[2][NBW], xf[2][4];
+    ldfrag(sa, 0, wf[0], xf[0]);
 #pragma unroll
     for (int kb = 0; kb < GBK / 16; ++kb) {
-      const int pp = 2 * kb + lh;
-      h8 wf[NBW], xf[4];
-#pragma unroll
-      for (int nb = 0; nb < NBW; ++nb)
-        wf[nb] = *reinterpret_cast<const h8*>(sbb + lds_swz(wn * (BN / 2) + nb * 32 + l32, pp));
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz(wm * 128 + mb * 32 + l32, pp));
+      if (kb + 1 < GBK / 16) ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[nb], xf[mb], acc[nb][mb]);
+        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[kb & 1][nb], xf[kb & 1][mb], acc[nb][mb]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -377,6 +406,7 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
     p.ntiles = a.F / 128;
   } else {
     if (a.N % 4 != 0) return false;
+    if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
     p.bn = 128;
     p.ntiles = (a.N + 127) / 128;
   }
