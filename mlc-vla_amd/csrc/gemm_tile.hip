@@ -180,14 +180,40 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, __attr
 #endif
 }
 
-__device__ __forceinline__ int lds_swz(int r, int p) { return (r >> 3) * 1024 + (r & 7) * 128 + ((p ^ (r & 7)) << 4); }
+// LDS image of a row-major operand tile of BK halfs per row: one 1 KB DMA instruction holds
+// RPI = 512 / BK rows, row r's 16-byte piece p sits in slot p ^ swz(r) of the row.  The
+// MFMA operand read (consecutive lanes = consecutive rows, one piece) then hits distinct
+// banks: BK 64 (128-byte rows) swizzles by r mod 8, BK 32 (64-byte rows, 4 per 256 bytes
+// of banks) by (r / 4) mod 4.
+template <int BK>
+__device__ __forceinline__ int tile_swz(int r) { return BK == 64 ? (r & 7) : ((r >> 2) & 3); }
+template <int BK>
+__device__ __forceinline__ int lds_swz(int r, int p) {
+  constexpr int RPI = 512 / BK;
+  return (r / RPI) * 1024 + (r % RPI) * (BK * 2) + ((p ^ tile_swz<BK>(r)) << 4);
+}
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+// LDS barrier without a wait for outstanding global loads (the DMA of later stages)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
-template <int BN, int EPI, bool SPLIT>
+template <int BN, int BK, int NST, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   constexpr int NBW = BN / 64;                  // n blocks of 32 per wave
-  constexpr int ASZ = GBM * GBK * 2, BSZ = BN * GBK * 2;
+  constexpr int ASZ = GBM * BK * 2, BSZ = BN * BK * 2;
   constexpr int STG = ASZ + BSZ;
-  __shared__ __attribute__((aligned(16))) char lds[2 * STG];
+  constexpr int RPI = 512 / BK, LPR = BK / 8;   // rows per DMA instruction, lanes per row
+  __shared__ __attribute__((aligned(16))) char lds[NST * STG];
   typedef __attribute__((address_space(3))) void* lptr_t;
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -204,23 +230,23 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   if (tile >= ntile_all) return;
   const int tm = tile % p.mtiles, tn = tile / p.mtiles;
   const int m0 = tm * GBM;
-  const int kt0 = s * p.kt_per, nkt = min(p.kt_per, a.K / GBK - kt0);
+  const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg) / BK;
 
   // DMA of this wave's rows: A rows [64 w, +64), B rows [BN/4 w, +BN/4), 8 rows per
   // instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in the
   // scalar offset; rows past the operand read zeros (the buffer's size)
-  constexpr int NAI = 8, NBI = BN / 32;
-  const int lr = lane >> 3, pc = (lane & 7) ^ lr;  // row in the 8, and its piece
+  constexpr int NAI = GBM / RPI / 4, NBI = BN / RPI / 4, NI = NAI + NBI;
+  const int lr = lane / LPR, pc = (lane % LPR) ^ tile_swz<BK>(lr);  // row in the instruction, its piece
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<_Float16*>(a.a), 0, (int)min((size_t)a.M * a.lda * 2, (size_t)0x7fffffff), 0x00020000);
   int aoff[NAI];
 #pragma unroll
-  for (int i = 0; i < NAI; ++i) aoff[i] = ((m0 + 64 * w + 8 * i + lr) * a.lda + pc * 8) * 2;
+  for (int i = 0; i < NAI; ++i) aoff[i] = ((m0 + (NAI * w + i) * RPI + lr) * a.lda + pc * 8) * 2;
   const _Float16* bbase[NBI];  // per instruction (wave-uniform): segment base and bytes
   int bbytes[NBI], boff[NBI];
 #pragma unroll
   for (int i = 0; i < NBI; ++i) {
-    const int r0 = (BN / 4) * w + 8 * i;  // first B tile row of the instruction (uniform)
+    const int r0 = (NBI * w + i) * RPI;  // first B tile row of the instruction (uniform)
     const _Float16* base;
     int rows, row;
     if constexpr (EPI == TG_GEGLU) {
@@ -241,16 +267,20 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     bbytes[i] = (int)min((size_t)rows * a.ldb * 2, (size_t)0x7fffffff);
     boff[i] = (row * a.ldb + pc * 8) * 2;
   }
-  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+  // DMA instruction i (A rows for i < NAI, then B rows) of k tile kt into a stage
+  auto dma1 = [&](int i, int kt, int stage) __attribute__((always_inline)) {
     char* sb = lds + stage * STG;
-    const int ko = (kt0 + kt) * GBK * 2;
+    const int ko = (kbeg + kt * BK) * 2;
+    if (i < NAI)
+      buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), aoff[i], ko);
+    else
+      buffer_to_lds16(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i - NAI]), 0, bbytes[i - NAI], 0x00020000),
+          (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), boff[i - NAI], ko);
+  };
+  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < NAI; ++i)
-      buffer_to_lds16(rA, (lptr_t)(sb + (8 * w + i) * 1024), aoff[i], ko);
-#pragma unroll
-    for (int i = 0; i < NBI; ++i)
-      buffer_to_lds16(__builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i]), 0, bbytes[i], 0x00020000),
-                      (lptr_t)(sb + ASZ + ((BN / 32) * w + i) * 1024), boff[i], ko);
+    for (int i = 0; i < NI; ++i) dma1(i, kt, stage);
   };
 
   f16v acc[NBW][4];
@@ -266,29 +296,48 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     const int pp = 2 * kb + lh;
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
-      wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz(wn * (BN / 2) + nb * 32 + l32, pp));
+      wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz<BK>(wn * (BN / 2) + nb * 32 + l32, pp));
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz(wm * 128 + mb * 32 + l32, pp));
+    for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz<BK>(wm * 128 + mb * 32 + l32, pp));
   };
 
-  if (nkt > 0) dma(0, 0);
+  // NST-stage ring: the DMA of tiles kt+1 .. kt+NST-2 stays in flight while tile kt
+  // multiplies; tile kt+NST-1 goes into the stage tile kt-1 used
+#pragma unroll
+  for (int t = 0; t < NST - 1; ++t)
+    if (t < nkt) dma(t, t);
   for (int kt = 0; kt < nkt; ++kt) {
-    wait_all_memory();  // this wave's DMA of tile kt has landed in LDS
-    __syncthreads();    // every wave's has; stage kt+1 is no longer read
-    if (kt + 1 < nkt) dma(kt + 1, (kt + 1) & 1);
-    const char* sa = lds + (kt & 1) * STG;
-    // the fragments of k step kb + 1 are read while step kb multiplies
+    // this wave's DMA of tile kt has landed (loads complete in issue order); at the end of
+    // the K range fewer later tiles are in flight, so wait for all
+    if (kt + NST - 2 < nkt) vm_wait<(NST - 2) * NI>();
+    else vm_wait<0>();
+    lds_barrier();  // every wave's has, and nobody reads tile kt-1's stage any more
+    const bool more = kt + NST - 1 < nkt;
+    const int knext = kt + NST - 1, snext = (kt + NST - 1) % NST;
+    const char* sa = lds + (kt % NST) * STG;
+    // the fragments of k step kb + 1 are read while step kb multiplies; the DMA
+    // instructions of tile kt+NST-1 are spread between the MFMA groups (issued in one
+    // burst, a busy memory pipeline holds the wave at issue while its MFMA unit idles)
+    constexpr int NP = (BK / 16) * NBW;  // MFMA groups of 4 per tile
     h8 wf[2][NBW], xf[2][4];
     ldfrag(sa, 0, wf[0], xf[0]);
 #pragma unroll
-    for (int kb = 0; kb < GBK / 16; ++kb) {
-      if (kb + 1 < GBK / 16) ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
+    for (int kb = 0; kb < BK / 16; ++kb) {
+      if (kb + 1 < BK / 16) ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int nb = 0; nb < NBW; ++nb)
+      for (int nb = 0; nb < NBW; ++nb) {
+        const int piece = kb * NBW + nb;
+        if (more) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+            if ((i * NP) / NI == piece) dma1(i, knext, snext);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[kb & 1][nb], xf[kb & 1][mb], acc[nb][mb]);
-      __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
@@ -431,13 +480,14 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
 int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   const int tiles = p.mtiles * p.ntiles;
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
-  if (a.epi == TG_GEGLU) big_gemm_kernel<256, TG_GEGLU, false><<<blocks, 256, 0, st>>>(a, p);
+  // 256 x 256 tiles: 4 stages of 32 k (128 KB); 256 x 128: 3 stages of 64 k (144 KB)
+  if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false><<<blocks, 256, 0, st>>>(a, p);
   else if (p.splitk > 1) {
-    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
-    else big_gemm_kernel<128, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, 64, 3, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<128, 64, 3, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
   } else {
-    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, TG_RESIDUAL, false><<<blocks, 256, 0, st>>>(a, p);
-    else big_gemm_kernel<128, TG_STORE, false><<<blocks, 256, 0, st>>>(a, p);
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, 64, 3, TG_RESIDUAL, false><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<128, 64, 3, TG_STORE, false><<<blocks, 256, 0, st>>>(a, p);
   }
   MLCV_HIP(hipGetLastError());
   return 0;
