@@ -456,8 +456,11 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
   } else {
     if (a.N % 4 != 0) return false;
     if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
-    p.bn = 128;
-    p.ntiles = (a.N + 127) / 128;
+    // long K (down_proj): 256 x 256 tiles over up to 8 K slices load a third less through
+    // L2 than 256 x 128 tiles over 4; shorter K keeps 256 x 128 tiles
+    p.bn = (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N))
+               ? 256 : 128;
+    p.ntiles = (a.N + p.bn - 1) / p.bn;
   }
   p.mtiles = (a.M + GBM - 1) / GBM;
   const int tiles = p.mtiles * p.ntiles, kts = a.K / GBK;
@@ -482,7 +485,10 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
   // 256 x 256 tiles: 4 stages of 32 k (128 KB); 256 x 128: 3 stages of 64 k (144 KB)
   if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false><<<blocks, 256, 0, st>>>(a, p);
-  else if (p.splitk > 1) {
+  else if (p.bn == 256) {
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<256, 32, 4, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<256, 32, 4, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+  } else if (p.splitk > 1) {
     if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, 64, 3, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
     else big_gemm_kernel<128, 64, 3, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
   } else {
@@ -496,8 +502,8 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
 }  // namespace
 
 size_t tg_sync_words() { return (size_t)std::max(device_cus(), 1) * 32; }
-// one 256 x 128 fp32 partial per CU
-size_t tg_ws_floats() { return (size_t)std::max(device_cus(), 1) * GBM * 128; }
+// one 256 x 256 fp32 partial per CU
+size_t tg_ws_floats() { return (size_t)std::max(device_cus(), 1) * GBM * 256; }
 
 int tg_launch(const TgArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.K % 8 == 0 && a.lda % 8 == 0 && a.ldb % 8 == 0, "tile GEMM needs 16-byte aligned rows");
