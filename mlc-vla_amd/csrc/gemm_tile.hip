@@ -433,19 +433,6 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   }
 }
 
-// compute units of the current device (cached per device)
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // 256-row tile plan; false = the shape needs the 128 x 128 kernel
 bool big_plan(const TgArgs& a, GemmPlan& p) {
   if (a.small_tiles || a.K % GBK != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
@@ -500,6 +487,18 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
 }
 
 }  // namespace
+
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
 
 size_t tg_sync_words() { return (size_t)std::max(device_cus(), 1) * 32; }
 // one 256 x 256 fp32 partial per CU

@@ -245,6 +245,8 @@ struct TgArgs {
   int sync_tiles;
   int small_tiles;       // 1: the 128 x 128 tile kernel only
 };
+// compute units of the current device (cached per device; 0 if it cannot be queried)
+int device_cus();
 // words of meeting counters and floats of partials the 256-row tile path can use
 size_t tg_sync_words();
 size_t tg_ws_floats();
