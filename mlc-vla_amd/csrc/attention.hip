@@ -775,7 +775,75 @@ __global__ void kv_writer_kernel(const _Float16* __restrict__ qkv, int ld, int k
   vo[i + half] = vr[i + half];
 }
 
-// plain Gemma RMSNorm: out = fp16(x / sqrt(mean(x^2) + eps) * (1 + w)), one block per row
+// the same with 4 consecutive dims per thread (hd % 8 == 0, ld, koff, voff multiples of 4)
+__global__ void kv_writer4_kernel(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
+                                  const float* __restrict__ cosb, const float* __restrict__ sinb, int P, int KV, int hd,
+                                  float* __restrict__ keys, _Float16* __restrict__ values) {
+  const int half = hd / 2, q4 = half / 4;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)P * KV * q4;
+  if (idx >= total) return;
+  const int i = (int)(idx % q4) * 4;
+  const int kvh = (int)((idx / q4) % KV);
+  const int p = (int)(idx / ((long)q4 * KV));
+  const _Float16* kr = qkv + (size_t)p * ld + koff + (size_t)kvh * hd;
+  const _Float16* vr = qkv + (size_t)p * ld + voff + (size_t)kvh * hd;
+  const f4 c = *reinterpret_cast<const f4*>(cosb + (size_t)p * half + i);
+  const f4 sn = *reinterpret_cast<const f4*>(sinb + (size_t)p * half + i);
+  const h4 a = *reinterpret_cast<const h4*>(kr + i), b = *reinterpret_cast<const h4*>(kr + i + half);
+  f4 o1, o2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x1 = h2f(a[e]), x2 = h2f(b[e]);
+    o1[e] = x1 * c[e] - x2 * sn[e];
+    o2[e] = x2 * c[e] + x1 * sn[e];
+  }
+  float* ko = keys + ((size_t)kvh * P + p) * hd;
+  _Float16* vo = values + ((size_t)kvh * P + p) * hd;
+  *reinterpret_cast<f4*>(ko + i) = o1;
+  *reinterpret_cast<f4*>(ko + i + half) = o2;
+  *reinterpret_cast<h4*>(vo + i) = *reinterpret_cast<const h4*>(vr + i);
+  *reinterpret_cast<h4*>(vo + i + half) = *reinterpret_cast<const h4*>(vr + i + half);
+}
+
+// plain Gemma RMSNorm: out = fp16(x / sqrt(mean(x^2) + eps) * (1 + w)), one block per row.
+// Rows of at most 256 x 8 x NP halfs (dim % 8 == 0) stay in registers between the two
+// passes, one 16-byte load per piece.
+template <int NP>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const _Float16* __restrict__ x, const _Float16* __restrict__ w,
+                                                          _Float16* __restrict__ out, int dim, float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, tid = threadIdx.x, n8 = dim / 8;
+  const _Float16* xr = x + (size_t)r * dim;
+  h8 v[NP];
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = tid + 256 * p;
+    v[p] = i < n8 ? *reinterpret_cast<const h8*>(xr + 8 * i) : (h8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = h2f(v[p][e]);
+      ss += f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float dn = sqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = tid + 256 * p;
+    if (i >= n8) break;
+    const h8 wv = *reinterpret_cast<const h8*>(w + 8 * i);
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = f2h(h2f(v[p][e]) / dn * (1.0f + h2f(wv[e])));
+    *reinterpret_cast<h8*>(out + (size_t)r * dim + 8 * i) = o;
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const _Float16* __restrict__ x, const _Float16* __restrict__ w,
                                                       _Float16* __restrict__ out, int dim, float eps) {
   __shared__ float red[4];
@@ -959,16 +1027,30 @@ int attn_img_prep_launch(const void* keys, int k_f32, const _Float16* values, co
 
 int kv_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin, int P,
                      int KV, int hd, float* keys, _Float16* values, hipStream_t st) {
-  const long total = (long)P * KV * (hd / 2);
-  kv_writer_kernel<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(qkv, ld, koff, voff, cos, sin, P, KV, hd, keys,
-                                                                     values);
+  const bool vec = hd % 8 == 0 && ld % 4 == 0 && koff % 4 == 0 && voff % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(keys) |
+                     reinterpret_cast<uintptr_t>(values) | reinterpret_cast<uintptr_t>(cos) |
+                     reinterpret_cast<uintptr_t>(sin)) & 15) == 0;
+  if (vec) {
+    const long total = (long)P * KV * (hd / 8);
+    kv_writer4_kernel<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(qkv, ld, koff, voff, cos, sin, P, KV, hd, keys,
+                                                                        values);
+  } else {
+    const long total = (long)P * KV * (hd / 2);
+    kv_writer_kernel<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(qkv, ld, koff, voff, cos, sin, P, KV, hd, keys,
+                                                                       values);
+  }
   MLCV_HIP(hipGetLastError());
   return 0;
 }
 
 int rmsnorm_launch(const _Float16* x, const _Float16* w, _Float16* out, int rows, int dim, float eps,
                    hipStream_t st) {
-  rmsnorm_kernel<<<rows, 256, 0, st>>>(x, w, out, dim, eps);
+  const bool vec = dim % 8 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                      reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (vec && dim <= 256 * 8) rmsnorm_vec_kernel<1><<<rows, 256, 0, st>>>(x, w, out, dim, eps);
+  else if (vec && dim <= 256 * 8 * 4) rmsnorm_vec_kernel<4><<<rows, 256, 0, st>>>(x, w, out, dim, eps);
+  else rmsnorm_kernel<<<rows, 256, 0, st>>>(x, w, out, dim, eps);
   MLCV_HIP(hipGetLastError());
   return 0;
 }
