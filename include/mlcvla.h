@@ -88,6 +88,18 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
                  void* stream);
 
+/* denoise_step -- Pi0Model.denoise_step (pi0_model.py:111-125), the joint prefix + suffix
+ * ("M0") velocity that get_default_spec exports as "denoise_step" (pi0_model.py:221-225):
+ *   prefix_embs [1,P,vlm_width] f16, x_t [1,T,A] f16, time_emb [1, ae_width] f16
+ *   ->  v_out [1,T,A] f32.
+ * Every prefix token is valid, and the RoPE positions run over 0..P+T-1
+ * (pi0_model.py:113-115).  The prefix rows attend the prefix only and the suffix rows
+ * attend all (the mask of _build_additive_mask, pi0_model.py:29-41). So the forward is
+ * the prefix expert over the prefix, whose per-layer K/V go to the context's cache, then the
+ * suffix path over that cache, in one graph.  Overwrites the context's prefill cache. */
+int mlcv_denoise_step(mlcv_ctx* ctx, const void* prefix_embs, const void* x_t, const void* time_emb, float* v_out,
+                      void* stream);
+
 /* denoise_step_kv -- Pi0Model.denoise_step_kv (pi0_model.py:142-163).
  *   keys f32 / values f16 as produced by prefill, x_t [1,T,A] f16,
  *   time_emb [1, ae_width] f16, suffix_cos / suffix_sin [1,T,1,hd/2] f32,

@@ -162,6 +162,8 @@ struct Ctx {
   // prefill path
   _Float16 *px, *pxn, *pqkv, *pctx, *ph, *pvalues;
   float *pcos, *psin, *pkeys;
+  // the joint forward (denoise_step): suffix RoPE tables at positions P..P+T-1, all-valid mask
+  float *m0cos = nullptr, *m0sin = nullptr, *m0mask = nullptr;
   // workspaces
   float* skws = nullptr;
   size_t skws_floats = 0;
@@ -209,10 +211,10 @@ struct Ctx {
   size_t ncounters_side = 0;
 
   hipStream_t cap = nullptr;
-  Graph g_step, g_loop, g_prefill, g_chunk;
+  Graph g_step, g_loop, g_prefill, g_chunk, g_m0;
 
   void drop_graphs() {
-    for (Graph* g : {&g_step, &g_loop, &g_prefill, &g_chunk}) {
+    for (Graph* g : {&g_step, &g_loop, &g_prefill, &g_chunk, &g_m0}) {
       if (g->exec) (void)hipGraphExecDestroy(g->exec);
       g->exec = nullptr;
       g->key.clear();
@@ -785,18 +787,26 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.pkeys, (size_t)c.D * kv_slice(c));
   ALLOC(c.pvalues, (size_t)c.D * kv_slice(c));
 
-  // prefix RoPE tables: radians = pos / theta^((2/hd) i) in float64, cast to float32
+  ALLOC(c.m0cos, (size_t)T * hd / 2);
+  ALLOC(c.m0sin, (size_t)T * hd / 2);
+  ALLOC(c.m0mask, P);
+  // RoPE tables of positions 0..P+T-1: radians = pos / theta^((2/hd) i) in float64, cast to
+  // float32; rows 0..P-1 are the prefill's, rows P..P+T-1 the joint forward's suffix rows
   {
-    std::vector<float> hc(P * hd / 2), hs(P * hd / 2);
-    for (size_t p = 0; p < P; ++p)
+    std::vector<float> hc((P + T) * hd / 2), hs((P + T) * hd / 2);
+    for (size_t p = 0; p < P + T; ++p)
       for (int i = 0; i < hd / 2; ++i) {
         const double ts = std::pow((double)cfg->rope_theta, (2.0 / hd) * i);
         const double rad = (double)p / ts;
         hc[p * (hd / 2) + i] = (float)std::cos(rad);
         hs[p * (hd / 2) + i] = (float)std::sin(rad);
       }
-    if (hipMemcpy(c.pcos, hc.data(), hc.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(c.psin, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    const size_t np = (size_t)P * hd / 2, ns = (size_t)T * hd / 2;
+    if (hipMemcpy(c.pcos, hc.data(), np * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c.psin, hs.data(), np * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c.m0cos, hc.data() + np, ns * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c.m0sin, hs.data() + np, ns * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(c.m0mask, 0, (size_t)P * 4) != hipSuccess) {
       set_error("copy of rope tables failed");
       return fail(-1);
     }
@@ -1097,6 +1107,29 @@ static void suffix_jobs(const Ctx& c, const float* cos, const float* sin, const 
   jobs.push_back({cos, c.cos, (size_t)c.T * half * 4});
   jobs.push_back({sin, c.sin, (size_t)c.T * half * 4});
   jobs.push_back({mask, c.mask, (size_t)c.P * 4});
+}
+
+int mlcv_denoise_step(mlcv_ctx* ctx, const void* prefix_embs, const void* x_t, const void* time_emb, float* v_out,
+                      void* stream) {
+  MLCV_REQUIRE(ctx && prefix_embs && x_t && time_emb && v_out, "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.bound, "parameters not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  std::vector<CopyJob> jobs = {{prefix_embs, c.px, (size_t)c.P * c.W0 * 2},
+                               {x_t, c.xin16, (size_t)c.T * c.A * 2},
+                               {time_emb, c.te, (size_t)c.W1 * 2}};
+  suffix_jobs(c, c.m0cos, c.m0sin, c.m0mask, jobs);
+  MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
+  MLCV_TRY(run_graph(c, c.g_m0, {},
+                     [&](hipStream_t s) {
+                       MLCV_TRY(enqueue_prefill(c, c.pkeys, c.pvalues, s));
+                       c.use_img = false;
+                       MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
+                       return enqueue_step(c, c.pkeys, c.pvalues, c.mod, false, s, c.fork_mod);
+                     },
+                     st));
+  MLCV_HIP(hipMemcpyAsync(v_out, c.vout, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  return 0;
 }
 
 int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, const void* x_t, const void* time_emb,

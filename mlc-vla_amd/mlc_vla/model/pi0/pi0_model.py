@@ -121,6 +121,11 @@ def get_default_spec(config: Pi0Config, functions: Optional[Sequence[str]] = Non
     rope = (1, config.suffix_len, 1, vlm.head_dim // 2)
     act = (1, config.action_horizon, config.action_dim)
     spec = {
+        "denoise_step": {
+            "prefix_embs": TensorSpec((1, config.prefix_len, vlm.width), dt),
+            "x_t": TensorSpec(act, dt),
+            "time_emb": TensorSpec((1, ae.width), dt),
+        },
         "prefill": {
             "prefix_embs": TensorSpec((1, config.prefix_len, vlm.width), dt),
             "prefix_mask": TensorSpec(pm, "float32"),

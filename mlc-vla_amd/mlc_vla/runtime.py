@@ -142,7 +142,7 @@ class Executable:
 
 
 class VirtualMachine:
-    """``vm["prefill" | "denoise_step_kv" | "denoise_loop_kv" | "chunk"](*tensors, params)``."""
+    """``vm["denoise_step" | "prefill" | "denoise_step_kv" | "denoise_loop_kv" | "chunk"](*tensors, params)``."""
 
     def __init__(self, ex: Executable, dev: Optional[Device] = None):
         self.ex = ex
@@ -205,13 +205,22 @@ class VirtualMachine:
         return out
 
     def __getitem__(self, name: str):
-        fns = {"prefill": self.prefill, "denoise_step_kv": self.denoise_step_kv,
+        fns = {"denoise_step": self.denoise_step, "prefill": self.prefill, "denoise_step_kv": self.denoise_step_kv,
                "denoise_loop_kv": self.denoise_loop_kv, "chunk": self.chunk}
         if name not in fns:
             raise KeyError(f"function {name!r} is not built (available: {sorted(fns)})")
         return fns[name]
 
     # exported functions ------------------------------------------------------
+    def denoise_step(self, prefix_embs, x_t, time_emb, params):
+        """The joint prefix + suffix velocity (Pi0Model.denoise_step, pi0_model.py:111-125):
+        every prefix token valid, RoPE positions 0..P+T-1; returns v [1,T,A] f32."""
+        self._bind(params)
+        a = self._args("denoise_step", (prefix_embs, x_t, time_emb))
+        v = empty(a[1].shape, "float32", self.dev)
+        N.call("mlcv_denoise_step", self._ctx, *[_ptr(t) for t in a], _ptr(v), self._stream())
+        return v
+
     def prefill(self, prefix_embs, prefix_mask, params):
         self._bind(params)
         pe, pm = self._args("prefill", (prefix_embs, prefix_mask))

@@ -125,6 +125,29 @@ def test_m1_vs_m0_joint_forward(tiny):
     _tol(got, ref)
 
 
+@pytest.mark.parametrize("which", ["tiny", "dummy"])
+def test_denoise_step_joint_vs_m0_oracle_and_m1(which, tiny, dummy):
+    """vm["denoise_step"] (Pi0Model.denoise_step, the joint prefix + suffix forward, all prefix
+    tokens valid) against the float64 torch joint forward, and against the M1 path on the GPU
+    (prefill + denoise_step_kv with suffix RoPE positions P..P+T-1): compare_kv's gate.  The M1
+    tables come from numpy's float64 cos/sin and the joint forward's from the C library, which
+    may differ in the last float32 ulp, so M1 is compared to a tight tolerance, not bitwise."""
+    m = tiny if which == "tiny" else dummy
+    te = np.random.default_rng(6).standard_normal((1, m.cfg.action_expert.width)).astype(np.float16)
+    got = m.runner.vm["denoise_step"](m.dev(m.prefix), m.dev(m.x_t), m.dev(te), m.params).numpy()
+    assert got.shape == (1, m.cfg.action_horizon, m.cfg.action_dim) and got.dtype == np.float32
+    ref = m0_torch.denoise_step_m0({k_: v_.astype(np.float64) for k_, v_ in m.p16.items()}, m.d,
+                                   m.prefix.astype(np.float64), m.x_t.astype(np.float64), te.astype(np.float64))
+    _tol(got, ref)
+    pm = make_prefix_mask_np(m.cfg.prefix_len)
+    k, v = _prefill(m, pm)
+    cos, sin = make_rope_np(m.cfg.suffix_len, m.cfg.vlm.head_dim, m.cfg.rope_theta, offset=m.cfg.prefix_len)
+    m1 = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                        m.params).numpy()
+    assert cosine(got, m1) >= 0.999999
+    assert max_abs(got, m1) <= 1e-3 * max(1.0, float(np.abs(m1).max()))
+
+
 def test_sample_vs_oracle_and_graph_loop(tiny):
     """sample (host loop) vs the oracle; sample_graph (device loop) vs sample (compare_loop)."""
     m = tiny
