@@ -88,6 +88,13 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
                  void* stream);
 
+/* embed_language -- Pi0Model.embed_language (pi0_model.py:101-104), exported as
+ * "embed_language" (pi0_model.py:217-220): input_ids [n] int32 (device), the embedding table
+ * embed_tokens.weight [vocab, width] f16 -> out [n, width] f16 with
+ * out[t] = fp16(table[ids[t]] * fp16(sqrt(width))).  Ids outside [0, vocab) are clamped. */
+int mlcv_embed_language(const int32_t* input_ids, int32_t n, const void* table, int32_t vocab, int32_t width,
+                        void* out, void* stream);
+
 /* denoise_step -- Pi0Model.denoise_step (pi0_model.py:111-125), the joint prefix + suffix
  * ("M0") velocity that get_default_spec exports as "denoise_step" (pi0_model.py:221-225):
  *   prefix_embs [1,P,vlm_width] f16, x_t [1,T,A] f16, time_emb [1, ae_width] f16

@@ -1109,6 +1109,13 @@ static void suffix_jobs(const Ctx& c, const float* cos, const float* sin, const 
   jobs.push_back({mask, c.mask, (size_t)c.P * 4});
 }
 
+int mlcv_embed_language(const int32_t* input_ids, int32_t n, const void* table, int32_t vocab, int32_t width,
+                        void* out, void* stream) {
+  MLCV_REQUIRE(input_ids && table && out && n > 0 && vocab > 0 && width > 0, "bad argument");
+  return embed_language_launch(input_ids, n, reinterpret_cast<const _Float16*>(table), vocab, width,
+                               reinterpret_cast<_Float16*>(out), reinterpret_cast<hipStream_t>(stream));
+}
+
 int mlcv_denoise_step(mlcv_ctx* ctx, const void* prefix_embs, const void* x_t, const void* time_emb, float* v_out,
                       void* stream) {
   MLCV_REQUIRE(ctx && prefix_embs && x_t && time_emb && v_out, "null argument");

@@ -245,6 +245,10 @@ struct TgArgs {
   int sync_tiles;
   int small_tiles;       // 1: the 128 x 128 tile kernel only
 };
+// out[t] = fp16(table[ids[t]] * fp16(sqrt(width))) for n tokens (ids clamped into the table)
+int embed_language_launch(const int32_t* ids, int n, const _Float16* table, int vocab, int width, _Float16* out,
+                          hipStream_t st);
+
 // compute units of the current device (cached per device; 0 if it cannot be queried)
 int device_cus();
 // words of meeting counters and floats of partials the 256-row tile path can use

@@ -46,6 +46,7 @@ SIGNATURES = {
     "mlcv_set_option": (ctypes.c_int, [_vp, _i32, ctypes.c_int64]),
     "mlcv_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "mlcv_denoise_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "mlcv_embed_language": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _vp]),
     "mlcv_denoise_step_kv": (ctypes.c_int, [_vp] * 10),
     "mlcv_denoise_loop_kv": (ctypes.c_int, [_vp] * 10),
     "mlcv_chunk": (ctypes.c_int, [_vp] * 9),

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import warnings
 
-from .model.pi0.pi0_model import KV_FUNCS, named_params
+from .model.pi0.pi0_model import BUILT_FUNCS, KV_FUNCS, named_params
 from .runtime import Device, Executable, device
 
 GPU_TARGETS = ("rocm", "hip", "cuda", "gfx950")
@@ -48,14 +48,16 @@ def check_config(config) -> None:
 
 def compile_model(config, target: str = "rocm", functions=None, cuda_graph: bool = False, cublas=None,
                   hoist_modulation: bool = True):
-    """Return ``(executable, named_params)`` for the M1 functions (compile.py:99-133)."""
+    """Return ``(executable, named_params)`` (compile.py:99-133).  ``functions`` may name
+    embed_language, denoise_step, prefill, denoise_step_kv and denoise_loop_kv; the default is
+    the M1 functions (prefill, denoise_step_kv, denoise_loop_kv)."""
     _target_kind(target)
     check_config(config)
     resolve_cublas(cublas, "rocm")
     funcs = tuple(functions) if functions is not None else KV_FUNCS
-    unknown = [f for f in funcs if f not in KV_FUNCS]
+    unknown = [f for f in funcs if f not in BUILT_FUNCS]
     if unknown:
-        raise NotImplementedError(f"functions {unknown} are not built on gfx950 (available: {KV_FUNCS})")
+        raise NotImplementedError(f"functions {unknown} are not built on gfx950 (available: {BUILT_FUNCS})")
     npar = named_params(config, funcs)
     return Executable(config, funcs, npar, None, cuda_graph, hoist_modulation), npar
 

@@ -11,7 +11,7 @@ from __future__ import annotations
 import numpy as np
 
 from .compile import _target_kind, check_config
-from .model.pi0.pi0_model import KV_FUNCS, named_params, quantized_named_params
+from .model.pi0.pi0_model import BACKBONE_FUNCS, KV_FUNCS, named_params, quantized_named_params
 from .quant import QuantizeMapping, get_quant
 from .runtime import Executable
 
@@ -32,6 +32,9 @@ def compile_model_quant(config, target: str, functions, quant_name: str, cuda_gr
     if quant.model_dtype != config.dtype:
         raise ValueError("config.dtype must equal the preset's model dtype")
     funcs = tuple(functions) if functions is not None else KV_FUNCS
+    unknown = [f for f in funcs if f not in BACKBONE_FUNCS]
+    if unknown:
+        raise NotImplementedError(f"functions {unknown}: the q4f16_1 build covers {BACKBONE_FUNCS}")
     qnp = quantized_named_params(config, quant.group_size, quant.num_elem_per_storage, funcs)
     qmap = QuantizeMapping({}, {})
     for name, p in named_params(config, funcs):

@@ -17,6 +17,9 @@ from typing import Dict, List, Optional, Sequence, Tuple
 from .pi0_config import Pi0Config
 
 KV_FUNCS = ("prefill", "denoise_step_kv", "denoise_loop_kv")
+BACKBONE_FUNCS = ("denoise_step",) + KV_FUNCS
+BUILT_FUNCS = ("embed_language",) + BACKBONE_FUNCS  # embed_image (SigLIP) is not built on gfx950
+PALIGEMMA_VOCAB_SIZE = 257_152  # pi0_model.py:79
 _ALL_STAGES = ("vision", "embed", "backbone")
 
 
@@ -85,10 +88,17 @@ def backbone_param_shapes(config: Pi0Config) -> List[Tuple[str, Tuple[int, ...]]
 
 
 def named_params(config: Pi0Config, functions: Optional[Sequence[str]] = None) -> List[Tuple[str, Param]]:
-    """``[(name, Param(shape, dtype))]`` as the reference's export_tvm returns for the backbone."""
-    if "backbone" not in include_for(functions):
-        raise NotImplementedError("only the backbone functions (prefill / denoise_*) are built on gfx950")
-    return [(name, Param(shape, config.dtype)) for name, shape in backbone_param_shapes(config)]
+    """``[(name, Param(shape, dtype))]`` as the reference's export_tvm returns them, in attribute
+    order: ``embed_tokens`` before the backbone (pi0_model.py:75-88)."""
+    need = include_for(functions)
+    if "vision" in need and functions is not None:
+        raise NotImplementedError("embed_image (the SigLIP tower) is not built on gfx950")
+    out: List[Tuple[str, Param]] = []
+    if "embed" in need and functions is not None:
+        out.append(("embed_tokens.weight", Param((PALIGEMMA_VOCAB_SIZE, config.vlm.width), config.dtype)))
+    if "backbone" in need:
+        out += [(name, Param(shape, config.dtype)) for name, shape in backbone_param_shapes(config)]
+    return out
 
 
 def quantized_named_params(config: Pi0Config, group_size: int = 32, elems_per_word: int = 8,
@@ -121,6 +131,9 @@ def get_default_spec(config: Pi0Config, functions: Optional[Sequence[str]] = Non
     rope = (1, config.suffix_len, 1, vlm.head_dim // 2)
     act = (1, config.action_horizon, config.action_dim)
     spec = {
+        "embed_language": {
+            "input_ids": TensorSpec((1, config.max_token_len), "int32"),
+        },
         "denoise_step": {
             "prefix_embs": TensorSpec((1, config.prefix_len, vlm.width), dt),
             "x_t": TensorSpec(act, dt),

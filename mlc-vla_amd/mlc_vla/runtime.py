@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import _native as N
-from .model.pi0.pi0_model import get_default_spec
+from .model.pi0.pi0_model import BACKBONE_FUNCS, get_default_spec
 
 _TORCH = {"float16": torch.float16, "float32": torch.float32, "int32": torch.int32, "uint32": torch.int32}
 
@@ -142,20 +142,27 @@ class Executable:
 
 
 class VirtualMachine:
-    """``vm["denoise_step" | "prefill" | "denoise_step_kv" | "denoise_loop_kv" | "chunk"](*tensors, params)``."""
+    """``vm["embed_language" | "denoise_step" | "prefill" | "denoise_step_kv" | "denoise_loop_kv" |
+    "chunk"](*tensors, params)``.  The backbone functions share one native context (created
+    when any of them is compiled); ``embed_language`` is a stateless kernel over the
+    ``embed_tokens`` table, the first parameter when it is compiled."""
 
     def __init__(self, ex: Executable, dev: Optional[Device] = None):
         self.ex = ex
         self.dev = dev or device()
         self._spec = get_default_spec(ex.config)
-        cfg = ex.c_config()
-        h = ctypes.c_void_p()
-        with torch.cuda.device(self.dev.index):
-            N.call("mlcv_create", ctypes.byref(cfg), ctypes.byref(h))
-        self._ctx = h
+        self._emb = bool(ex.named_params) and ex.named_params[0][0] == "embed_tokens.weight"
+        self._backbone = any(f in BACKBONE_FUNCS for f in ex.functions)
+        self._ctx = ctypes.c_void_p()
         self._bound = None
-        self.set_graph(ex.cuda_graph)
-        self.set_hoist(ex.hoist_modulation)
+        if self._backbone:
+            cfg = ex.c_config()
+            h = ctypes.c_void_p()
+            with torch.cuda.device(self.dev.index):
+                N.call("mlcv_create", ctypes.byref(cfg), ctypes.byref(h))
+            self._ctx = h
+            self.set_graph(ex.cuda_graph)
+            self.set_hoist(ex.hoist_modulation)
 
     def __del__(self):
         h = getattr(self, "_ctx", None)
@@ -177,7 +184,7 @@ class VirtualMachine:
     def _stream(self) -> ctypes.c_void_p:
         return ctypes.c_void_p(torch.cuda.current_stream(self.dev.index).cuda_stream)
 
-    def _bind(self, params: Sequence) -> None:
+    def _check_params(self, params: Sequence) -> List[Tensor]:
         specs = self.ex.named_params
         if len(params) != len(specs):
             raise ValueError(f"expected {len(specs)} params, got {len(params)}")
@@ -185,6 +192,12 @@ class VirtualMachine:
         for (name, sp), t in zip(specs, ts):
             want = "int32" if sp.dtype == "uint32" and t.dtype == "int32" else sp.dtype
             _check("params", name, t, sp.shape, want)
+        return ts
+
+    def _bind(self, params: Sequence) -> None:
+        if not self._backbone:
+            raise KeyError("no backbone function is compiled in this executable")
+        ts = self._check_params(params)[1 if self._emb else 0:]
         key = tuple(t.torch.data_ptr() for t in ts)
         if key == self._bound:
             return
@@ -205,13 +218,28 @@ class VirtualMachine:
         return out
 
     def __getitem__(self, name: str):
-        fns = {"denoise_step": self.denoise_step, "prefill": self.prefill, "denoise_step_kv": self.denoise_step_kv,
-               "denoise_loop_kv": self.denoise_loop_kv, "chunk": self.chunk}
+        fns = {}
+        if "embed_language" in self.ex.functions:
+            fns["embed_language"] = self.embed_language
+        if self._backbone:
+            fns.update({"denoise_step": self.denoise_step, "prefill": self.prefill,
+                        "denoise_step_kv": self.denoise_step_kv, "denoise_loop_kv": self.denoise_loop_kv,
+                        "chunk": self.chunk})
         if name not in fns:
             raise KeyError(f"function {name!r} is not built (available: {sorted(fns)})")
         return fns[name]
 
     # exported functions ------------------------------------------------------
+    def embed_language(self, input_ids, params):
+        """[1, max_token_len] int32 -> [1, max_token_len, vlm_width]: the embed_tokens rows
+        times sqrt(width) in the model dtype (pi0_model.py:101-104)."""
+        table = self._check_params(params)[0]
+        (ids,) = self._args("embed_language", (input_ids,))
+        vocab, width = table.shape
+        out = empty((1, ids.shape[1], width), self.ex.config.dtype, self.dev)
+        N.call("mlcv_embed_language", _ptr(ids), ids.shape[1], _ptr(table), vocab, width, _ptr(out), self._stream())
+        return out
+
     def denoise_step(self, prefix_embs, x_t, time_emb, params):
         """The joint prefix + suffix velocity (Pi0Model.denoise_step, pi0_model.py:111-125):
         every prefix token valid, RoPE positions 0..P+T-1; returns v [1,T,A] f32."""

@@ -27,6 +27,9 @@ prefill                     model/pi0/pi0_model.py:128-140,                 M1==
 denoise_step_kv             model/pi0/pi0_model.py:142-163,                 M1==M0, pad invariance
                             gemma_dual.py:255-275,343-351,417-433
 denoise_loop_kv             model/pi0/pi0_model.py:165-194                  loop == host euler_loop (bit-exact)
+embed_language              model/pi0/pi0_model.py:101-104                  float64 product rounded once to fp16
+                                                                            (all ids, every vocabulary row); the
+                                                                            constant's fp16 dtype is parity unpinned
 param_specs                 model/pi0/pi0_model.py:81-88,                   count 18*depth+11, shapes
                             gemma_dual.py:60-73,125-148,281-291,357-371
 ==========================  ==============================================  =====================================
@@ -223,6 +226,16 @@ def make_time_embs(num_steps: int, width: int) -> List[np.ndarray]:
         out.append(sinusoidal_time_emb(t, width))
         t += dt
     return out
+
+
+def embed_language(table: np.ndarray, input_ids: np.ndarray) -> np.ndarray:
+    """Pi0Model.embed_language (pi0_model.py:101-104): ``embed_tokens(ids) * sqrt(width)``.
+    The table is fp16 and the Python float becomes a constant of the tensor's dtype, so the
+    result is the fp16 product of two fp16 values (numpy float16 arithmetic rounds it once)."""
+    width = table.shape[1]
+    scale = np.float16(math.sqrt(width))
+    with np.errstate(over="ignore"):  # products past the fp16 range round to inf, as on the GPU
+        return (table[np.asarray(input_ids)].astype(np.float16) * scale).astype(np.float16)
 
 
 def make_rope_np(num_positions: int, head_dim: int, theta: float,

@@ -117,6 +117,22 @@ def test_tile_linear_vs_exact(m, k, n, epi, small):
     assert cosine(got.cpu().numpy(), (ref if epi == 2 else target).cpu().numpy()) > 0.99999
 
 
+@pytest.mark.parametrize("vocab,width,n", [(1000, 2048, 77), (300, 256, 32), (50, 100, 9)])
+def test_embed_language_bitexact(vocab, width, n):
+    """embed_language rows (16-byte and scalar paths) against the oracle, bit-exact; ids
+    outside the table are clamped to its ends."""
+    print(f"embed_language vocab={vocab} width={width} n={n}", flush=True)
+    rng = np.random.default_rng(vocab + width)
+    table = (rng.standard_normal((vocab, width)) * 3).astype(np.float16)
+    ids = rng.integers(0, vocab, size=n).astype(np.int32)
+    ids[0], ids[-1] = -5, vocab + 7
+    out = torch.empty((n, width), dtype=torch.float16, device="cuda")
+    idsd, tabd = _dev(ids), _dev(table)  # alive until the kernel has run
+    N.call("mlcv_embed_language", _p(idsd), n, _p(tabd), vocab, width, _p(out), _st())
+    ref = O.embed_language(table, np.clip(ids, 0, vocab - 1))
+    np.testing.assert_array_equal(_host(out).view(np.uint16), ref.view(np.uint16))
+
+
 LIN_SHAPES = [(1, 1024, 3072), (50, 1024, 2560), (50, 2048, 1024), (50, 4096, 1024), (8, 32, 128), (50, 1024, 32),
               (100, 256, 64), (4, 64, 16)]
 

@@ -148,6 +148,26 @@ def test_denoise_step_joint_vs_m0_oracle_and_m1(which, tiny, dummy):
     assert max_abs(got, m1) <= 1e-3 * max(1.0, float(np.abs(m1).max()))
 
 
+def test_vm_embed_language(tiny):
+    """vm["embed_language"] from compile_model(functions=["embed_language"]): the parameter list
+    is [embed_tokens.weight] at the PaliGemma vocabulary; bit-exact against the oracle."""
+    from mlc_vla.compile import compile_model
+    from mlc_vla.runtime import VirtualMachine
+
+    cfg = tiny.cfg
+    ex, npar = compile_model(cfg, "rocm", functions=["embed_language"])
+    assert [n for n, _ in npar] == ["embed_tokens.weight"] and npar[0][1].shape == (257152, cfg.vlm.width)
+    vm = VirtualMachine(ex, tiny.runner.dev)
+    rng = np.random.default_rng(12)
+    table = rng.standard_normal(npar[0][1].shape, dtype=np.float32).astype(np.float16)
+    ids = rng.integers(0, 257152, size=(1, cfg.max_token_len)).astype(np.int32)
+    got = vm["embed_language"](tiny.dev(ids), [tiny.dev(table)]).numpy()
+    assert got.shape == (1, cfg.max_token_len, cfg.vlm.width) and got.dtype == np.float16
+    np.testing.assert_array_equal(got.view(np.uint16), O.embed_language(table, ids).view(np.uint16))
+    with pytest.raises(KeyError):
+        vm["prefill"]
+
+
 def test_sample_vs_oracle_and_graph_loop(tiny):
     """sample (host loop) vs the oracle; sample_graph (device loop) vs sample (compare_loop)."""
     m = tiny

@@ -243,3 +243,23 @@ def test_fp16_emulation_tracks_fp64():
     got = _m1(p16, d, P.cast(prefix), P.cast(x_t), P.cast(te), P=P)
     assert cosine(got, truth) > 0.9999
     assert max_abs(got, truth) < 5e-3
+
+
+def test_embed_language_is_one_fp16_rounding_of_the_exact_product():
+    """embed_language: table rows times the fp16 constant sqrt(width), rounded once to fp16.
+    Checked against the float64 product rounded to fp16 over normal, subnormal and
+    near-overflow entries; a float32 constant or a double rounding would differ."""
+    rng = np.random.default_rng(11)
+    width = 2048
+    table = np.concatenate([rng.standard_normal((40, width)) * s for s in (1e-6, 1e-3, 1.0, 30.0, 1400.0)])
+    table = table.astype(np.float16)
+    ids = rng.integers(0, table.shape[0], size=(1, 77))
+    got = O.embed_language(table, ids)
+    c = np.float16(np.sqrt(width))
+    assert c == np.float16(45.25)
+    with np.errstate(over="ignore"):  # the largest rows overflow to inf in fp16
+        exact = (table[ids].astype(np.float64) * np.float64(c)).astype(np.float16)
+        wrong = (table[ids].astype(np.float32) * np.float32(np.sqrt(width))).astype(np.float16)
+    np.testing.assert_array_equal(got.view(np.uint16), exact.view(np.uint16))
+    assert got.shape == (1, 77, width) and got.dtype == np.float16
+    assert not np.array_equal(got.view(np.uint16), wrong.view(np.uint16))
