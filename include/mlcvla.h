@@ -88,6 +88,22 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
                  void* stream);
 
+/* embed_image -- Pi0Model.embed_image (pi0_model.py:97-99): the SigLIP tower and the
+ * PaliGemma projector (siglip.py:20-120) over one channels-last image [S,S,C] f16
+ * -> out [num_patches, projection_dim] f16.  `params` are the vision tower's parameters in
+ * named_params order (mlcv_vision_param_count of them: 3 + 16 per layer + 4), device
+ * pointers to f16.  `workspace` is caller-owned device memory of
+ * mlcv_embed_image_workspace bytes.  Calls on one device are serialized. */
+typedef struct mlcv_vision_config {
+  int32_t image_size, patch_size, num_channels, hidden_size, intermediate_size, num_hidden_layers,
+      num_attention_heads, projection_dim;
+  float layer_norm_eps;
+} mlcv_vision_config;
+int mlcv_vision_param_count(const mlcv_vision_config* cfg, int32_t* count);
+int mlcv_embed_image_workspace(const mlcv_vision_config* cfg, size_t* bytes);
+int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, int32_t count, const void* image,
+                     void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* embed_language -- Pi0Model.embed_language (pi0_model.py:101-104), exported as
  * "embed_language" (pi0_model.py:217-220): input_ids [n] int32 (device), the embedding table
  * embed_tokens.weight [vocab, width] f16 -> out [n, width] f16 with

@@ -1335,17 +1335,12 @@ int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, i
                            K, reinterpret_cast<hipStream_t>(stream));
 }
 
-int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
-                     int32_t small_tiles, void* stream) {
-  MLCV_REQUIRE(x && w && y && M > 0 && K > 0 && N > 0, "bad argument");
-  MLCV_REQUIRE(epi == TG_STORE || epi == TG_RESIDUAL || epi == TG_GEGLU, "unknown epilogue");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // split-K workspace and meeting counters of this entry point (per device, kept; calls on
-  // one device are serialized by the lock)
-  static std::mutex mu;
+// split-K workspace and meeting counters of the standalone tile-GEMM entry points (per
+// device, kept until the process ends; the callers serialize on tile_mu)
+static std::mutex tile_mu;
+static int tile_scratch(float** ws_out, unsigned** sync_out) {
   static float* ws[64] = {};
   static unsigned* sync[64] = {};
-  std::lock_guard<std::mutex> lk(mu);
   int dev = 0;
   MLCV_HIP(hipGetDevice(&dev));
   MLCV_REQUIRE(dev >= 0 && dev < 64, "device index");
@@ -1354,6 +1349,56 @@ int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t
     MLCV_HIP(hipMalloc(&sync[dev], tg_sync_words() * sizeof(unsigned)));
     MLCV_HIP(hipMemset(sync[dev], 0, tg_sync_words() * sizeof(unsigned)));
   }
+  *ws_out = ws[dev];
+  *sync_out = sync[dev];
+  return 0;
+}
+
+static VisionCfg vision_cfg(const mlcv_vision_config& c) {
+  return VisionCfg{c.image_size, c.patch_size, c.num_channels, c.hidden_size, c.intermediate_size,
+                   c.num_hidden_layers, c.num_attention_heads, c.projection_dim, c.layer_norm_eps};
+}
+
+int mlcv_vision_param_count(const mlcv_vision_config* cfg, int32_t* count) {
+  MLCV_REQUIRE(cfg && count && cfg->num_hidden_layers >= 0, "bad argument");
+  *count = 3 + 16 * cfg->num_hidden_layers + 4;
+  return 0;
+}
+
+int mlcv_embed_image_workspace(const mlcv_vision_config* cfg, size_t* bytes) {
+  MLCV_REQUIRE(cfg && bytes && cfg->patch_size > 0, "bad argument");
+  *bytes = vision_ws_bytes(vision_cfg(*cfg));
+  return 0;
+}
+
+int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, int32_t count, const void* image,
+                     void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  MLCV_REQUIRE(cfg && params && image && out && workspace, "null argument");
+  MLCV_REQUIRE(cfg->image_size > 0 && cfg->patch_size > 0 && cfg->num_channels > 0 && cfg->hidden_size > 0 &&
+                   cfg->intermediate_size > 0 && cfg->num_hidden_layers >= 0 && cfg->num_attention_heads > 0 &&
+                   cfg->projection_dim > 0,
+               "bad vision config");
+  MLCV_REQUIRE(count == 3 + 16 * cfg->num_hidden_layers + 4, "vision parameter count");
+  for (int i = 0; i < count; ++i) MLCV_REQUIRE(params[i] != nullptr, "null vision parameter");
+  std::lock_guard<std::mutex> lk(tile_mu);
+  float* gws = nullptr;
+  unsigned* gsync = nullptr;
+  MLCV_TRY(tile_scratch(&gws, &gsync));
+  return embed_image_enqueue(vision_cfg(*cfg), reinterpret_cast<const _Float16* const*>(params),
+                             reinterpret_cast<const _Float16*>(image), reinterpret_cast<_Float16*>(out), workspace,
+                             workspace_bytes, gws, tg_ws_floats(), gsync, (int)(tg_sync_words() / 32),
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
+                     int32_t small_tiles, void* stream) {
+  MLCV_REQUIRE(x && w && y && M > 0 && K > 0 && N > 0, "bad argument");
+  MLCV_REQUIRE(epi == TG_STORE || epi == TG_RESIDUAL || epi == TG_GEGLU, "unknown epilogue");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lk(tile_mu);
+  float* gws = nullptr;
+  unsigned* gsync = nullptr;
+  MLCV_TRY(tile_scratch(&gws, &gsync));
   TgArgs g{};
   g.a = reinterpret_cast<const _Float16*>(x);
   g.lda = K;
@@ -1367,9 +1412,9 @@ int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t
   g.K = K;
   g.epi = epi;
   g.F = N;
-  g.ws = ws[dev];
+  g.ws = gws;
   g.ws_floats = tg_ws_floats();
-  g.sync = sync[dev];
+  g.sync = gsync;
   g.sync_tiles = (int)(tg_sync_words() / 32);
   g.small_tiles = small_tiles ? 1 : 0;
   MLCV_HIP(hipStreamSynchronize(st));

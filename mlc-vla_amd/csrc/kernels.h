@@ -249,6 +249,18 @@ struct TgArgs {
 int embed_language_launch(const int32_t* ids, int n, const _Float16* table, int vocab, int width, _Float16* out,
                           hipStream_t st);
 
+// SigLIP tower + projector of one image (vision.hip); params in named_params order:
+// patch_embedding w, b, position_embedding, per layer q w,b k w,b v w,b out w,b fc1 w,b
+// fc2 w,b layer_norm1 w,b layer_norm2 w,b, then post_layernorm w,b, projector w,b
+struct VisionCfg {
+  int image_size, patch_size, num_channels, hidden, inter, layers, heads, proj;
+  float eps;
+};
+size_t vision_ws_bytes(const VisionCfg& v);
+int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _Float16* image, _Float16* out,
+                        void* ws, size_t ws_bytes, float* gemm_ws, size_t gemm_ws_floats, unsigned* gemm_sync,
+                        int gemm_sync_tiles, hipStream_t st);
+
 // compute units of the current device (cached per device; 0 if it cannot be queried)
 int device_cus();
 // words of meeting counters and floats of partials the 256-row tile path can use

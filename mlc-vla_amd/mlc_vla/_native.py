@@ -36,6 +36,13 @@ class Config(ctypes.Structure):
     ]
 
 
+class VisionConfig(ctypes.Structure):
+    """mlcv_vision_config (include/mlcvla.h)."""
+    _fields_ = [(n, _i32) for n in ("image_size", "patch_size", "num_channels", "hidden_size", "intermediate_size",
+                                     "num_hidden_layers", "num_attention_heads", "projection_dim")] + \
+               [("layer_norm_eps", ctypes.c_float)]
+
+
 # name -> (restype, argtypes): every symbol include/mlcvla.h declares
 SIGNATURES = {
     "mlcv_last_error": (ctypes.c_char_p, []),
@@ -47,6 +54,10 @@ SIGNATURES = {
     "mlcv_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "mlcv_denoise_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "mlcv_embed_language": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _vp]),
+    "mlcv_vision_param_count": (ctypes.c_int, [ctypes.POINTER(VisionConfig), ctypes.POINTER(_i32)]),
+    "mlcv_embed_image_workspace": (ctypes.c_int, [ctypes.POINTER(VisionConfig), ctypes.POINTER(ctypes.c_size_t)]),
+    "mlcv_embed_image": (ctypes.c_int, [ctypes.POINTER(VisionConfig), ctypes.POINTER(_vp), _i32, _vp, _vp, _vp,
+                                        ctypes.c_size_t, _vp]),
     "mlcv_denoise_step_kv": (ctypes.c_int, [_vp] * 10),
     "mlcv_denoise_loop_kv": (ctypes.c_int, [_vp] * 10),
     "mlcv_chunk": (ctypes.c_int, [_vp] * 9),

@@ -18,7 +18,7 @@ from .pi0_config import Pi0Config
 
 KV_FUNCS = ("prefill", "denoise_step_kv", "denoise_loop_kv")
 BACKBONE_FUNCS = ("denoise_step",) + KV_FUNCS
-BUILT_FUNCS = ("embed_language",) + BACKBONE_FUNCS  # embed_image (SigLIP) is not built on gfx950
+BUILT_FUNCS = ("embed_image", "embed_language") + BACKBONE_FUNCS
 PALIGEMMA_VOCAB_SIZE = 257_152  # pi0_model.py:79
 _ALL_STAGES = ("vision", "embed", "backbone")
 
@@ -87,13 +87,33 @@ def backbone_param_shapes(config: Pi0Config) -> List[Tuple[str, Tuple[int, ...]]
     return out
 
 
+def vision_param_shapes(config: Pi0Config) -> List[Tuple[str, Tuple[int, ...]]]:
+    """(name, shape) of the SigLIP tower + projector in attribute order (siglip.py:73-90)."""
+    s = config.siglip
+    out: List[Tuple[str, Tuple[int, ...]]] = []
+    _linear(out, "vision.patch_embedding", s.hidden_size, s.patch_size * s.patch_size * s.num_channels, True)
+    out.append(("vision.position_embedding", (s.num_patches, s.hidden_size)))
+    for i in range(s.num_hidden_layers):
+        p = f"vision.layers.{i}."
+        for proj in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            _linear(out, f"{p}self_attn.{proj}", s.hidden_size, s.hidden_size, True)
+        _linear(out, p + "mlp.fc1", s.intermediate_size, s.hidden_size, True)
+        _linear(out, p + "mlp.fc2", s.hidden_size, s.intermediate_size, True)
+        for ln in ("layer_norm1", "layer_norm2"):
+            out += [(f"{p}{ln}.weight", (s.hidden_size,)), (f"{p}{ln}.bias", (s.hidden_size,))]
+    out += [("vision.post_layernorm.weight", (s.hidden_size,)), ("vision.post_layernorm.bias", (s.hidden_size,))]
+    _linear(out, "vision.multi_modal_projector", s.projection_dim, s.hidden_size, True)
+    return out
+
+
 def named_params(config: Pi0Config, functions: Optional[Sequence[str]] = None) -> List[Tuple[str, Param]]:
     """``[(name, Param(shape, dtype))]`` as the reference's export_tvm returns them, in attribute
-    order: ``embed_tokens`` before the backbone (pi0_model.py:75-88)."""
+    order: the vision tower, then ``embed_tokens``, then the backbone (pi0_model.py:75-88).
+    With ``functions`` None the backbone alone is listed (the M1 functions)."""
     need = include_for(functions)
-    if "vision" in need and functions is not None:
-        raise NotImplementedError("embed_image (the SigLIP tower) is not built on gfx950")
     out: List[Tuple[str, Param]] = []
+    if "vision" in need and functions is not None:
+        out += [(name, Param(shape, config.dtype)) for name, shape in vision_param_shapes(config)]
     if "embed" in need and functions is not None:
         out.append(("embed_tokens.weight", Param((PALIGEMMA_VOCAB_SIZE, config.vlm.width), config.dtype)))
     if "backbone" in need:
@@ -130,7 +150,11 @@ def get_default_spec(config: Pi0Config, functions: Optional[Sequence[str]] = Non
     pm = (1, 1, 1, config.prefix_len)
     rope = (1, config.suffix_len, 1, vlm.head_dim // 2)
     act = (1, config.action_horizon, config.action_dim)
+    sg = config.siglip
     spec = {
+        "embed_image": {
+            "image": TensorSpec((1, sg.image_size, sg.image_size, sg.num_channels), dt),
+        },
         "embed_language": {
             "input_ids": TensorSpec((1, config.max_token_len), "int32"),
         },

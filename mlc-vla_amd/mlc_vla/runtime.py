@@ -151,8 +151,12 @@ class VirtualMachine:
         self.ex = ex
         self.dev = dev or device()
         self._spec = get_default_spec(ex.config)
-        self._emb = bool(ex.named_params) and ex.named_params[0][0] == "embed_tokens.weight"
+        names = [n for n, _ in ex.named_params]
+        self._nvis = sum(1 for n in names if n.startswith("vision."))
+        self._emb = "embed_tokens.weight" in names
+        self._bb0 = self._nvis + (1 if self._emb else 0)  # first backbone parameter
         self._backbone = any(f in BACKBONE_FUNCS for f in ex.functions)
+        self._vis_ws = None
         self._ctx = ctypes.c_void_p()
         self._bound = None
         if self._backbone:
@@ -197,7 +201,7 @@ class VirtualMachine:
     def _bind(self, params: Sequence) -> None:
         if not self._backbone:
             raise KeyError("no backbone function is compiled in this executable")
-        ts = self._check_params(params)[1 if self._emb else 0:]
+        ts = self._check_params(params)[self._bb0:]
         key = tuple(t.torch.data_ptr() for t in ts)
         if key == self._bound:
             return
@@ -219,6 +223,8 @@ class VirtualMachine:
 
     def __getitem__(self, name: str):
         fns = {}
+        if "embed_image" in self.ex.functions:
+            fns["embed_image"] = self.embed_image
         if "embed_language" in self.ex.functions:
             fns["embed_language"] = self.embed_language
         if self._backbone:
@@ -233,11 +239,31 @@ class VirtualMachine:
     def embed_language(self, input_ids, params):
         """[1, max_token_len] int32 -> [1, max_token_len, vlm_width]: the embed_tokens rows
         times sqrt(width) in the model dtype (pi0_model.py:101-104)."""
-        table = self._check_params(params)[0]
+        table = self._check_params(params)[self._nvis]
         (ids,) = self._args("embed_language", (input_ids,))
         vocab, width = table.shape
         out = empty((1, ids.shape[1], width), self.ex.config.dtype, self.dev)
         N.call("mlcv_embed_language", _ptr(ids), ids.shape[1], _ptr(table), vocab, width, _ptr(out), self._stream())
+        return out
+
+    def embed_image(self, image, params):
+        """[1, S, S, C] channels-last -> [1, num_patches, projection_dim]: the SigLIP tower and
+        the PaliGemma projector (pi0_model.py:97-99, siglip.py:73-120)."""
+        vis = self._check_params(params)[: self._nvis]
+        (img,) = self._args("embed_image", (image,))
+        s = self.ex.config.siglip
+        cfg = N.VisionConfig(image_size=s.image_size, patch_size=s.patch_size, num_channels=s.num_channels,
+                             hidden_size=s.hidden_size, intermediate_size=s.intermediate_size,
+                             num_hidden_layers=s.num_hidden_layers, num_attention_heads=s.num_attention_heads,
+                             projection_dim=s.projection_dim, layer_norm_eps=s.layer_norm_eps)
+        if self._vis_ws is None:
+            nbytes = ctypes.c_size_t()
+            N.call("mlcv_embed_image_workspace", ctypes.byref(cfg), ctypes.byref(nbytes))
+            self._vis_ws = torch.empty(nbytes.value, dtype=torch.uint8, device=self.dev.torch)
+        out = empty((1, s.num_patches, s.projection_dim), self.ex.config.dtype, self.dev)
+        arr = (ctypes.c_void_p * len(vis))(*[ctypes.c_void_p(t.torch.data_ptr()) for t in vis])
+        N.call("mlcv_embed_image", ctypes.byref(cfg), arr, len(vis), _ptr(img), _ptr(out),
+               ctypes.c_void_p(self._vis_ws.data_ptr()), self._vis_ws.numel(), self._stream())
         return out
 
     def denoise_step(self, prefix_embs, x_t, time_emb, params):

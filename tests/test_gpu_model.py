@@ -168,6 +168,37 @@ def test_vm_embed_language(tiny):
         vm["prefill"]
 
 
+@pytest.mark.parametrize("sig", [
+    dict(image_size=28, patch_size=14, hidden_size=144, intermediate_size=200, num_hidden_layers=2,
+         num_attention_heads=2, projection_dim=64),
+    dict(image_size=56, patch_size=14, hidden_size=128, intermediate_size=96, num_hidden_layers=1,
+         num_attention_heads=2, projection_dim=32),
+    dict(num_hidden_layers=1),  # one layer of So400m/14 at 224 x 224: 256 patches, hd 72, projector to 2048
+], ids=["hd72", "hd64", "so400m_1layer"])
+def test_vm_embed_image_vs_oracle(sig, tiny):
+    """vm["embed_image"] (SigLIP tower + projector) against the oracle at the reference's fp16
+    cast points (siglip_oracle, pinned to torch conv2d / layer_norm / SDPA in float64)."""
+    from mlc_vla.compile import compile_model
+    from mlc_vla.model.pi0 import Pi0Config, SiglipConfig
+    from mlc_vla.runtime import VirtualMachine
+    from oracle import siglip_oracle as S
+
+    sc = SiglipConfig(**sig)
+    cfg = Pi0Config(**{**TINY_KWARGS, "siglip": sc})
+    ex, npar = compile_model(cfg, "rocm", functions=["embed_image"])
+    assert [n for n, _ in npar] == [n for n, _ in S.vision_param_specs(sc)]
+    vm = VirtualMachine(ex, tiny.runner.dev)
+    P = S.make_vision_params(sc, 7)
+    img = np.random.default_rng(8).standard_normal((sc.image_size, sc.image_size, sc.num_channels)).astype(np.float16)
+    got = vm["embed_image"](tiny.dev(img[None]), [tiny.dev(P[n]) for n, _ in npar]).numpy()
+    assert got.shape == (1, sc.num_patches, sc.projection_dim) and got.dtype == np.float16
+    ref = S.embed_image(P, sc, img, "f16")
+    g = got[0].astype(np.float64)
+    assert np.all(np.isfinite(g))
+    assert cosine(g, ref) >= 0.9999, cosine(g, ref)
+    assert max_abs(g, ref) <= 2e-2 * float(np.abs(ref).max()), (max_abs(g, ref), float(np.abs(ref).max()))
+
+
 def test_sample_vs_oracle_and_graph_loop(tiny):
     """sample (host loop) vs the oracle; sample_graph (device loop) vs sample (compare_loop)."""
     m = tiny
