@@ -46,6 +46,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-q4", action="store_true")
+    ap.add_argument("--no-embed", action="store_true", help="skip the embed_image timing")
     ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
                     help="print a per-kernel, per-launch-shape table of a rocprofv3 --kernel-trace CSV and exit")
     ap.add_argument("--summarize-pmc", metavar="COUNTER_CSV",
@@ -496,11 +497,54 @@ def main():
                                "cold_p90_us": round(_pct(q_cold, 0.9), 1)}
         del vmq, qparams
 
+    if not args.no_embed:
+        out["embed_image"] = embed_image_timing(cfg, dev)
+
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
+
+
+def embed_image_timing(cfg, dev, iters: int = 10):
+    """embed_image of one 224 x 224 image through the full SigLIP So400m/14 tower (27 layers)
+    and the projector, random weights drawn on the GPU; HIP events around `iters` calls."""
+    import torch
+
+    from mlc_vla import runtime
+    from mlc_vla.compile import compile_model
+
+    ex, npar = compile_model(cfg, "rocm", functions=["embed_image"])
+    vm = runtime.VirtualMachine(ex, dev)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    params = []
+    for name, p in npar:
+        fan = p.shape[1] if len(p.shape) == 2 else 1
+        t = torch.randn(p.shape, generator=g, device="cuda") / (fan ** 0.5 if len(p.shape) == 2 else 50.0)
+        if "layer_norm" in name and name.endswith(".weight") or name.endswith("post_layernorm.weight"):
+            t = t + 1.0
+        params.append(runtime.as_tensor(t.half()))
+    s = cfg.siglip
+    img = runtime.as_tensor(torch.randn((1, s.image_size, s.image_size, s.num_channels), generator=g,
+                                        device="cuda").half())
+    for _ in range(2):
+        vm["embed_image"](img, params)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        o = vm["embed_image"](img, params)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    flops = 2 * s.num_patches * (s.patch_size ** 2 * s.num_channels * s.hidden_size + s.num_hidden_layers * (
+        4 * s.hidden_size ** 2 + 2 * s.hidden_size * s.intermediate_size + 2 * s.num_patches * s.hidden_size) +
+        s.hidden_size * s.projection_dim)
+    ok = bool(torch.isfinite(o.torch).all())
+    del vm, params
+    return {"workload": "SigLIP So400m/14 + projector, one 224x224 image (256 patches), fp16",
+            "ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "finite": ok}
 
 
 if __name__ == "__main__":

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   if (tile >= ntile_all) return;
   const int tm = tile % p.mtiles, tn = tile / p.mtiles;
   const int m0 = tm * GBM;
-  const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg) / BK;
+  const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg + BK - 1) / BK;
 
   // DMA of this wave's rows: A rows [64 w, +64), B rows [BN/4 w, +BN/4), 8 rows per
   // instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in the
@@ -268,15 +268,19 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     boff[i] = (row * a.ldb + pc * 8) * 2;
   }
   // DMA instruction i (A rows for i < NAI, then B rows) of k tile kt into a stage
+  // K past the last multiple of BK: this lane's 8-half piece at k >= K gets an offset past the
+  // buffer, which reads zeros (K % 8 == 0, so a piece is wholly inside or outside)
+  constexpr int OOB = 0x7ffffff0;
   auto dma1 = [&](int i, int kt, int stage) __attribute__((always_inline)) {
     char* sb = lds + stage * STG;
     const int ko = (kbeg + kt * BK) * 2;
+    const bool kin = kbeg + kt * BK + pc * 8 < a.K;
     if (i < NAI)
-      buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), aoff[i], ko);
+      buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), kin ? aoff[i] : OOB, ko);
     else
       buffer_to_lds16(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i - NAI]), 0, bbytes[i - NAI], 0x00020000),
-          (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), boff[i - NAI], ko);
+          (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), kin ? boff[i - NAI] : OOB, ko);
   };
   auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
 #pragma unroll
@@ -435,7 +439,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 
 // 256-row tile plan; false = the shape needs the 128 x 128 kernel
 bool big_plan(const TgArgs& a, GemmPlan& p) {
-  if (a.small_tiles || a.K % GBK != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
+  if (a.small_tiles || a.K % 8 != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
   if (a.epi == TG_GEGLU) {
     if (a.F % 128 != 0) return false;
     p.bn = 256;
@@ -450,7 +454,7 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
     p.ntiles = (a.N + p.bn - 1) / p.bn;
   }
   p.mtiles = (a.M + GBM - 1) / GBM;
-  const int tiles = p.mtiles * p.ntiles, kts = a.K / GBK;
+  const int tiles = p.mtiles * p.ntiles, kts = (a.K + GBK - 1) / GBK;
   const int slots = ((tiles + NXCD - 1) / NXCD) * NXCD;  // tile slots of the XCD-major grid
   int S = 1;
   if (a.epi != TG_GEGLU && a.ws && a.sync && tiles <= a.sync_tiles) {

@@ -92,24 +92,28 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const _Float16* __restri
     out[(size_t)r * n + c] = f2h((h2f(xr[c]) - mean) * rstd * h2f(w[c]) + h2f(b[c]));
 }
 
-constexpr int VA_ROWS = 64, VA_KEYS = 64;
+constexpr int VA_ROWS = 64, VA_KEYS = 64, VA_LANES = 4;
 
-// bidirectional attention of one head over T tokens, one thread per query row: qkv [T][3 H hd]
-// (q | k | v), out [T][H hd].  Pass 1 finds each row's max logit and exp sum, pass 2 forms
-// the fp16 probabilities and accumulates P.V; keys stream through LDS in tiles of 64.
+// bidirectional attention of one head over T tokens: qkv [T][3 H hd] (q | k | v), out
+// [T][H hd].  A block holds 64 query rows with 4 lanes per row (consecutive lanes of one
+// wave), each lane taking every 4th key of the tiles that stream through LDS.  Pass 1 finds
+// each row's max logit and exp sum (combined over the 4 lanes by shuffles), pass 2 forms the
+// fp16 probabilities and accumulates P.V, summed over the 4 lanes at the end.
 template <int HD>
-__global__ __launch_bounds__(VA_ROWS) void vis_attention_kernel(const _Float16* __restrict__ qkv, int T, int H,
-                                                                _Float16 qscale, _Float16* __restrict__ out) {
+__global__ __launch_bounds__(VA_ROWS* VA_LANES) void vis_attention_kernel(const _Float16* __restrict__ qkv, int T,
+                                                                          int H, _Float16 qscale,
+                                                                          _Float16* __restrict__ out) {
   constexpr int hd = HD;
   __shared__ float ks[VA_KEYS][HD];
   __shared__ _Float16 vs[VA_KEYS][HD];
-  const int h = blockIdx.y, tid = threadIdx.x, row = blockIdx.x * VA_ROWS + tid;
+  const int h = blockIdx.y, tid = threadIdx.x, kl = tid % VA_LANES;
+  const int row = blockIdx.x * VA_ROWS + tid / VA_LANES;
   const int ld = 3 * H * hd;
   const bool ok = row < T;
   float q[HD], acc[HD];
 #pragma unroll
   for (int d = 0; d < hd; ++d) {
-    q[d] = ok ? h2f(hmul(qkv[(size_t)min(row, T - 1) * ld + h * hd + d], qscale)) : 0.f;
+    q[d] = h2f(hmul(qkv[(size_t)min(row, T - 1) * ld + h * hd + d], qscale));
     acc[d] = 0.f;
   }
   float mx = -INFINITY, sum = 0.f;
@@ -117,13 +121,13 @@ __global__ __launch_bounds__(VA_ROWS) void vis_attention_kernel(const _Float16* 
     for (int k0 = 0; k0 < T; k0 += VA_KEYS) {
       const int nk = min(VA_KEYS, T - k0);
       __syncthreads();
-      for (int i = tid; i < nk * hd; i += VA_ROWS) {
+      for (int i = tid; i < nk * hd; i += VA_ROWS * VA_LANES) {
         const int j = i / hd, d = i % hd;
         ks[j][d] = h2f(qkv[(size_t)(k0 + j) * ld + H * hd + h * hd + d]);
         vs[j][d] = qkv[(size_t)(k0 + j) * ld + 2 * H * hd + h * hd + d];
       }
       __syncthreads();
-      for (int j = 0; j < nk; ++j) {
+      for (int j = kl; j < nk; j += VA_LANES) {
         float l = 0.f;
 #pragma unroll
         for (int d = 0; d < hd; ++d) l += q[d] * ks[j][d];
@@ -138,8 +142,22 @@ __global__ __launch_bounds__(VA_ROWS) void vis_attention_kernel(const _Float16* 
         }
       }
     }
+    if (pass == 0) {  // the row's max and sum over its 4 lanes
+#pragma unroll
+      for (int o = 1; o < VA_LANES; o <<= 1) {
+        const float m2 = __shfl_xor(mx, o), s2 = __shfl_xor(sum, o);
+        const float m = fmaxf(mx, m2);
+        sum = (mx == -INFINITY ? 0.f : sum * expf(mx - m)) + (m2 == -INFINITY ? 0.f : s2 * expf(m2 - m));
+        mx = m;
+      }
+    }
   }
-  if (ok) {
+#pragma unroll
+  for (int d = 0; d < hd; ++d) {
+    acc[d] += __shfl_xor(acc[d], 1);
+    acc[d] += __shfl_xor(acc[d], 2);
+  }
+  if (ok && kl == 0) {
 #pragma unroll
     for (int d = 0; d < hd; ++d) out[(size_t)row * H * hd + h * hd + d] = f2h(acc[d]);
   }
@@ -224,11 +242,12 @@ int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _F
     MLCV_TRY(gemm(hn, H, lp[0], lp[2], lp[4], H, 2 * H, H, qkv, 3 * H, np, 3 * H, H));
     for (int s = 0; s < 3; ++s) MLCV_TRY(epi(qkv + s * H, 3 * H, lp[1 + 2 * s], H, VE_BIAS, nullptr, nullptr));
     const dim3 ag((np + VA_ROWS - 1) / VA_ROWS, v.heads);
+    constexpr int NT = VA_ROWS * VA_LANES;
     switch (hd) {
-      case 16: vis_attention_kernel<16><<<ag, VA_ROWS, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      case 32: vis_attention_kernel<32><<<ag, VA_ROWS, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      case 64: vis_attention_kernel<64><<<ag, VA_ROWS, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      default: vis_attention_kernel<72><<<ag, VA_ROWS, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
+      case 16: vis_attention_kernel<16><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
+      case 32: vis_attention_kernel<32><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
+      case 64: vis_attention_kernel<64><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
+      default: vis_attention_kernel<72><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
     }
     MLCV_HIP(hipGetLastError());
     MLCV_TRY(gemm(ctx, H, lp[6], lp[6], lp[6], H, H, H, t, H, np, H, H));
