@@ -63,3 +63,32 @@ def test_null_arguments_fail_cleanly():
     assert b"null" in lib.mlcv_last_error()
     with pytest.raises(N.MlcvError):
         N.call("mlcv_denoise_step_kv", *([None] * 10))
+
+
+def test_vision_and_embedding_queries_and_argument_checks():
+    """embed_image's host queries (parameter count, workspace bytes) and the argument checks of
+    the newer entry points, all answered before any device call."""
+    lib = N.load()
+    vc = N.VisionConfig(image_size=224, patch_size=14, num_channels=3, hidden_size=1152, intermediate_size=4304,
+                        num_hidden_layers=27, num_attention_heads=16, projection_dim=2048, layer_norm_eps=1e-6)
+    n = ctypes.c_int32()
+    N.call("mlcv_vision_param_count", ctypes.byref(vc), ctypes.byref(n))
+    assert n.value == 3 + 16 * 27 + 4
+    nb = ctypes.c_size_t()
+    N.call("mlcv_embed_image_workspace", ctypes.byref(vc), ctypes.byref(nb))
+    np_, kp = 256, 592
+    assert nb.value >= 2 * (np_ * kp + 1152 * kp + np_ * 1152 * 7 + np_ * 4304)
+    arr = (ctypes.c_void_p * n.value)()
+    with pytest.raises(N.MlcvError, match="null"):
+        N.call("mlcv_embed_image", ctypes.byref(vc), arr, n.value, None, None, None, 0, None)
+    one = ctypes.c_void_p(16)
+    with pytest.raises(N.MlcvError, match="parameter count"):
+        N.call("mlcv_embed_image", ctypes.byref(vc), arr, n.value - 1, one, one, one, 0, None)
+    with pytest.raises(N.MlcvError, match="null vision parameter"):
+        N.call("mlcv_embed_image", ctypes.byref(vc), arr, n.value, one, one, one, nb.value, None)
+    with pytest.raises(N.MlcvError, match="bad argument"):
+        N.call("mlcv_embed_language", None, 4, None, 10, 8, None, None)
+    with pytest.raises(N.MlcvError, match="null"):
+        N.call("mlcv_denoise_step", None, None, None, None, None, None)
+    with pytest.raises(N.MlcvError, match="bad argument"):
+        N.call("mlcv_tile_linear", None, 4, 8, None, 8, None, 0, 0, None)
