@@ -93,7 +93,9 @@ int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mas
  * -> out [num_patches, projection_dim] f16.  `params` are the vision tower's parameters in
  * named_params order (mlcv_vision_param_count of them: 3 + 16 per layer + 4), device
  * pointers to f16.  `workspace` is caller-owned device memory of
- * mlcv_embed_image_workspace bytes.  The split-K scratch of its GEMMs is kept per device
+ * mlcv_embed_image_workspace bytes; the image is copied into it, the tower runs as a hipGraph
+ * kept per device (captured again when the parameters, workspace or config change), and the
+ * result is copied to `out`.  The split-K scratch of its GEMMs is kept per device
  * and shared with mlcv_tile_linear: calls that run concurrently on different streams of
  * one device race on it, so issue them on one stream. */
 typedef struct mlcv_vision_config {

@@ -1367,9 +1367,18 @@ int mlcv_vision_param_count(const mlcv_vision_config* cfg, int32_t* count) {
   return 0;
 }
 
+// the caller's workspace: [image copy | output | the tower's buffers], 256-byte aligned parts
+static size_t vis_io_bytes(const mlcv_vision_config& c, size_t* img_b, size_t* out_b) {
+  const size_t np = (size_t)(c.image_size / c.patch_size) * (c.image_size / c.patch_size);
+  *img_b = ((size_t)c.image_size * c.image_size * c.num_channels * 2 + 255) / 256 * 256;
+  *out_b = (np * c.projection_dim * 2 + 255) / 256 * 256;
+  return *img_b + *out_b + 256;
+}
+
 int mlcv_embed_image_workspace(const mlcv_vision_config* cfg, size_t* bytes) {
   MLCV_REQUIRE(cfg && bytes && cfg->patch_size > 0, "bad argument");
-  *bytes = vision_ws_bytes(vision_cfg(*cfg));
+  size_t ib = 0, ob = 0;
+  *bytes = vis_io_bytes(*cfg, &ib, &ob) + vision_ws_bytes(vision_cfg(*cfg));
   return 0;
 }
 
@@ -1386,10 +1395,62 @@ int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, i
   float* gws = nullptr;
   unsigned* gsync = nullptr;
   MLCV_TRY(tile_scratch(&gws, &gsync));
-  return embed_image_enqueue(vision_cfg(*cfg), reinterpret_cast<const _Float16* const*>(params),
-                             reinterpret_cast<const _Float16*>(image), reinterpret_cast<_Float16*>(out), workspace,
-                             workspace_bytes, gws, tg_ws_floats(), gsync, (int)(tg_sync_words() / 32),
-                             reinterpret_cast<hipStream_t>(stream));
+  // the ~330 launches of one image run as a hipGraph, captured on a private stream and kept
+  // per device; a call with other pointers or another config captures again
+  struct VisGraph {
+    std::vector<const void*> key;
+    hipGraphExec_t exec = nullptr;
+    hipStream_t cap = nullptr;
+  };
+  static VisGraph graphs[64];
+  int dev = 0;
+  MLCV_HIP(hipGetDevice(&dev));
+  MLCV_REQUIRE(dev >= 0 && dev < 64, "device index");
+  VisGraph& G = graphs[dev];
+  if (!G.cap) MLCV_HIP(hipStreamCreateWithFlags(&G.cap, hipStreamNonBlocking));
+  size_t img_b = 0, out_b = 0;
+  const size_t io = vis_io_bytes(*cfg, &img_b, &out_b);
+  MLCV_REQUIRE(workspace_bytes >= io, "vision workspace too small");
+  char* wbase = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255));
+  _Float16* wimg = reinterpret_cast<_Float16*>(wbase);
+  _Float16* wout = reinterpret_cast<_Float16*>(wbase + img_b);
+  char* wrest = wbase + img_b + out_b;
+  const size_t rest_bytes = workspace_bytes - (size_t)(wrest - static_cast<char*>(workspace));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  std::vector<const void*> key(params, params + count);
+  key.push_back(workspace);
+  for (int f : {cfg->image_size, cfg->patch_size, cfg->num_channels, cfg->hidden_size, cfg->intermediate_size,
+                cfg->num_hidden_layers, cfg->num_attention_heads, cfg->projection_dim})
+    key.push_back(reinterpret_cast<const void*>((intptr_t)f));
+  key.push_back(reinterpret_cast<const void*>((intptr_t)__builtin_bit_cast(int32_t, cfg->layer_norm_eps)));
+  key.push_back(reinterpret_cast<const void*>((uintptr_t)workspace_bytes));
+  if (!G.exec || G.key != key) {
+    if (G.exec) (void)hipGraphExecDestroy(G.exec);
+    G.exec = nullptr;
+    G.key.clear();
+    MLCV_HIP(hipStreamBeginCapture(G.cap, hipStreamCaptureModeThreadLocal));
+    const int r = embed_image_enqueue(vision_cfg(*cfg), reinterpret_cast<const _Float16* const*>(params), wimg,
+                                      wout, wrest, rest_bytes, gws, tg_ws_floats(), gsync,
+                                      (int)(tg_sync_words() / 32), G.cap);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(G.cap, &graph);
+    if (r != 0) {
+      if (e == hipSuccess && graph) (void)hipGraphDestroy(graph);
+      return r;
+    }
+    MLCV_HIP(e);
+    const hipError_t ie = hipGraphInstantiate(&G.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    MLCV_HIP(ie);
+    G.key = key;
+  }
+  const size_t img_bytes = (size_t)cfg->image_size * cfg->image_size * cfg->num_channels * 2;
+  const size_t out_bytes = (size_t)(cfg->image_size / cfg->patch_size) * (cfg->image_size / cfg->patch_size) *
+                           cfg->projection_dim * 2;
+  MLCV_HIP(hipMemcpyAsync(wimg, image, img_bytes, hipMemcpyDeviceToDevice, st));
+  MLCV_HIP(hipGraphLaunch(G.exec, st));
+  MLCV_HIP(hipMemcpyAsync(out, wout, out_bytes, hipMemcpyDeviceToDevice, st));
+  return 0;
 }
 
 int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,

@@ -5,10 +5,13 @@
 // The linears run on the tile GEMMs (fp32 accumulation, one fp16 rounding), followed by
 // an elementwise pass that adds the bias in fp16 and applies GELU or the residual add.
 // LayerNorm keeps its statistics in fp32 (siglip.py:20-35).  The attention follows the
-// reference's cast points (siglip.py:58-70): q * scale in fp16, logits and softmax in fp32,
-// probabilities rounded to fp16, P.V accumulated in fp32 and rounded to fp16.
+// reference's cast points (siglip.py:58-70) on the MFMA attention kernel of the step: keys
+// and q at fp32-level precision (q * scale stays fp32, where the reference rounds it to
+// fp16), fp32 logits and softmax, fp16 probabilities, P.V accumulated in fp32.  head_dim 72
+// runs padded with zeros to 128 (no logit or output changes).
 #include "kernels.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace mlcv {
@@ -92,92 +95,59 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const _Float16* __restri
     out[(size_t)r * n + c] = f2h((h2f(xr[c]) - mean) * rstd * h2f(w[c]) + h2f(b[c]));
 }
 
-constexpr int VA_ROWS = 64, VA_KEYS = 64, VA_LANES = 4;
+// q, k, v of every head from the fused projection [T][3 H hd] into the attention kernel's
+// layouts at head_dim hp >= hd, zero past hd: q [T][H][hp], k and v [H][T][hp]
+__global__ void vis_pad_qkv_kernel(const _Float16* __restrict__ qkv, int T, int H, int hd, int hp,
+                                   _Float16* __restrict__ q, _Float16* __restrict__ k, _Float16* __restrict__ v) {
+  const int t = blockIdx.x, h = blockIdx.y;
+  const _Float16* src = qkv + (size_t)t * 3 * H * hd + (size_t)h * hd;
+  for (int d = threadIdx.x; d < hp; d += blockDim.x) {
+    const bool in = d < hd;
+    const _Float16 z = (_Float16)0.f;
+    q[((size_t)t * H + h) * hp + d] = in ? src[d] : z;
+    k[((size_t)h * T + t) * hp + d] = in ? src[H * hd + d] : z;
+    v[((size_t)h * T + t) * hp + d] = in ? src[2 * H * hd + d] : z;
+  }
+}
 
-// bidirectional attention of one head over T tokens: qkv [T][3 H hd] (q | k | v), out
-// [T][H hd].  A block holds 64 query rows with 4 lanes per row (consecutive lanes of one
-// wave), each lane taking every 4th key of the tiles that stream through LDS.  Pass 1 finds
-// each row's max logit and exp sum (combined over the 4 lanes by shuffles), pass 2 forms the
-// fp16 probabilities and accumulates P.V, summed over the 4 lanes at the end.
-template <int HD>
-__global__ __launch_bounds__(VA_ROWS* VA_LANES) void vis_attention_kernel(const _Float16* __restrict__ qkv, int T,
-                                                                          int H, _Float16 qscale,
-                                                                          _Float16* __restrict__ out) {
-  constexpr int hd = HD;
-  __shared__ float ks[VA_KEYS][HD];
-  __shared__ _Float16 vs[VA_KEYS][HD];
-  const int h = blockIdx.y, tid = threadIdx.x, kl = tid % VA_LANES;
-  const int row = blockIdx.x * VA_ROWS + tid / VA_LANES;
-  const int ld = 3 * H * hd;
-  const bool ok = row < T;
-  float q[HD], acc[HD];
-#pragma unroll
-  for (int d = 0; d < hd; ++d) {
-    q[d] = h2f(hmul(qkv[(size_t)min(row, T - 1) * ld + h * hd + d], qscale));
-    acc[d] = 0.f;
-  }
-  float mx = -INFINITY, sum = 0.f;
-  for (int pass = 0; pass < 2; ++pass) {
-    for (int k0 = 0; k0 < T; k0 += VA_KEYS) {
-      const int nk = min(VA_KEYS, T - k0);
-      __syncthreads();
-      for (int i = tid; i < nk * hd; i += VA_ROWS * VA_LANES) {
-        const int j = i / hd, d = i % hd;
-        ks[j][d] = h2f(qkv[(size_t)(k0 + j) * ld + H * hd + h * hd + d]);
-        vs[j][d] = qkv[(size_t)(k0 + j) * ld + 2 * H * hd + h * hd + d];
-      }
-      __syncthreads();
-      for (int j = kl; j < nk; j += VA_LANES) {
-        float l = 0.f;
-#pragma unroll
-        for (int d = 0; d < hd; ++d) l += q[d] * ks[j][d];
-        if (pass == 0) {
-          const float m2 = fmaxf(mx, l);
-          sum = sum * expf(mx - m2) + expf(l - m2);
-          mx = m2;
-        } else {
-          const float pr = h2f(f2h(expf(l - mx) / sum));
-#pragma unroll
-          for (int d = 0; d < hd; ++d) acc[d] += pr * h2f(vs[j][d]);
-        }
-      }
-    }
-    if (pass == 0) {  // the row's max and sum over its 4 lanes
-#pragma unroll
-      for (int o = 1; o < VA_LANES; o <<= 1) {
-        const float m2 = __shfl_xor(mx, o), s2 = __shfl_xor(sum, o);
-        const float m = fmaxf(mx, m2);
-        sum = (mx == -INFINITY ? 0.f : sum * expf(mx - m)) + (m2 == -INFINITY ? 0.f : s2 * expf(m2 - m));
-        mx = m;
-      }
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < hd; ++d) {
-    acc[d] += __shfl_xor(acc[d], 1);
-    acc[d] += __shfl_xor(acc[d], 2);
-  }
-  if (ok && kl == 0) {
-#pragma unroll
-    for (int d = 0; d < hd; ++d) out[(size_t)row * H * hd + h * hd + d] = f2h(acc[d]);
-  }
+// attention output [T][H][hp] -> [T][H hd]
+__global__ void vis_unpad_kernel(const _Float16* __restrict__ o, int H, int hd, int hp, _Float16* __restrict__ out) {
+  const int t = blockIdx.x;
+  for (int i = threadIdx.x; i < H * hd; i += blockDim.x)
+    out[(size_t)t * H * hd + i] = o[((size_t)t * H + i / hd) * hp + i % hd];
+}
+
+int vis_head_pad(int hd) {
+  for (int hp : {16, 32, 64, 128, 256})
+    if (hd <= hp) return hp;
+  return 0;
+}
+
+// key splits of the attention over T tokens of H heads: one round of workgroups on the CUs
+void vis_attn_plan(int T, int H, int* nsplit, int* kps) {
+  const int rb = (T + 63) / 64;
+  const int target = std::max(1, std::max(device_cus(), 1) / (rb * H)) * rb;
+  attn_plan(T, T, 0, target, nsplit, kps);
 }
 
 }  // namespace
 
 size_t vision_ws_bytes(const VisionCfg& v) {
-  const size_t np = (size_t)(v.image_size / v.patch_size) * (v.image_size / v.patch_size);
+  const int np = (v.image_size / v.patch_size) * (v.image_size / v.patch_size);
   const size_t kp = ((size_t)v.patch_size * v.patch_size * v.num_channels + 7) / 8 * 8;
-  const size_t halfs = np * kp + (size_t)v.hidden * kp + np * v.hidden * 4 + np * 3 * v.hidden + np * v.inter;
-  return halfs * 2 + 256;
+  const int hp = vis_head_pad(v.hidden / std::max(v.heads, 1));
+  int nsplit = 1, kps = 32;
+  vis_attn_plan(np, v.heads, &nsplit, &kps);
+  const size_t halfs = (size_t)np * kp + (size_t)v.hidden * kp + (size_t)np * v.hidden * 4 +
+                       (size_t)np * 3 * v.hidden + (size_t)np * v.inter + (size_t)4 * np * v.heads * hp;
+  return halfs * 2 + attn_ws_floats(v.heads, np, hp, nsplit) * 4 + 512;
 }
 
 int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _Float16* image, _Float16* out,
                         void* ws, size_t ws_bytes, float* gemm_ws, size_t gemm_ws_floats, unsigned* gemm_sync,
                         int gemm_sync_tiles, hipStream_t st) {
   MLCV_REQUIRE(v.image_size % v.patch_size == 0 && v.hidden % v.heads == 0, "vision config");
-  const int hdv = v.hidden / v.heads;
-  MLCV_REQUIRE(hdv == 16 || hdv == 32 || hdv == 64 || hdv == 72, "vision head_dim must be 16, 32, 64 or 72");
+  MLCV_REQUIRE(vis_head_pad(v.hidden / v.heads) > 0, "vision head_dim above 256");
   MLCV_REQUIRE(v.hidden % 8 == 0 && v.inter % 8 == 0 && v.proj % 4 == 0, "vision widths must be multiples of 8");
   MLCV_REQUIRE(ws_bytes >= vision_ws_bytes(v), "vision workspace too small");
   const int side = v.image_size / v.patch_size, np = side * side, H = v.hidden, hd = H / v.heads;
@@ -198,6 +168,37 @@ int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _F
   _Float16* qkv = p;
   p += (size_t)np * 3 * H;
   _Float16* u = p;
+  p += (size_t)np * v.inter;
+  const int hp = vis_head_pad(hd);
+  _Float16* qp = p;
+  p += (size_t)np * v.heads * hp;
+  _Float16* kpd = p;
+  p += (size_t)np * v.heads * hp;
+  _Float16* vpd = p;
+  p += (size_t)np * v.heads * hp;
+  _Float16* op = p;
+  p += (size_t)np * v.heads * hp;
+  float* aws = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(p) + 255) & ~uintptr_t(255));
+  // the attention: the MFMA kernel of the step and prefill at head_dim hp, no RoPE, no mask
+  AttnArgs at{};
+  at.q = qp;
+  at.q_ld = v.heads * hp;
+  at.q_scale = (float)(1.0 / std::sqrt((double)hd));
+  at.Tq = np;
+  at.H = v.heads;
+  at.KV = v.heads;
+  at.hd = hp;
+  at.kp = kpd;
+  at.kp_f32 = 0;
+  at.vp = vpd;
+  at.Sp = np;
+  at.out = op;
+  at.out_ld = v.heads * hp;
+  vis_attn_plan(np, v.heads, &at.nsplit, &at.kps);
+  at.rows = np;
+  at.rpad = ((np + 63) / 64) * 64;
+  at.part_o = aws;
+  at.part_ml = aws + (size_t)v.heads * at.nsplit * at.rpad * hp;
 
   auto gemm = [&](const _Float16* a, int lda, const _Float16* b0, const _Float16* b1, const _Float16* b2, int n1,
                   int n2, int ldb, _Float16* c, int ldc, int M, int N, int K) {
@@ -234,21 +235,16 @@ int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _F
   MLCV_HIP(hipGetLastError());
   MLCV_TRY(gemm(patches, kp, wpad, wpad, wpad, H, H, kp, x, H, np, H, kp));
   MLCV_TRY(epi(x, H, prm[1], H, VE_BIAS_POS, nullptr, prm[2]));
-  const _Float16 qscale = (_Float16)(1.0 / std::sqrt((double)hd));
   for (int L = 0; L < v.layers; ++L) {
     const _Float16* const* lp = prm + 3 + 16 * L;  // q w,b  k w,b  v w,b  o w,b  fc1 w,b  fc2 w,b  ln1 w,b  ln2 w,b
     layernorm_kernel<<<np, 256, 0, st>>>(x, lp[12], lp[13], H, v.eps, hn);
     MLCV_HIP(hipGetLastError());
     MLCV_TRY(gemm(hn, H, lp[0], lp[2], lp[4], H, 2 * H, H, qkv, 3 * H, np, 3 * H, H));
     for (int s = 0; s < 3; ++s) MLCV_TRY(epi(qkv + s * H, 3 * H, lp[1 + 2 * s], H, VE_BIAS, nullptr, nullptr));
-    const dim3 ag((np + VA_ROWS - 1) / VA_ROWS, v.heads);
-    constexpr int NT = VA_ROWS * VA_LANES;
-    switch (hd) {
-      case 16: vis_attention_kernel<16><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      case 32: vis_attention_kernel<32><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      case 64: vis_attention_kernel<64><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-      default: vis_attention_kernel<72><<<ag, NT, 0, st>>>(qkv, np, v.heads, qscale, ctx); break;
-    }
+    vis_pad_qkv_kernel<<<dim3(np, v.heads), 128, 0, st>>>(qkv, np, v.heads, hd, hp, qp, kpd, vpd);
+    MLCV_HIP(hipGetLastError());
+    MLCV_TRY(attn_launch(at, st));
+    vis_unpad_kernel<<<np, 256, 0, st>>>(op, v.heads, hd, hp, ctx);
     MLCV_HIP(hipGetLastError());
     MLCV_TRY(gemm(ctx, H, lp[6], lp[6], lp[6], H, H, H, t, H, np, H, H));
     MLCV_TRY(epi(t, H, lp[7], H, VE_BIAS_RESIDUAL, x, nullptr));

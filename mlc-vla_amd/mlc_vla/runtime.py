@@ -157,6 +157,7 @@ class VirtualMachine:
         self._bb0 = self._nvis + (1 if self._emb else 0)  # first backbone parameter
         self._backbone = any(f in BACKBONE_FUNCS for f in ex.functions)
         self._vis_ws = None
+        self._vis_key = None  # (ids of the last parameter list, its tensors, their pointer array)
         self._ctx = ctypes.c_void_p()
         self._bound = None
         if self._backbone:
@@ -249,7 +250,12 @@ class VirtualMachine:
     def embed_image(self, image, params):
         """[1, S, S, C] channels-last -> [1, num_patches, projection_dim]: the SigLIP tower and
         the PaliGemma projector (pi0_model.py:97-99, siglip.py:73-120)."""
-        vis = self._check_params(params)[: self._nvis]
+        key = tuple(id(p) for p in params)
+        if self._vis_key is None or self._vis_key[0] != key:  # validate once per parameter list
+            vis = self._check_params(params)[: self._nvis]
+            arr = (ctypes.c_void_p * len(vis))(*[ctypes.c_void_p(t.torch.data_ptr()) for t in vis])
+            self._vis_key = (key, vis, arr)
+        _, vis, arr = self._vis_key
         (img,) = self._args("embed_image", (image,))
         s = self.ex.config.siglip
         cfg = N.VisionConfig(image_size=s.image_size, patch_size=s.patch_size, num_channels=s.num_channels,
@@ -261,7 +267,6 @@ class VirtualMachine:
             N.call("mlcv_embed_image_workspace", ctypes.byref(cfg), ctypes.byref(nbytes))
             self._vis_ws = torch.empty(nbytes.value, dtype=torch.uint8, device=self.dev.torch)
         out = empty((1, s.num_patches, s.projection_dim), self.ex.config.dtype, self.dev)
-        arr = (ctypes.c_void_p * len(vis))(*[ctypes.c_void_p(t.torch.data_ptr()) for t in vis])
         N.call("mlcv_embed_image", ctypes.byref(cfg), arr, len(vis), _ptr(img), _ptr(out),
                ctypes.c_void_p(self._vis_ws.data_ptr()), self._vis_ws.numel(), self._stream())
         return out
