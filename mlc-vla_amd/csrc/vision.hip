@@ -50,6 +50,35 @@ __global__ void vis_epilogue_kernel(_Float16* __restrict__ y, int ldy, const _Fl
                                     int mode, _Float16* __restrict__ x, int ldx, const _Float16* __restrict__ pos,
                                     int npos) {
   const int m = blockIdx.x;
+  if ((n & 7) == 0 && (ldy & 7) == 0 && (ldx & 7) == 0 &&
+      ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(x) |
+        reinterpret_cast<uintptr_t>(pos)) & 15) == 0) {
+    // 16-byte pieces, the same arithmetic per element
+    for (int c = 8 * threadIdx.x; c < n; c += 8 * blockDim.x) {
+      const h8 yv = *reinterpret_cast<const h8*>(y + (size_t)m * ldy + c), bv = *reinterpret_cast<const h8*>(b + c);
+      h8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = hadd(yv[e], bv[e]);
+        if (mode == VE_BIAS_GELU) v[e] = f2h(gelu_tanh(h2f(v[e])));
+      }
+      if (mode == VE_BIAS_RESIDUAL) {
+        h8* xp = reinterpret_cast<h8*>(x + (size_t)m * ldx + c);
+        const h8 xv = *xp;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = hadd(xv[e], v[e]);
+        *xp = v;
+        continue;
+      }
+      if (mode == VE_BIAS_POS) {
+        const h8 pv = *reinterpret_cast<const h8*>(pos + (size_t)(m % npos) * n + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = hadd(v[e], pv[e]);
+      }
+      *reinterpret_cast<h8*>(y + (size_t)m * ldy + c) = v;
+    }
+    return;
+  }
   for (int c = threadIdx.x; c < n; c += blockDim.x) {
     _Float16 v = hadd(y[(size_t)m * ldy + c], b[c]);
     if (mode == VE_BIAS_GELU) v = f2h(gelu_tanh(h2f(v)));
