@@ -146,6 +146,13 @@ def test_denoise_step_joint_vs_m0_oracle_and_m1(which, tiny, dummy):
                                         m.params).numpy()
     assert cosine(got, m1) >= 0.999999
     assert max_abs(got, m1) <= 1e-3 * max(1.0, float(np.abs(m1).max()))
+    # a second call replays the joint graph with new inputs staged into it
+    x2 = np.random.default_rng(13).standard_normal(m.x_t.shape).astype(np.float16)
+    got2 = m.runner.vm["denoise_step"](m.dev(m.prefix), m.dev(x2), m.dev(te), m.params).numpy()
+    ref2 = m0_torch.denoise_step_m0({k_: v_.astype(np.float64) for k_, v_ in m.p16.items()}, m.d,
+                                    m.prefix.astype(np.float64), x2.astype(np.float64), te.astype(np.float64))
+    _tol(got2, ref2)
+    assert not np.array_equal(got2, got)
 
 
 def test_vm_embed_language(tiny):
@@ -197,6 +204,14 @@ def test_vm_embed_image_vs_oracle(sig, tiny):
     assert np.all(np.isfinite(g))
     assert cosine(g, ref) >= 0.9999, cosine(g, ref)
     assert max_abs(g, ref) <= 2e-2 * float(np.abs(ref).max()), (max_abs(g, ref), float(np.abs(ref).max()))
+    # the second call replays the captured graph: the new image is staged into it
+    img2 = np.random.default_rng(9).standard_normal(img.shape).astype(np.float16)
+    params = [tiny.dev(P[n]) for n, _ in npar]
+    got2 = vm["embed_image"](tiny.dev(img2[None]), params).numpy()[0].astype(np.float64)
+    again = vm["embed_image"](tiny.dev(img[None]), params).numpy()[0]
+    ref2 = S.embed_image(P, sc, img2, "f16")
+    assert cosine(got2, ref2) >= 0.9999 and max_abs(got2, ref2) <= 2e-2 * float(np.abs(ref2).max())
+    np.testing.assert_array_equal(again, got[0])
 
 
 def test_sample_vs_oracle_and_graph_loop(tiny):
