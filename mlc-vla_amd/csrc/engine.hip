@@ -197,6 +197,7 @@ struct Ctx {
   // launch over a segment table).  With fork_mod the step runs them on `side` so that the
   // second piece streams while layer 0 runs; ops wait for their piece (events mod_ev).
   std::vector<OpDesc> mod_ops;
+  OpDesc mod_all;  // every modulation in one launch (16-row tiles, used without the side stream)
   hipStream_t side = nullptr;
   hipEvent_t cond_ev = nullptr;
   std::vector<hipEvent_t> mod_ev;
@@ -280,6 +281,7 @@ int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool for
     MLCV_HIP(hipStreamWaitEvent(c.side, c.cond_ev, 0));
     ms = c.side;
   }
+  if (!fork && c.mod_all.nseg > 0) return run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, M), st);
   for (int p = 0; p < (int)c.mod_ops.size(); ++p) {
     SkOp op = make_op(c, c.mod_ops[p], c.cond, c.W1, M);
     if (fork) {
@@ -850,7 +852,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       {tiles(W1, 16), W1, mb_s, 16, c.tilings.tmlp.splits},                      // time mlp
       {tiles(W1, 64), W1, mb_s, 64, 0},
       {std::max(2, c.NM - 2) * tiles(3 * W1, 64), W1, mb_s, 64, 0},              // modulation pieces
-      {std::max(2, c.NM - 2) * tiles(3 * W1, 16), W1, mb_s, 16, MOD_SPLITS},
+      {std::max(2, c.NM) * tiles(3 * W1, 16), W1, mb_s, 16, MOD_SPLITS},
       {tiles(W1, TR_AIN), c.A, mb_t, TR_AIN, SPLIT_AIN},                         // action_in
       {tiles(c.A, tile_head(c).tr), W1, mb_t, tile_head(c).tr, tile_head(c).splits},  // action_out
   };
@@ -1068,6 +1070,15 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     seg_ops(c, c.mod_ops[0], first, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
     seg_ops(c, c.mod_ops[1], rest, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
     for (OpDesc& d : c.mod_ops) d.xrow = c.small_m;
+    // one launch instead of two: the second piece's grid waits for the first anyway without
+    // the side stream, and each tile's arithmetic is the same in either grouping
+    c.mod_all = OpDesc{};
+    if (c.small_m && MOD_SPLITS == 1) {
+      std::vector<SkSeg> all(first);
+      all.insert(all.end(), rest.begin(), rest.end());
+      seg_ops(c, c.mod_all, all, W1, EPI_STORE, c.q4, gtr, MOD_SPLITS);
+      c.mod_all.xrow = true;
+    }
   }
   seg_ops(c, c.op_ain, {seg_of(c.ain, c.x16, W1, W1)}, c.A, EPI_STORE, c.q4, TR_AIN, SPLIT_AIN);
   {
@@ -1217,7 +1228,11 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
     switch (op) {
       case MLCV_OP_TIME_MOD: MLCV_TRY(enqueue_time_mod(c, c.te, 1, st, false)); break;
       case MLCV_OP_MODULATION:
-        for (const OpDesc& d : c.mod_ops) MLCV_TRY(run_op(c, d, make_op(c, d, c.cond, c.W1, 1), st));
+        if (c.mod_all.nseg > 0) {
+          MLCV_TRY(run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, 1), st));
+        } else {
+          for (const OpDesc& d : c.mod_ops) MLCV_TRY(run_op(c, d, make_op(c, d, c.cond, c.W1, 1), st));
+        }
         break;
       case MLCV_OP_QKV: MLCV_TRY(enqueue_qkv(c, layer, c.mod, st)); break;
       case MLCV_OP_ATTENTION:
