@@ -58,7 +58,7 @@ struct LayerTilings {
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
 constexpr int ATTN_TARGET = 128;  // workgroups of the step's attention (row blocks x key splits)
-constexpr int MOD_SPLITS = 1;   // modulation pieces (16-row tiles: 384 workgroups each)
+constexpr int MOD_SPLITS = 1;   // K slices of the modulation GEMV's 16-row tiles (1: whole K per tile)
 // prefetch assignments (which launch of a layer fetches which later operand into the
 // memory-side cache): the attention runs on half the CUs for the longest span of the layer
 enum : unsigned {
@@ -193,9 +193,9 @@ struct Ctx {
   std::vector<SkSeg> h_segs;
   std::vector<OpDesc> layer_ops;  // 4 per layer: qkv, o, gate_up, down
   OpDesc op_tin, op_tout, op_ain, op_aout;
-  // the adaRMS modulations in 2 pieces: layer 0's two norms, then every other norm (one
-  // launch over a segment table).  With fork_mod the step runs them on `side` so that the
-  // second piece streams while layer 0 runs; ops wait for their piece (events mod_ev).
+  // for the side stream, the adaRMS modulations in 2 pieces: layer 0's two norms, then every
+  // other norm (one launch over a segment table).  With fork_mod the step runs them on `side`
+  // so that the second piece streams while layer 0 runs; ops wait for their piece (mod_ev).
   std::vector<OpDesc> mod_ops;
   OpDesc mod_all;  // every modulation in one launch (16-row tiles, used without the side stream)
   hipStream_t side = nullptr;
