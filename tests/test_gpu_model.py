@@ -347,6 +347,29 @@ def test_multi_slab_tiles_bit_identical(kw, monkeypatch):
     np.testing.assert_array_equal(outs[1][1], outs[0][1])
 
 
+def test_side_stream_modulations_bit_identical(tiny, monkeypatch):
+    """The modulations as one launch over all 2 D + 1 norms (default) and as two pieces on
+    a second stream (MLCV_FORK_MOD=1, layer 0 first) run the same tiles: the step and the
+    graph loop are bit-identical."""
+    monkeypatch.setenv("MLCV_FORK_MOD", "1")
+    alt = Model(TINY_KWARGS)
+    monkeypatch.delenv("MLCV_FORK_MOD")
+    ref = tiny
+    pm = make_prefix_mask_np(ref.cfg.prefix_len)
+    cos, sin = make_rope_np(ref.cfg.suffix_len, ref.cfg.vlm.head_dim, ref.cfg.rope_theta,
+                            offset=ref.cfg.prefix_len)
+    te = make_time_embs(ref.cfg.num_denoise_steps, ref.cfg.action_expert.width)[3].astype(np.float16)
+    outs = []
+    for m in (ref, alt):
+        k, v = _prefill(m, pm)
+        step = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                              m.params).numpy()
+        outs.append((step, m.runner.sample_graph(m.params, m.prefix, noise=m.noise)))
+    assert np.all(np.isfinite(outs[0][0])) and np.all(np.isfinite(outs[0][1]))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1], outs[0][1])
+
+
 def test_full_size_step_vs_oracle():
     """One fp16 denoise_step_kv at the full pi0.5 shape (18 layers, width 1024, P=968, T=50)
     against the float32 oracle, with N(0,1) stand-in prefix K/V."""
