@@ -135,8 +135,10 @@ def test_embed_language_bitexact(vocab, width, n):
     np.testing.assert_array_equal(_host(out).view(np.uint16), ref.view(np.uint16))
 
 
-LIN_SHAPES = [(1, 1024, 3072), (50, 1024, 2560), (50, 2048, 1024), (50, 4096, 1024), (8, 32, 128), (50, 1024, 32),
-              (100, 256, 64), (4, 64, 16)]
+# (M, K, N): the step's modulation, q/k/v, o_proj, down and gate_up shapes, the time MLP, action_in and
+# action_out, then ragged shapes
+LIN_SHAPES = [(1, 1024, 3072), (50, 1024, 2560), (50, 2048, 1024), (50, 4096, 1024), (50, 1024, 8192), (1, 1024, 1024),
+              (50, 32, 1024), (8, 32, 128), (50, 1024, 32), (100, 256, 64), (4, 64, 16)]
 
 
 @pytest.mark.parametrize("m,k,n", LIN_SHAPES)
