@@ -11,7 +11,8 @@
  *
  * Conventions
  *  - Every function returns 0 on success, a negative code on failure
- *    (-1 HIP runtime error, -2 invalid argument, -3 not bound / unsupported);
+ *    (-1 HIP runtime error, -2 invalid argument, -3 not bound / unsupported,
+ *    -4 a persistent step ended early, reported by mlcv_sync);
  *    mlcv_last_error() returns the message of the last failure on this thread.
  *  - All tensor pointers are device pointers (HBM), row-major, no padding.
  *    "f16" is IEEE binary16, "f32" IEEE binary32.
@@ -23,6 +24,7 @@
 #ifndef MLCVLA_H_
 #define MLCVLA_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -80,7 +82,40 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * MLP and all adaRMS modulations of all steps as one M=num_steps GEMM. */
 #define MLCV_OPT_USE_GRAPH 1
 #define MLCV_OPT_HOIST_MODULATION 2
+/* MLCV_OPT_PERSIST (default 0; env MLCV_PERSIST=1): run each step after its modulations as
+ * one persistent kernel (one workgroup per CU) instead of one launch per operation. Built
+ * only for fragment-major shapes; setting it elsewhere returns an error.
+ * MLCV_OPT_PERSIST_SPIN: polls before a wait between the persistent step's phases gives up
+ * (the launch then ends early and mlcv_sync reports it). */
+#define MLCV_OPT_PERSIST 3
+#define MLCV_OPT_PERSIST_SPIN 4
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
+
+/* Synchronize `stream` and report a persistent step that ended early (a wait between its
+ * phases gave up, e.g. when its workgroups could not all be resident): returns -4 with a
+ * message and resets the context's step state; the affected outputs are invalid.  No
+ * counterpart in the reference (whose VM raises at .numpy()); the Python VM calls it where
+ * the reference would synchronize. */
+int mlcv_sync(mlcv_ctx* ctx, void* stream);
+
+/* Copy one intermediate of the last persistent step on this context to host memory `out`
+ * (testing only; no counterpart in the reference): synchronizes `stream` first.
+ *   MLCV_PROBE_X      residual stream entering layer `layer` (layer == depth: after the last) [T][W1] f16
+ *   MLCV_PROBE_Q      q roped and scaled by 1/sqrt(hd) [T][H*hd] f32 (the attention's operand)
+ *   MLCV_PROBE_K      suffix k roped [T][KV*hd] f32;  MLCV_PROBE_V  suffix v [T][KV*hd] f16
+ *   MLCV_PROBE_ATTN   joint attention output [T][H*hd] f16
+ *   MLCV_PROBE_X_MID  residual stream after the attention's gated residual [T][W1] f16
+ *   MLCV_PROBE_H      GeGLU output [T][ae_mlp] f16
+ *   MLCV_PROBE_MOD    adaRMS modulations [2 depth + 1][3 W1] f16 (layer 0) */
+#define MLCV_PROBE_X 0
+#define MLCV_PROBE_Q 1
+#define MLCV_PROBE_K 2
+#define MLCV_PROBE_V 3
+#define MLCV_PROBE_ATTN 4
+#define MLCV_PROBE_X_MID 5
+#define MLCV_PROBE_H 6
+#define MLCV_PROBE_MOD 7
+int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream);
 
 /* prefill -- Pi0Model.prefill (pi0_model.py:128-140).
  *   prefix_embs [1, P, vlm_width] f16, prefix_mask [1,1,1,P] f32 (0 / -1e9)

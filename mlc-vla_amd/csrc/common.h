@@ -84,6 +84,17 @@ __device__ __forceinline__ T load_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
   else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, AUX));
   else return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, AUX));
 }
+// Buffer stores with explicit cache-policy bits: AUX 16 (device scope, sc1) writes through
+// this XCD's L2 to the memory side, so that a workgroup on another XCD of the same launch
+// reads the value with a device-scope load once it has seen the writer's progress flag.
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+template <class T, int AUX = 16>
+__device__ __forceinline__ void store_dev(__amdgpu_buffer_rsrc_t r, int byte_off, T v) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "4, 8 or 16 bytes");
+  if constexpr (sizeof(T) == 16) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, byte_off, 0, AUX);
+  else if constexpr (sizeof(T) == 8) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, v), r, byte_off, 0, AUX);
+  else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, byte_off, 0, AUX);
+}
 // cache policy of the streamed operands (measured on the step at P=968, T=50):
 // prefix / suffix keys and values: device scope, 4 us per step faster than plain loads;
 // weights (layer GEMMs, and the row-major time-MLP / modulation GEMVs): non-temporal (2),
@@ -213,6 +224,30 @@ __device__ __forceinline__ bool group_meet_gen(unsigned* ctr, unsigned n, unsign
     __builtin_amdgcn_s_sleep(2);
   }
   return false;
+}
+
+// q4f16_1 in registers: the 8 nibbles of a word -> fp16 (q - 7) * s, ordered
+// [n0,n4,n1,n5,n2,n6,n3,n7] (0x6400 | q is 1024 + q in fp16, so (v - 1031) * s is exact
+// before its one rounding); perm8 puts 8 consecutive X values in that order.
+__device__ __forceinline__ h8 dequant_word(uint32_t word, _Float16 s) {
+  h8 r;
+  const h2 bias = {(_Float16)1031.0f, (_Float16)1031.0f};
+  const h2 sc = {s, s};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    uint32_t bits = ((word >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
+    h2 v = __builtin_bit_cast(h2, bits);
+    v = (v - bias) * sc;
+    r[2 * p] = v[0];
+    r[2 * p + 1] = v[1];
+  }
+  return r;
+}
+__device__ __forceinline__ h8 perm8(h8 v) {
+  h8 r;
+  r[0] = v[0]; r[1] = v[4]; r[2] = v[1]; r[3] = v[5];
+  r[4] = v[2]; r[5] = v[6]; r[6] = v[3]; r[7] = v[7];
+  return r;
 }
 
 // Split an fp32 value into fp16 hi + lo with hi + lo ~= x to ~2^-22 relative

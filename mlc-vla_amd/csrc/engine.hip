@@ -213,6 +213,17 @@ struct Ctx {
   unsigned* counters_side = nullptr;
   size_t ncounters_side = 0;
 
+  // persistent step (step_persistent.hip): one launch per step after the modulations, for
+  // the fragment-major shapes it is built for; off by default (MLCV_PERSIST=1 or
+  // MLCV_OPT_PERSIST turns it on); activations are per layer so every launch writes each
+  // buffer once
+  bool pk_ok = false;   // the shapes allow it (decided at create)
+  bool pk_on = false;   // ... and it is enabled
+  PkArgs pk{};          // buffers, dims and plan; weights filled at bind
+  PkLin* d_pklin = nullptr;
+  float* nscale = nullptr;  // [steps][2D+1] prescale of each norm's pre-scaled input
+  _Float16* ain16 = nullptr;  // action_in weights in fp16 (q4 models: dequantized at bind)
+
   hipStream_t cap = nullptr;
   Graph g_step, g_loop, g_prefill, g_chunk, g_m0;
 
@@ -233,6 +244,7 @@ struct Ctx {
     for (hipEvent_t e : mod_ev)
       if (e) (void)hipEventDestroy(e);
     if (d_segs) (void)hipFree(d_segs);
+    if (d_pklin) (void)hipFree(d_pklin);
   }
 };
 
@@ -275,22 +287,28 @@ int run_op(const Ctx& c, const OpDesc& d, SkOp op, hipStream_t st) { return sk_l
 int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool fork) {
   MLCV_TRY(run_op(c, c.op_tin, make_op(c, c.op_tin, te, c.W1, M), st));
   MLCV_TRY(run_op(c, c.op_tout, make_op(c, c.op_tout, c.tmp, c.W1, M), st));
+  if (c.pk_on) fork = false;  // the persistent step starts after every modulation
   hipStream_t ms = st;
   if (fork) {
     MLCV_HIP(hipEventRecord(c.cond_ev, st));
     MLCV_HIP(hipStreamWaitEvent(c.side, c.cond_ev, 0));
     ms = c.side;
   }
-  if (!fork && c.mod_all.nseg > 0) return run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, M), st);
-  for (int p = 0; p < (int)c.mod_ops.size(); ++p) {
-    SkOp op = make_op(c, c.mod_ops[p], c.cond, c.W1, M);
-    if (fork) {
-      op.ws = c.skws_side;
-      op.counters = c.counters_side;
+  if (!fork && c.mod_all.nseg > 0) {
+    MLCV_TRY(run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, M), st));
+  } else {
+    for (int p = 0; p < (int)c.mod_ops.size(); ++p) {
+      SkOp op = make_op(c, c.mod_ops[p], c.cond, c.W1, M);
+      if (fork) {
+        op.ws = c.skws_side;
+        op.counters = c.counters_side;
+      }
+      MLCV_TRY(run_op(c, c.mod_ops[p], op, ms));
+      if (fork) MLCV_HIP(hipEventRecord(c.mod_ev[p], ms));
     }
-    MLCV_TRY(run_op(c, c.mod_ops[p], op, ms));
-    if (fork) MLCV_HIP(hipEventRecord(c.mod_ev[p], ms));
   }
+  // the persistent step's prescale of every norm's pre-scaled input
+  if (c.pk_on) MLCV_TRY(pk_nscale_launch(c.mod, c.W1, M * c.NM, c.nscale, st));
   return 0;
 }
 
@@ -477,6 +495,24 @@ int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  //
 // forked: the modulation pieces run on the side stream (enqueue_time_mod with fork)
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
                  hipStream_t st, bool forked = false) {
+  if (c.pk_on) {
+    PkArgs p = c.pk;
+    const size_t mi = (size_t)(modp - c.mod) / ((size_t)3 * c.W1);  // first norm of this step
+    p.modp = modp;
+    p.nscale = c.nscale + mi;
+    p.keys = keys;
+    p.values = values;
+    p.mask = c.mask;
+    p.cos = c.cos;
+    p.sin = c.sin;
+    p.xin = c.xin16;
+    p.vout = c.vout;
+    p.x32 = c.x32;
+    p.x16 = c.xin16;
+    p.dt = (float)(-1.0 / c.NS);
+    p.euler = euler ? 1 : 0;
+    return pk_launch(p, c.q4, st);
+  }
   MLCV_TRY(wait_mod(c, 0, forked, st));
   SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
   ain.rowss_out = c.rowss;
@@ -838,6 +874,99 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   c.img_layer_bytes = attn_img_bytes(c.KV, c.P, hd);
   ALLOC(c.kvimg, (size_t)c.D * c.img_layer_bytes);
 
+  // persistent step: shapes it is built for, its plan and its per-layer activations
+  {
+    auto env_int = [](const char* name, int dflt) {
+      const char* e = std::getenv(name);
+      return e ? std::atoi(e) : dflt;
+    };
+    // K slices of o_proj / down: the largest power of two up to 4 whose slices are whole
+    // 128-column chunks per wave (q4: 512) of at most 1024 columns
+    const int unit = c.q4 ? 512 : 128;
+    auto pick = [&](int K, int want) {
+      for (int s = want; s >= 1; s >>= 1)
+        if (K % (s * unit) == 0 && K / s / 128 <= 8) return s;
+      return 0;
+    };
+    const int so = pick(nq, env_int("MLCV_PK_SO", 4)), sd = pick(c.F1, env_int("MLCV_PK_SD", 4));
+    const int G = device_cus();
+    c.pk_ok = c.frag && pk_head_dim_ok(hd) && c.A % 32 == 0 && W1 / 128 <= 8 && so > 0 && sd > 0 && G > 0 &&
+              G <= 512 && (c.KV == 1 || c.KV == c.H) && c.st_nsplit <= 32 &&
+              (!c.q4 || (W1 / 128) % 4 == 0) && c.NS * c.NM <= 65536;
+    c.pk_on = c.pk_ok && env_int("MLCV_PERSIST", 0) != 0;
+    if (c.pk_ok) {
+      PkArgs& p = c.pk;
+      p.D = c.D;
+      p.T = T;
+      p.A = c.A;
+      p.W1 = W1;
+      p.F1 = c.F1;
+      p.H = c.H;
+      p.KV = c.KV;
+      p.HD = hd;
+      p.P = c.P;
+      p.nq = nq;
+      p.nkv = nkv;
+      p.eps = cfg->rms_norm_eps;
+      p.G = G;
+      p.so = so;
+      p.sd = sd;
+      p.gu_sw = env_int("MLCV_PK_GUSW", 2) == 1 || c.F1 % 16 != 0 ? 1 : 2;
+      p.nsplit = c.st_nsplit;
+      p.kps = c.st_kps;
+      p.rows = T * (c.H / c.KV);
+      p.rpad = c.attn_rpad;
+      p.spin = (unsigned)env_int("MLCV_PK_SPIN", 1 << 22);
+      // idle workgroups of the attention phase prefetching the layer's later weights: measured
+      // slower (they compete with the attention), so off unless asked for
+      p.prefetch = env_int("MLCV_PK_PREFETCH", 0);
+      p.merge_comb = (p.rpad / 64) * c.st_nsplit * c.KV <= G && env_int("MLCV_PK_MERGE_COMB", 1) != 0;
+      auto al = [](size_t n) { return (n + 127) / 128 * 128; };  // whole 256-byte lines per layer
+      p.s_x = al((size_t)T * W1);
+      p.s_r = al((size_t)T * (W1 / 16));
+      p.s_u = al((size_t)64 * W1);
+      p.s_qf = al(qf_halfs);
+      p.s_k = al((size_t)T * nkv);
+      p.s_part = al(attn_ws_floats(c.KV, p.rows, hd, c.st_nsplit));
+      p.s_attn = al((size_t)64 * nq);
+      p.s_h = al((size_t)64 * c.F1);
+      p.s_sko = al((size_t)(W1 / 16) * so * 4 * 64 * 4);
+      p.s_skd = al((size_t)(W1 / 16) * sd * 4 * 64 * 4);
+      const size_t D1 = (size_t)c.D + 1, Dn = (size_t)c.D;
+      ALLOC(p.xres, D1 * p.s_x);
+      ALLOC(p.rres, D1 * p.s_r);
+      ALLOC(p.ures, D1 * p.s_u);
+      ALLOC(p.xmid, Dn * p.s_x);
+      ALLOC(p.rmid, Dn * p.s_r);
+      ALLOC(p.umid, Dn * p.s_u);
+      ALLOC(p.qf, Dn * p.s_qf);
+      ALLOC(p.k32, Dn * p.s_k);
+      ALLOC(p.vs, Dn * p.s_k);
+      ALLOC(p.part, Dn * p.s_part);
+      ALLOC(p.attn, Dn * p.s_attn);
+      ALLOC(p.h, Dn * p.s_h);
+      ALLOC(p.sko, Dn * p.s_sko);
+      ALLOC(p.skd, Dn * p.s_skd);
+      ALLOC(p.cnto, Dn * (W1 / 16));
+      ALLOC(p.cntd, Dn * (W1 / 16));
+      ALLOC(p.cntm, Dn * c.KV * (p.rpad / 64));
+      ALLOC(p.prog, (size_t)G);
+      ALLOC(p.err, 1);
+      ALLOC(c.nscale, (size_t)c.NS * c.NM);
+      const std::pair<void*, size_t> zero_fill[] = {
+          {p.xres, D1 * p.s_x * 2}, {p.rres, D1 * p.s_r * 4}, {p.ures, D1 * p.s_u * 2}, {p.xmid, Dn * p.s_x * 2},
+          {p.rmid, Dn * p.s_r * 4}, {p.umid, Dn * p.s_u * 2}, {p.qf, Dn * p.s_qf * 2}, {p.k32, Dn * p.s_k * 4},
+          {p.vs, Dn * p.s_k * 2}, {p.part, Dn * p.s_part * 4}, {p.attn, Dn * p.s_attn * 2}, {p.h, Dn * p.s_h * 2},
+          {p.cnto, Dn * (W1 / 16) * 4}, {p.cntd, Dn * (W1 / 16) * 4}, {p.cntm, Dn * c.KV * (p.rpad / 64) * 4},
+          {p.prog, (size_t)G * 4}, {p.err, 4}};
+      for (const auto& z : zero_fill)
+        if (hipMemset(z.first, 0, z.second) != hipSuccess) {
+          set_error("persistent step buffers: memset failed");
+          return fail(-1);
+        }
+    }
+  }
+
   // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
   const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
   struct Shape {
@@ -921,7 +1050,13 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
   Ctx& c = ctx->c;
   if (key == MLCV_OPT_USE_GRAPH) c.use_graph = value != 0;
   else if (key == MLCV_OPT_HOIST_MODULATION) c.hoist = value != 0;
-  else MLCV_REQUIRE(false, "unknown option");
+  else if (key == MLCV_OPT_PERSIST) {
+    MLCV_REQUIRE(value == 0 || c.pk_ok, "the persistent step is not built for this configuration");
+    c.pk_on = value != 0;
+  } else if (key == MLCV_OPT_PERSIST_SPIN) {
+    MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "spin limit");
+    c.pk.spin = (unsigned)value;
+  } else MLCV_REQUIRE(false, "unknown option");
   c.drop_graphs();
   return 0;
 }
@@ -934,6 +1069,9 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
   MLCV_REQUIRE(count == want, "parameter count mismatch (expected " + std::to_string(want) + ")");
   for (int i = 0; i < count; ++i) MLCV_REQUIRE(ptrs[i] != nullptr, "null parameter pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // unbound until this call has finished: a failure below leaves the context refusing every
+  // entry point ("parameters not bound") instead of pointing at freed copies
+  c.bound = false;
   c.drop_graphs();
   MLCV_HIP(hipStreamSynchronize(st));
   for (void* p : c.bind_owned) (void)hipFree(p);
@@ -1020,6 +1158,8 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
   c.h_segs.clear();
   c.layer_ops.assign(4 * c.D, OpDesc{});
   const int W1 = c.W1;
+  std::vector<PkLin> pklin;  // the persistent step's weight table [D][PK_NLIN]
+  auto pkl = [](const Lin& l) { return PkLin{l.w, l.qw, l.qs, l.b}; };
   for (int L = 0; L < c.D; ++L) {
     Layer& ly = c.layers[L];
     OpDesc* ops = &c.layer_ops[4 * L];
@@ -1028,6 +1168,7 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     const Lin fq = frag_copy(ly.q[1], 0, c.HD), fk = frag_copy(ly.k[1], 0, c.HD), fv = frag_copy(ly.v[1], 0);
     const Lin fo = frag_copy(ly.o[1], 0), fgu = frag_copy(ly.gu[1], c.F1), fdn = frag_copy(ly.dn[1], 0);
     for (const Lin* l : {&fq, &fk, &fv, &fo, &fgu, &fdn}) MLCV_REQUIRE(l->N >= 0, get_error());
+    for (const Lin* l : {&fq, &fk, &fv, &fo, &fgu, &fdn}) pklin.push_back(pkl(*l));
     {
       SkSeg sq = seg_of(fq, c.q, nq, nq), sk = seg_of(fk, c.k, nkv, nkv);
       if (c.frag) {
@@ -1086,6 +1227,20 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     MLCV_REQUIRE(fa.N >= 0, get_error());
     seg_ops(c, c.op_aout, {seg_of(fa, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, tile_head(c).tr, tile_head(c).splits);
     c.op_aout.frag = c.frag;
+    c.pk.aout = pkl(fa);
+  }
+  if (c.pk_ok) {
+    // action_in as fp16 rows (a q4 model's copy is dequantized once here)
+    c.ain16 = const_cast<_Float16*>(c.ain.w);
+    if (c.q4) {
+      MLCV_TRY(dalloc(&c.ain16, (size_t)W1 * c.A, c.bind_owned));
+      MLCV_TRY(q4_dequant_launch(c.ain.qw, c.ain.qs, c.ain16, W1, c.A, st));
+    }
+    c.pk.ain_w = c.ain16;
+    c.pk.ain_b = c.ain.b;
+    if (!c.d_pklin) MLCV_HIP(hipMalloc(&c.d_pklin, (size_t)c.D * PK_NLIN * sizeof(PkLin)));
+    MLCV_HIP(hipMemcpy(c.d_pklin, pklin.data(), pklin.size() * sizeof(PkLin), hipMemcpyHostToDevice));
+    c.pk.lw = c.d_pklin;
   }
 
   if (c.d_segs) {
@@ -1213,6 +1368,95 @@ int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask,
                      st));
   MLCV_HIP(hipMemcpyAsync(x_out, c.x32, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
   return 0;
+}
+
+int mlcv_sync(mlcv_ctx* ctx, void* stream) {
+  MLCV_REQUIRE(ctx, "null context");
+  Ctx& c = ctx->c;
+  MLCV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  if (!c.pk_ok) return 0;
+  unsigned err = 0;
+  MLCV_HIP(hipMemcpy(&err, c.pk.err, 4, hipMemcpyDeviceToHost));
+  if (err == 0) return 0;
+  // progress words and split-K counters are inconsistent after an abandoned launch: start over
+  const size_t Dn = (size_t)c.D, W16 = (size_t)c.W1 / 16;
+  MLCV_HIP(hipMemset(c.pk.prog, 0, (size_t)c.pk.G * 4));
+  MLCV_HIP(hipMemset(c.pk.cnto, 0, Dn * W16 * 4));
+  MLCV_HIP(hipMemset(c.pk.cntd, 0, Dn * W16 * 4));
+  MLCV_HIP(hipMemset(c.pk.cntm, 0, Dn * c.KV * (c.pk.rpad / 64) * 4));
+  MLCV_HIP(hipMemset(c.pk.err, 0, 4));
+  MLCV_HIP(hipDeviceSynchronize());
+  set_error("persistent step: a wait between phases gave up (error word " + std::to_string(err) +
+            "); the outputs of the calls since the last successful sync are invalid");
+  return -4;
+}
+
+int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream) {
+  MLCV_REQUIRE(ctx && out, "null argument");
+  Ctx& c = ctx->c;
+  MLCV_REQUIRE(c.pk_on, "probes need the persistent step (off or not built for this configuration)");
+  const PkArgs& p = c.pk;
+  const int T = c.T, W1 = c.W1, nq = c.H * c.HD, nkv = c.KV * c.HD;
+  const int last = what == MLCV_PROBE_X ? c.D : c.D - 1;
+  MLCV_REQUIRE(layer >= 0 && layer <= last, "probe layer out of range");
+  MLCV_TRY(mlcv_sync(ctx, stream));
+  auto fetch = [&](const void* src, size_t n, std::vector<char>& h) -> int {
+    h.resize(n);
+    MLCV_HIP(hipMemcpy(h.data(), src, n, hipMemcpyDeviceToHost));
+    return 0;
+  };
+  std::vector<char> raw;
+  const size_t L = (size_t)layer;
+  auto frag_rows = [&](const _Float16* src, int K) -> int {  // fragment-major [64][K] -> [T][K]
+    MLCV_REQUIRE(bytes == (size_t)T * K * 2, "probe output size");
+    MLCV_TRY(fetch(src, (size_t)64 * K * 2, raw));
+    const _Float16* f = reinterpret_cast<const _Float16*>(raw.data());
+    _Float16* o = static_cast<_Float16*>(out);
+    for (int m = 0; m < T; ++m)
+      for (int k = 0; k < K; ++k) o[(size_t)m * K + k] = f[xf_index(m, k)];
+    return 0;
+  };
+  switch (what) {
+    case MLCV_PROBE_X:
+      MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");
+      MLCV_HIP(hipMemcpy(out, p.xres + L * p.s_x, bytes, hipMemcpyDeviceToHost));
+      return 0;
+    case MLCV_PROBE_X_MID:
+      MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");
+      MLCV_HIP(hipMemcpy(out, p.xmid + L * p.s_x, bytes, hipMemcpyDeviceToHost));
+      return 0;
+    case MLCV_PROBE_K:
+      MLCV_REQUIRE(bytes == (size_t)T * nkv * 4, "probe output size");
+      MLCV_HIP(hipMemcpy(out, p.k32 + L * p.s_k, bytes, hipMemcpyDeviceToHost));
+      return 0;
+    case MLCV_PROBE_V:
+      MLCV_REQUIRE(bytes == (size_t)T * nkv * 2, "probe output size");
+      MLCV_HIP(hipMemcpy(out, p.vs + L * p.s_k, bytes, hipMemcpyDeviceToHost));
+      return 0;
+    case MLCV_PROBE_ATTN: return frag_rows(p.attn + L * p.s_attn, nq);
+    case MLCV_PROBE_H: return frag_rows(p.h + L * p.s_h, c.F1);
+    case MLCV_PROBE_Q: {  // hi + lo of the roped, scaled q fragments -> [T][H*hd] f32
+      MLCV_REQUIRE(bytes == (size_t)T * nq * 4, "probe output size");
+      MLCV_TRY(fetch(p.qf + L * p.s_qf, p.s_qf * 2, raw));
+      const _Float16* f = reinterpret_cast<const _Float16*>(raw.data());
+      float* o = static_cast<float*>(out);
+      const int grp = c.H / c.KV, ntiles = c.attn_rpad / 16, nks = (c.HD + 31) / 32;
+      for (int t = 0; t < T; ++t)
+        for (int h = 0; h < c.H; ++h)
+          for (int d = 0; d < c.HD; ++d) {
+            const int kvh = h / grp, row = (h % grp) * T + t;
+            o[(size_t)t * nq + h * c.HD + d] = (float)f[attn_qf_index(kvh, ntiles, nks, row, d, 0)] +
+                                              (float)f[attn_qf_index(kvh, ntiles, nks, row, d, 1)];
+          }
+      return 0;
+    }
+    case MLCV_PROBE_MOD: {  // the modulations [2D+1][3 W1] of the last step (first step of a loop)
+      MLCV_REQUIRE(layer == 0 && bytes == (size_t)c.NM * 3 * W1 * 2, "probe output size");
+      MLCV_HIP(hipMemcpy(out, c.mod, bytes, hipMemcpyDeviceToHost));
+      return 0;
+    }
+    default: MLCV_REQUIRE(false, "unknown probe");
+  }
 }
 
 int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,

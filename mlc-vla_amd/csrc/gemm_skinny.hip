@@ -39,21 +39,6 @@ constexpr int KC = 128;           // k per chunk (4 MFMA k-steps of 32)
 constexpr int MB = 64;            // m rows per block (4 MFMA m tiles)
 constexpr int MAX_SPLIT = 8;
 
-// 8 nibbles of a word -> fp16 (q - 7) * s, ordered [n0,n4,n1,n5,n2,n6,n3,n7].
-__device__ __forceinline__ h8 dequant_word(uint32_t word, _Float16 s) {
-  h8 r;
-  const h2 bias = {(_Float16)1031.0f, (_Float16)1031.0f};
-  const h2 sc = {s, s};
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    uint32_t bits = ((word >> (4 * p)) & 0x000F000Fu) | 0x64006400u;  // 1024 + q in each half
-    h2 v = __builtin_bit_cast(h2, bits);
-    v = (v - bias) * sc;                                                // exact, then one RNE
-    r[2 * p] = v[0];
-    r[2 * p + 1] = v[1];
-  }
-  return r;
-}
 
 // pre-scaled adaRMS input: fp16(x * (1 + scale)) for 4 columns
 __device__ __forceinline__ void store_xu(_Float16* p, h4 x, h4 scale) {
@@ -63,12 +48,6 @@ __device__ __forceinline__ void store_xu(_Float16* p, h4 x, h4 scale) {
   *reinterpret_cast<h4*>(p) = o;
 }
 
-__device__ __forceinline__ h8 perm8(h8 v) {
-  h8 r;
-  r[0] = v[0]; r[1] = v[4]; r[2] = v[1]; r[3] = v[5];
-  r[4] = v[2]; r[5] = v[6]; r[6] = v[3]; r[7] = v[7];
-  return r;
-}
 
 // raw weight bits of one chunk for one lane: fp16 (4 x 16 B) or q4 (16 B + one scale)
 template <bool Q4>

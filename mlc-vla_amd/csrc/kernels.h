@@ -270,6 +270,81 @@ int tg_launch(const TgArgs& a, hipStream_t st);
 
 int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStream_t st);
 
+// ---------------------------------------------------------------------------
+// Persistent step (step_persistent.hip): one launch of one workgroup per CU runs a whole
+// denoise_step_kv after the modulations -- action_in, the decoder layers (q/k/v, joint
+// attention, split combine, o_proj, gate_up, down) and the head -- as a sequence of phases.
+// Every workgroup owns fixed tasks (weight tiles, attention blocks) of each phase; it loads
+// the weights of its next task before it waits for the previous phase, and the phases
+// meet through per-workgroup progress words instead of kernel boundaries.
+// ---------------------------------------------------------------------------
+struct PkLin {
+  const _Float16* w;     // fragment-major 16-row slabs (wf_shuffle_launch), fp16, or
+  const uint32_t* qw;    // q4f16_1 blocks (wf_shuffle_q4_launch)
+  const _Float16* qs;
+  const _Float16* bias;  // [N] or null
+};
+enum : int { PK_Q = 0, PK_K, PK_V, PK_O, PK_GU, PK_DN, PK_NLIN };
+
+struct PkArgs {
+  const PkLin* lw;        // [D][PK_NLIN] weights of the decoder layers
+  PkLin aout;             // action_out, fragment-major [A][W1]
+  const _Float16* ain_w;  // action_in, row-major [W1][A]
+  const _Float16* ain_b;  // [W1]
+  const _Float16* modp;   // [2D+1][3 W1] adaRMS (scale | shift | gate) of this step
+  const float* nscale;    // [2D+1] power of two per norm with max |(1 + scale) * nscale| <= 1
+  const float* keys;      // prefix K [D][KV][P][HD] f32 (roped)
+  const _Float16* values; // prefix V [D][KV][P][HD]
+  const float* mask;      // [P] additive
+  const float* cos;       // suffix RoPE [T][HD/2]
+  const float* sin;
+  const _Float16* xin;    // x_t [T][A] fp16
+  float* vout;            // head: v [T][A] f32, or (euler) x32 += dt v and x16 = fp16(x32)
+  float* x32;
+  _Float16* x16;
+  float dt;
+  int euler;
+  // activations, each written once per launch (element strides per layer below)
+  _Float16* xres;         // [D+1][T][W1] residual stream entering layer L (D: final)
+  float* rres;            // [D+1][T][W1/16] its row sums of squares per 16 columns
+  _Float16* ures;         // [D+1][64][W1] fragment-major fp16(x (1 + scale) nscale), shift in row T
+  _Float16* xmid;         // [D][T][W1] after the attention residual
+  float* rmid;
+  _Float16* umid;
+  _Float16* qf;           // [D] q fragments (attn_qf_index)
+  float* k32;             // [D][T][nkv]
+  _Float16* vs;           // [D][T][nkv]
+  float* part;            // [D] attention split partials
+  _Float16* attn;         // [D][64][nq] fragment-major
+  _Float16* h;            // [D][64][F1] fragment-major
+  float* sko;             // [D] o_proj / down split-K partials
+  float* skd;
+  unsigned* cnto;         // [D][W1/16] split-K arrival counters (monotonic)
+  unsigned* cntd;
+  size_t s_x, s_r, s_u, s_qf, s_k, s_part, s_attn, s_h, s_sko, s_skd;
+  int D, T, A, W1, F1, H, KV, HD, P, nq, nkv;
+  float eps;
+  int G;                  // workgroups: one per CU, all resident
+  int so, sd;             // K slices of o_proj and down (powers of two)
+  int gu_sw;              // 16-row slabs per gate_up task (1 or 2)
+  int nsplit, kps, rows, rpad;  // attention plan
+  unsigned* prog;         // [G] progress words
+  unsigned* err;          // device error word (non-zero: a wait gave up)
+  unsigned* err_host;     // pinned host copy of the error word, or null
+  unsigned spin;          // polls before a wait gives up
+  int merge_comb;         // the attention's key splits combine their row block after meeting
+  unsigned* cntm;         // [D][KV][row blocks] arrival counters of those meetings (monotonic)
+  int prefetch;           // workgroups idle in the attention phase prefetch the layer's later weights
+  unsigned* sink;         // null (keeps the prefetch loads)
+};
+// device-scope error codes of the persistent step
+constexpr unsigned PK_ERR_TIMEOUT = 1;
+int pk_launch(const PkArgs& p, bool q4, hipStream_t st);
+// per-norm power-of-two prescale of `steps` x `norms` modulation vectors [3 W1] each
+int pk_nscale_launch(const _Float16* mod, int W1, int count, float* out, hipStream_t st);
+// head dims the persistent step is built for
+bool pk_head_dim_ok(int hd);
+
 // a batch of device-to-device copies in one launch (the entry points stage their inputs
 // into the context's buffers with one kernel instead of one copy launch per buffer)
 struct CopyJob {

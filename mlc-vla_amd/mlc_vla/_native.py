@@ -17,6 +17,9 @@ MLCV_QUANT_NONE = 0
 MLCV_QUANT_Q4F16_1 = 1
 MLCV_OPT_USE_GRAPH = 1
 MLCV_OPT_HOIST_MODULATION = 2
+MLCV_OPT_PERSIST = 3
+MLCV_OPT_PERSIST_SPIN = 4
+PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7}
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -51,6 +54,8 @@ SIGNATURES = {
     "mlcv_destroy": (ctypes.c_int, [_vp]),
     "mlcv_bind_params": (ctypes.c_int, [_vp, ctypes.POINTER(_vp), _i32, _vp]),
     "mlcv_set_option": (ctypes.c_int, [_vp, _i32, ctypes.c_int64]),
+    "mlcv_sync": (ctypes.c_int, [_vp, _vp]),
+    "mlcv_step_probe": (ctypes.c_int, [_vp, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
     "mlcv_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "mlcv_denoise_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "mlcv_embed_language": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _vp]),

@@ -52,19 +52,24 @@ def device(kind: str = "rocm", index: int = 0) -> Device:
 
 
 class Tensor:
-    """Device tensor with a logical dtype string (uint32 is stored as int32 bits)."""
+    """Device tensor with a logical dtype string (uint32 is stored as int32 bits).  An output
+    of a VM function carries its VM's ``check``: reading it on the host also reports a
+    persistent step of that VM that ended early (``mlcv_sync``)."""
 
-    __slots__ = ("torch", "dtype")
+    __slots__ = ("torch", "dtype", "_check")
 
-    def __init__(self, t: torch.Tensor, dtype: str):
+    def __init__(self, t: torch.Tensor, dtype: str, check=None):
         self.torch = t
         self.dtype = dtype
+        self._check = check
 
     @property
     def shape(self):
         return tuple(self.torch.shape)
 
     def numpy(self) -> np.ndarray:
+        if self._check is not None:
+            self._check()
         a = self.torch.detach().cpu().numpy()
         return a.view(np.uint32) if self.dtype == "uint32" else a
 
@@ -87,9 +92,9 @@ def tensor(arr, dev: Optional[Device] = None) -> Tensor:
     return Tensor(torch.from_numpy(a).to(dev.torch), dt)
 
 
-def empty(shape, dtype: str, dev: Optional[Device] = None) -> Tensor:
+def empty(shape, dtype: str, dev: Optional[Device] = None, check=None) -> Tensor:
     dev = dev or device()
-    return Tensor(torch.empty(tuple(shape), dtype=_TORCH[dtype], device=dev.torch), dtype)
+    return Tensor(torch.empty(tuple(shape), dtype=_TORCH[dtype], device=dev.torch), dtype, check)
 
 
 def as_tensor(x) -> Tensor:
@@ -185,6 +190,25 @@ class VirtualMachine:
     def set_hoist(self, on: bool) -> None:
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_HOIST_MODULATION, int(bool(on)))
 
+    def set_persist(self, on: bool) -> None:
+        """Run each step as one persistent kernel (off by default; only for shapes it is built for)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST, int(bool(on)))
+
+    def set_persist_spin(self, polls: int) -> None:
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST_SPIN, int(polls))
+
+    def check(self) -> None:
+        """Synchronize and raise if a persistent step of this VM ended early."""
+        if self._ctx:
+            N.call("mlcv_sync", self._ctx, self._stream())
+
+    def probe(self, what: str, layer: int, shape, dtype) -> np.ndarray:
+        """An intermediate of the last persistent step (testing): see mlcv_step_probe."""
+        out = np.empty(shape, dtype)
+        N.call("mlcv_step_probe", self._ctx, N.PROBES[what], int(layer), out.ctypes.data_as(ctypes.c_void_p),
+               out.nbytes, self._stream())
+        return out
+
     # plumbing --------------------------------------------------------------
     def _stream(self) -> ctypes.c_void_p:
         return ctypes.c_void_p(torch.cuda.current_stream(self.dev.index).cuda_stream)
@@ -207,6 +231,7 @@ class VirtualMachine:
         if key == self._bound:
             return
         arr = (ctypes.c_void_p * len(ts))(*[ctypes.c_void_p(k) for k in key])
+        self._bound = None  # a failing bind leaves the context unbound
         N.call("mlcv_bind_params", self._ctx, arr, len(ts), self._stream())
         self._bound = key
         self._keep = ts  # the caller owns them; kept alive while bound
@@ -276,7 +301,7 @@ class VirtualMachine:
         every prefix token valid, RoPE positions 0..P+T-1; returns v [1,T,A] f32."""
         self._bind(params)
         a = self._args("denoise_step", (prefix_embs, x_t, time_emb))
-        v = empty(a[1].shape, "float32", self.dev)
+        v = empty(a[1].shape, "float32", self.dev, self.check)
         N.call("mlcv_denoise_step", self._ctx, *[_ptr(t) for t in a], _ptr(v), self._stream())
         return v
 
@@ -284,22 +309,22 @@ class VirtualMachine:
         self._bind(params)
         pe, pm = self._args("prefill", (prefix_embs, prefix_mask))
         kvs = self._spec["denoise_step_kv"]["keys"].shape
-        keys = empty(kvs, "float32", self.dev)
-        values = empty(kvs, self.ex.config.dtype, self.dev)
+        keys = empty(kvs, "float32", self.dev, self.check)
+        values = empty(kvs, self.ex.config.dtype, self.dev, self.check)
         N.call("mlcv_prefill", self._ctx, _ptr(pe), _ptr(pm), _ptr(keys), _ptr(values), self._stream())
         return keys, values
 
     def denoise_step_kv(self, keys, values, x_t, time_emb, suffix_cos, suffix_sin, prefix_mask, params):
         self._bind(params)
         a = self._args("denoise_step_kv", (keys, values, x_t, time_emb, suffix_cos, suffix_sin, prefix_mask))
-        v = empty(a[2].shape, "float32", self.dev)
+        v = empty(a[2].shape, "float32", self.dev, self.check)
         N.call("mlcv_denoise_step_kv", self._ctx, *[_ptr(t) for t in a], _ptr(v), self._stream())
         return v
 
     def denoise_loop_kv(self, keys, values, x0, time_embs, suffix_cos, suffix_sin, prefix_mask, params):
         self._bind(params)
         a = self._args("denoise_loop_kv", (keys, values, x0, time_embs, suffix_cos, suffix_sin, prefix_mask))
-        x = empty(a[2].shape, "float32", self.dev)
+        x = empty(a[2].shape, "float32", self.dev, self.check)
         N.call("mlcv_denoise_loop_kv", self._ctx, *[_ptr(t) for t in a], _ptr(x), self._stream())
         return x
 
@@ -311,7 +336,7 @@ class VirtualMachine:
         x0t, te, c, s = (as_tensor(t) for t in (x0, time_embs, suffix_cos, suffix_sin))
         for arg, t in (("x0", x0t), ("time_embs", te), ("suffix_cos", c), ("suffix_sin", s)):
             _check("chunk", arg, t, lk[arg].shape, lk[arg].dtype)
-        x = empty(x0t.shape, "float32", self.dev)
+        x = empty(x0t.shape, "float32", self.dev, self.check)
         N.call("mlcv_chunk", self._ctx, _ptr(pe), _ptr(pm), _ptr(x0t), _ptr(te), _ptr(c), _ptr(s), _ptr(x),
                self._stream())
         return x
