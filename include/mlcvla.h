@@ -12,7 +12,8 @@
  * Conventions
  *  - Every function returns 0 on success, a negative code on failure
  *    (-1 HIP runtime error, -2 invalid argument, -3 not bound / unsupported,
- *    -4 a persistent step ended early, reported by mlcv_sync);
+ *    -4 a bounded device-side wait gave up -- a phase of the persistent step or a
+ *    split-K meeting of the tile GEMM -- reported by mlcv_sync or the synchronous call);
  *    mlcv_last_error() returns the message of the last failure on this thread.
  *  - All tensor pointers are device pointers (HBM), row-major, no padding.
  *    "f16" is IEEE binary16, "f32" IEEE binary32.
@@ -89,6 +90,10 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * (the launch then ends early and mlcv_sync reports it). */
 #define MLCV_OPT_PERSIST 3
 #define MLCV_OPT_PERSIST_SPIN 4
+/* MLCV_OPT_MEET_POLLS (default 2^22): polls of a split-K meeting of the prefill's tile GEMMs
+ * before a waiting workgroup gives up; the outputs of that call are then invalid and the next
+ * mlcv_sync on the context returns -4. */
+#define MLCV_OPT_MEET_POLLS 5
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 
 /* Synchronize `stream` and report a persistent step that ended early (a wait between its
@@ -212,12 +217,16 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
  *   MLCV_TILE_STORE     y = x . w^T
  *   MLCV_TILE_RESIDUAL  y = fp16(y + fp16(x . w^T))
  *   MLCV_TILE_GEGLU     y = fp16(fp16(gelu_tanh(fp16(x . wg^T))) * fp16(x . wu^T))
- * small_tiles = 1 runs the 128 x 128 tile kernel instead of the 256-row one.  Synchronous. */
+ * small_tiles = 1 runs the 128 x 128 tile kernel instead of the 256-row one.  Synchronous.
+ * meet_polls: polls of a split-K meeting before a waiting workgroup gives up (negative: the
+ * default, 2^22); a meeting that gives up makes the call return -4.  The split-K scratch is
+ * per device and shared with mlcv_embed_image: a meeting of an earlier mlcv_embed_image that
+ * gave up is reported by the next call of either. */
 #define MLCV_TILE_STORE 0
 #define MLCV_TILE_RESIDUAL 1
 #define MLCV_TILE_GEGLU 2
 int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
-                     int32_t small_tiles, void* stream);
+                     int32_t small_tiles, int32_t meet_polls, void* stream);
 
 /* Enqueue `iters` launches of one operation of denoise_step_kv on `stream`, on the
  * context's current buffers (benchmarking / profiling only; no counterpart in the

@@ -249,24 +249,6 @@ int copy_list_launch(const CopyJob* jobs, int n, hipStream_t st) {
   return 0;
 }
 
-void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps) {
-  // prefix splits of whole 32-key chunks, plus one split for the suffix block
-  const int rb = (rows + ROWS - 1) / ROWS;
-  const int chunks = (Sp + KCH - 1) / KCH;
-  int ns = (target_blocks + rb - 1) / rb - (Ts > 0 ? 1 : 0);
-  if (ns > 31) ns = 31;
-  if (ns > chunks) ns = chunks;
-  if (ns < 1) ns = 1;
-  const int cps = chunks > 0 ? (chunks + ns - 1) / ns : 1;
-  *kps = cps * KCH;
-  *nsplit = (chunks > 0 ? (chunks + cps - 1) / cps : 0) + (Ts > 0 ? 1 : 0);
-}
-
-size_t attn_ws_floats(int KV, int rows, int hd, int nsplit) {
-  const int rpad = ((rows + ROWS - 1) / ROWS) * ROWS;
-  return nsplit > 1 ? (size_t)KV * nsplit * rpad * (hd + 2) : 0;
-}
-
 int attn_launch(const AttnArgs& a, hipStream_t st) {
   MLCV_REQUIRE(a.H % a.KV == 0 && (a.KV == 1 || a.KV == a.H), "kv heads must broadcast to q heads");
   MLCV_REQUIRE(a.rows == a.Tq * (a.H / a.KV), "attention rows mismatch");

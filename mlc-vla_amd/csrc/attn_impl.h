@@ -31,12 +31,20 @@
 
 #include "kernels.h"
 
+// timeline stamps of the trace build of the persistent step (empty otherwise)
+#ifndef ATTN_STAMP
+#define ATTN_STAMP(k) \
+  do {                \
+  } while (0)
+#endif
+
 namespace mlcv {
 namespace {
 constexpr int KCH = 32;        // keys per chunk
 constexpr int ROWS = 64;       // query rows per workgroup (4 waves x 16)
 constexpr int VLD = KCH + 8;   // halfs per V^T row
 constexpr int NT = 256;        // threads per workgroup (4 waves, one 16-row query tile each)
+static_assert(ROWS == ATTN_ROWS && KCH == ATTN_KCH, "the planner's rows and chunk (plan.h)");
 
 template <int HD>
 struct AttnSmem {
@@ -584,6 +592,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
     store(R0, 0);
     if (nch > 1) store(R1, 1);
     lds_barrier();
+    ATTN_STAMP(1);
     if (nch > 2) load(2, R0);
     if (nch > 3) load(3, R1);
     for (int c = 0; c < nch; c += 2) {
@@ -603,6 +612,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
       }
     }
   };
+  ATTN_STAMP(0);
   if (QF && suffix) {
     ChunkRegs<HD> R0, R1;
     pipeline(
@@ -642,6 +652,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
         [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
   }
 
+  ATTN_STAMP(2);
   if (a.nsplit > 1) {
     // the split's output normalized by its own softmax sum (a convex combination of V
     // rows, so fp16 holds it), with (m, l) in fp32 for the combine.  The wave's 16 rows go
@@ -682,6 +693,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
         a.part_ml[pr * 2 + 1] = l_run;
       }
     }
+    ATTN_STAMP(3);
     return;
   }
   if (!row_ok) return;

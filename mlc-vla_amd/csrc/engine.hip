@@ -176,6 +176,11 @@ struct Ctx {
   size_t gemm_ws_floats = 0;
   unsigned* gemm_sync = nullptr;
   size_t gemm_sync_words = 0;
+  // error word of the prefill GEMMs' split-K meetings (pinned host memory; status_dev is its
+  // device address), read back by mlcv_sync; meet_polls bounds each meeting's wait
+  unsigned* status = nullptr;
+  unsigned* status_dev = nullptr;
+  unsigned meet_polls = TG_MEET_POLLS;
   bool gemm_small = false;  // MLCV_PREFILL_SMALL_TILES=1: the 128 x 128 tile kernel only
   // prefix K/V chunk images of every layer (built once per call from keys / values)
   char* kvimg = nullptr;
@@ -245,6 +250,7 @@ struct Ctx {
       if (e) (void)hipEventDestroy(e);
     if (d_segs) (void)hipFree(d_segs);
     if (d_pklin) (void)hipFree(d_pklin);
+    if (status) (void)hipHostFree(status);
   }
 };
 
@@ -294,8 +300,12 @@ int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool for
     MLCV_HIP(hipStreamWaitEvent(c.side, c.cond_ev, 0));
     ms = c.side;
   }
+  // with each piece of modulations, the power-of-two prescale of its norms' pre-scaled inputs
+  // (piece 0: layer 0's two norms; piece 1: the others)
+  const bool nsc = c.prescaled || c.pk_on;
   if (!fork && c.mod_all.nseg > 0) {
     MLCV_TRY(run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, M), st));
+    if (nsc) MLCV_TRY(nscale_launch(c.mod, c.W1, c.NM, M, 0, c.NM, c.nscale, st));
   } else {
     for (int p = 0; p < (int)c.mod_ops.size(); ++p) {
       SkOp op = make_op(c, c.mod_ops[p], c.cond, c.W1, M);
@@ -304,11 +314,10 @@ int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool for
         op.counters = c.counters_side;
       }
       MLCV_TRY(run_op(c, c.mod_ops[p], op, ms));
+      if (nsc) MLCV_TRY(nscale_launch(c.mod, c.W1, c.NM, M, p == 0 ? 0 : 2, p == 0 ? 2 : c.NM - 2, c.nscale, ms));
       if (fork) MLCV_HIP(hipEventRecord(c.mod_ev[p], ms));
     }
   }
-  // the persistent step's prescale of every norm's pre-scaled input
-  if (c.pk_on) MLCV_TRY(pk_nscale_launch(c.mod, c.W1, M * c.NM, c.nscale, st));
   return 0;
 }
 
@@ -328,10 +337,14 @@ Tiling tile_head(const Ctx& c) { return c.frag ? c.tilings.head : Tiling{64, 0};
 const _Float16* mod_of(const Ctx& c, const _Float16* modp, int idx) { return modp + (size_t)idx * 3 * c.W1; }
 
 // adaRMS consumer: pre-scaled X (T < 64) or the per-element prologue; m = [scale|shift|gate]
+// the prescale of the norm whose modulation vector is m (a norm of c.mod)
+const float* nsc_of(const Ctx& c, const _Float16* m) { return c.nscale + (m - c.mod) / (3 * c.W1); }
+
 void set_norm(const Ctx& c, SkOp& op, const _Float16* m) {
   op.rowss_in = c.rowss;
   if (c.prescaled) {
     op.prescaled = true;
+    op.nsc = nsc_of(c, m);
   } else {
     op.scale = m;
     op.shift = m + c.W1;
@@ -344,6 +357,7 @@ void set_next_norm(const Ctx& c, SkOp& op, const _Float16* m) {
   op.xu_out = c.xu;
   op.xu_scale = m;
   op.xu_shift = m + c.W1;
+  op.xu_nsc = nsc_of(c, m);
   op.frag_out = c.frag;
 }
 
@@ -536,6 +550,8 @@ void gemm_ws_args(const Ctx& c, TgArgs& g) {
   g.sync = c.gemm_sync;
   g.sync_tiles = (int)(c.gemm_sync_words / 32);
   g.small_tiles = c.gemm_small ? 1 : 0;
+  g.err = c.status_dev;
+  g.meet_polls = c.meet_polls;
 }
 
 // ---- prefill: expert-0 over the prefix, K/V written per layer ----------------
@@ -797,6 +813,14 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.cond, c.NS * W1);
   ALLOC(c.tmp, c.NS * W1);
   ALLOC(c.mod, (size_t)c.NS * c.NM * 3 * W1);
+  ALLOC(c.nscale, (size_t)c.NS * c.NM);
+  {  // prescale 1 until the first modulations (the per-op hooks may run a GEMM before them)
+    const std::vector<float> ones((size_t)c.NS * c.NM, 1.0f);
+    if (hipMemcpy(c.nscale, ones.data(), ones.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("prescale initialisation failed");
+      return fail(-1);
+    }
+  }
   ALLOC(c.te, c.NS * W1);
   ALLOC(c.xin16, T * c.A);
   ALLOC(c.x32, T * c.A);
@@ -952,7 +976,6 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       ALLOC(p.cntm, Dn * c.KV * (p.rpad / 64));
       ALLOC(p.prog, (size_t)G);
       ALLOC(p.err, 1);
-      ALLOC(c.nscale, (size_t)c.NS * c.NM);
       const std::pair<void*, size_t> zero_fill[] = {
           {p.xres, D1 * p.s_x * 2}, {p.rres, D1 * p.s_r * 4}, {p.ures, D1 * p.s_u * 2}, {p.xmid, Dn * p.s_x * 2},
           {p.rmid, Dn * p.s_r * 4}, {p.umid, Dn * p.s_u * 2}, {p.qf, Dn * p.s_qf * 2}, {p.k32, Dn * p.s_k * 4},
@@ -1018,6 +1041,13 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
     set_error("modulation stream / event setup failed");
     return fail(-1);
   }
+  if (hipHostMalloc(reinterpret_cast<void**>(&c.status), sizeof(unsigned), hipHostMallocMapped | hipHostMallocCoherent) !=
+          hipSuccess ||
+      hipHostGetDevicePointer(reinterpret_cast<void**>(&c.status_dev), c.status, 0) != hipSuccess) {
+    set_error("status word setup failed");
+    return fail(-1);
+  }
+  *c.status = 0;
   if (hipMemset(c.counters, 0, c.ncounters * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.gemm_sync, 0, c.gemm_sync_words * sizeof(unsigned)) != hipSuccess ||
       hipMemset(c.counters_side, 0, c.ncounters_side * sizeof(unsigned)) != hipSuccess ||
@@ -1056,6 +1086,9 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
   } else if (key == MLCV_OPT_PERSIST_SPIN) {
     MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "spin limit");
     c.pk.spin = (unsigned)value;
+  } else if (key == MLCV_OPT_MEET_POLLS) {
+    MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "meeting poll limit");
+    c.meet_polls = (unsigned)value;
   } else MLCV_REQUIRE(false, "unknown option");
   c.drop_graphs();
   return 0;
@@ -1374,6 +1407,13 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
   MLCV_REQUIRE(ctx, "null context");
   Ctx& c = ctx->c;
   MLCV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  if (const unsigned e = __atomic_load_n(c.status, __ATOMIC_ACQUIRE)) {
+    __atomic_store_n(c.status, 0u, __ATOMIC_RELEASE);
+    set_error("a split-K meeting of the prefill GEMMs gave up (error word " + std::to_string(e) +
+              "; other work held the CUs the split workgroups need); the outputs of the calls since the last "
+              "successful sync are invalid");
+    return -4;
+  }
   if (!c.pk_ok) return 0;
   unsigned err = 0;
   MLCV_HIP(hipMemcpy(&err, c.pk.err, 4, hipMemcpyDeviceToHost));
@@ -1599,12 +1639,23 @@ int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, i
 // split-K workspace and meeting counters of the standalone tile-GEMM entry points (per
 // device, kept until the process ends; the callers serialize on tile_mu)
 static std::mutex tile_mu;
-static int tile_scratch(float** ws_out, unsigned** sync_out) {
+// Per-device split-K scratch of the tile GEMM entry points (mlcv_tile_linear, mlcv_embed_image):
+// partials, meeting counters and the meetings' error word (pinned host memory: *err_out its
+// host address, *err_dev_out its device address).
+static int tile_scratch(float** ws_out, unsigned** sync_out, unsigned** err_out, unsigned** err_dev_out) {
   static float* ws[64] = {};
   static unsigned* sync[64] = {};
+  static unsigned* err[64] = {};
+  static unsigned* err_dev[64] = {};
   int dev = 0;
   MLCV_HIP(hipGetDevice(&dev));
   MLCV_REQUIRE(dev >= 0 && dev < 64, "device index");
+  if (!err[dev]) {
+    MLCV_HIP(hipHostMalloc(reinterpret_cast<void**>(&err[dev]), sizeof(unsigned),
+                           hipHostMallocMapped | hipHostMallocCoherent));
+    MLCV_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&err_dev[dev]), err[dev], 0));
+    *err[dev] = 0;
+  }
   if (!ws[dev]) {
     MLCV_HIP(hipMalloc(&ws[dev], tg_ws_floats() * sizeof(float)));
     MLCV_HIP(hipMalloc(&sync[dev], tg_sync_words() * sizeof(unsigned)));
@@ -1612,7 +1663,19 @@ static int tile_scratch(float** ws_out, unsigned** sync_out) {
   }
   *ws_out = ws[dev];
   *sync_out = sync[dev];
+  *err_out = err[dev];
+  *err_dev_out = err_dev[dev];
   return 0;
+}
+
+// a split-K meeting of an earlier call on this device's scratch gave up: report it once
+static int tile_meet_failed(unsigned* err, const char* what) {
+  const unsigned e = __atomic_load_n(err, __ATOMIC_ACQUIRE);
+  if (e == 0) return 0;
+  __atomic_store_n(err, 0u, __ATOMIC_RELEASE);
+  set_error(std::string(what) + ": a split-K meeting gave up (error word " + std::to_string(e) +
+            "; other work held the CUs the split workgroups need); that output is invalid");
+  return -4;
 }
 
 static VisionCfg vision_cfg(const mlcv_vision_config& c) {
@@ -1652,8 +1715,10 @@ int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, i
   for (int i = 0; i < count; ++i) MLCV_REQUIRE(params[i] != nullptr, "null vision parameter");
   std::lock_guard<std::mutex> lk(tile_mu);
   float* gws = nullptr;
-  unsigned* gsync = nullptr;
-  MLCV_TRY(tile_scratch(&gws, &gsync));
+  unsigned *gsync = nullptr, *gerr = nullptr, *gerr_dev = nullptr;
+  MLCV_TRY(tile_scratch(&gws, &gsync, &gerr, &gerr_dev));
+  // an earlier image whose GEMM meeting gave up is reported here (this call is not run)
+  MLCV_TRY(tile_meet_failed(gerr, "an earlier mlcv_embed_image or mlcv_tile_linear call"));
   // the ~330 launches of one image run as a hipGraph, captured on a private stream and kept
   // per device; a call with other pointers or another config captures again
   struct VisGraph {
@@ -1690,7 +1755,7 @@ int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, i
     MLCV_HIP(hipStreamBeginCapture(G.cap, hipStreamCaptureModeThreadLocal));
     const int r = embed_image_enqueue(vision_cfg(*cfg), reinterpret_cast<const _Float16* const*>(params), wimg,
                                       wout, wrest, rest_bytes, gws, tg_ws_floats(), gsync,
-                                      (int)(tg_sync_words() / 32), G.cap);
+                                      (int)(tg_sync_words() / 32), gerr_dev, G.cap);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(G.cap, &graph);
     if (r != 0) {
@@ -1713,14 +1778,14 @@ int mlcv_embed_image(const mlcv_vision_config* cfg, const void* const* params, i
 }
 
 int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t N, void* y, int32_t epi,
-                     int32_t small_tiles, void* stream) {
+                     int32_t small_tiles, int32_t meet_polls, void* stream) {
   MLCV_REQUIRE(x && w && y && M > 0 && K > 0 && N > 0, "bad argument");
   MLCV_REQUIRE(epi == TG_STORE || epi == TG_RESIDUAL || epi == TG_GEGLU, "unknown epilogue");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   std::lock_guard<std::mutex> lk(tile_mu);
   float* gws = nullptr;
-  unsigned* gsync = nullptr;
-  MLCV_TRY(tile_scratch(&gws, &gsync));
+  unsigned *gsync = nullptr, *gerr = nullptr, *gerr_dev = nullptr;
+  MLCV_TRY(tile_scratch(&gws, &gsync, &gerr, &gerr_dev));
   TgArgs g{};
   g.a = reinterpret_cast<const _Float16*>(x);
   g.lda = K;
@@ -1739,10 +1804,13 @@ int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t
   g.sync = gsync;
   g.sync_tiles = (int)(tg_sync_words() / 32);
   g.small_tiles = small_tiles ? 1 : 0;
+  g.err = gerr_dev;
+  g.meet_polls = meet_polls < 0 ? TG_MEET_POLLS : (unsigned)meet_polls;
   MLCV_HIP(hipStreamSynchronize(st));
+  MLCV_TRY(tile_meet_failed(gerr, "an earlier mlcv_embed_image call"));
   MLCV_TRY(tg_launch(g, st));
   MLCV_HIP(hipStreamSynchronize(st));
-  return 0;
+  return tile_meet_failed(gerr, "mlcv_tile_linear");
 }
 
 int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,

@@ -38,13 +38,15 @@ namespace {
 constexpr int KC = 128;           // k per chunk (4 MFMA k-steps of 32)
 constexpr int MB = 64;            // m rows per block (4 MFMA m tiles)
 constexpr int MAX_SPLIT = 8;
+static_assert(KC == SK_KC && MAX_SPLIT == SK_MAX_SPLIT, "the planner's chunk and split limits (plan.h)");
 
 
-// pre-scaled adaRMS input: fp16(x * (1 + scale)) for 4 columns
-__device__ __forceinline__ void store_xu(_Float16* p, h4 x, h4 scale) {
+// pre-scaled adaRMS input: fp16(x * (1 + scale) * c) for 4 columns (c: the norm's power-of-two
+// prescale, exact in fp32)
+__device__ __forceinline__ void store_xu(_Float16* p, h4 x, h4 scale, float c) {
   h4 o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = f2h(h2f(x[e]) * (1.0f + h2f(scale[e])));
+  for (int e = 0; e < 4; ++e) o[e] = f2h(h2f(x[e]) * (1.0f + h2f(scale[e])) * c);
   *reinterpret_cast<h4*>(p) = o;
 }
 
@@ -228,6 +230,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     xus = load_global(reinterpret_cast<const h4*>(has_xu ? op.xu_scale + ncl : zero_h));
     xush = load_global(reinterpret_cast<const h4*>(has_xu ? op.xu_shift + ncl : zero_h));
   }
+  const float xuc = op.xu_nsc ? *op.xu_nsc : 1.0f;
 
   // adaRMS row statistics: the producer's partial sums of squares per 16-column group,
   // stored [row][group]; one row per lane, every wave keeps its own copy of the row scales
@@ -495,11 +498,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       if (kg + i * KG == mtM && r16 == cM) shiftacc[slab * 4 + g] = own[i];
     __syncthreads();
     const f4 sv = shiftacc[slab * 4 + g];
+    const float nsc = op.nsc ? *op.nsc : 1.0f;
 #pragma unroll
     for (int i = 0; i < NOWN; ++i) {
       const int m = 16 * (kg + i * KG) + r16;
       const float tot = ((denom[0][m] + denom[1][m]) + denom[2][m]) + denom[3][m];
-      const float rinv = 1.0f / sqrtf(tot / (float)K + op.eps);
+      const float rinv = 1.0f / sqrtf(tot / (float)K + op.eps) / nsc;
 #pragma unroll
       for (int e = 0; e < 4; ++e) own[i][e] = fmaf(own[i][e], rinv, sv[e]);
     }
@@ -598,7 +602,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       }
       if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = o;
       if (op.xu_out && mok && nok)
-        store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), o, xus);
+        store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), o, xus, xuc);
     } else {
       h4 y;
 #pragma unroll
@@ -611,7 +615,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_SILU) {
         if (mok && nok) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(seg.out) + mo) = y;
         if (EPI == EPI_STORE && op.xu_out && mok && nok)
-          store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), y, xus);
+          store_xu(op.xu_out + (op.frag_out ? xf_index(m0 + 16 * mt + r16, n0) : mo), y, xus, xuc);
 #pragma unroll
         for (int e = 0; e < 4; ++e) s2 += h2f(y[e]) * h2f(y[e]);
       } else if constexpr (EPI == EPI_VOUT) {
@@ -827,30 +831,6 @@ int launch_q(const SkOp& op, int norm, int nc, dim3 grid, hipStream_t st) {
 
 }  // namespace
 
-SkPlan sk_plan(int ntiles, int K, int mblocks, int splits) {
-  // splits > 0: that many K slices (at most one per 128-k chunk); otherwise one wave of
-  // workgroups (<= 256, one per CU) with at most 8 splits
-  const int chunks = (K + KC - 1) / KC;
-  int want = splits;
-  if (want <= 0) {
-    const int blocks = ntiles * mblocks;
-    want = (256 + blocks - 1) / blocks;
-    if (want > MAX_SPLIT) want = MAX_SPLIT;
-  }
-  if (want > MAX_SPLIT) want = MAX_SPLIT;
-  if (want > chunks) want = chunks;
-  if (want < 1) want = 1;
-  const int cps = (chunks + want - 1) / want;
-  SkPlan p;
-  p.kper = cps * KC;
-  p.splitk = (chunks + cps - 1) / cps;
-  return p;
-}
-
-size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p, int tr) {
-  return p.splitk > 1 ? (size_t)ntiles * mblocks * p.splitk * tr * 64 : 0;
-}
-
 int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   MLCV_REQUIRE(op.K % 32 == 0 && op.K >= 32, "skinny GEMM needs K % 32 == 0");
   MLCV_REQUIRE(op.M >= 1, "skinny GEMM needs M >= 1");
@@ -944,6 +924,37 @@ int q4_dequant_launch(const uint32_t* qw, const _Float16* qs, _Float16* out, int
   MLCV_REQUIRE(K % 32 == 0, "q4 dequant needs K % 32 == 0");
   const long words = (long)N * (K / 8);
   q4_dequant_kernel<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(qw, qs, out, N, K);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+namespace {
+// one norm per workgroup
+__global__ __launch_bounds__(256) void nscale_kernel(const _Float16* __restrict__ mod, int W1, int NM, int norm_lo,
+                                                     int norms_n, float* __restrict__ out) {
+  __shared__ float red[4];
+  const int n = (blockIdx.x / norms_n) * NM + norm_lo + blockIdx.x % norms_n;
+  const _Float16* sc = mod + (size_t)n * 3 * W1;
+  float mx = 0.f;
+  for (int j = threadIdx.x; j < W1; j += 256) mx = fmaxf(mx, fabsf(1.0f + h2f(sc[j])));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float c = 1.0f;
+    if (v <= 3.0e38f) {  // finite (a NaN or inf modulation leaves c = 1)
+      while (v * c > 1.0f) c *= 0.5f;
+    }
+    out[n] = c;
+  }
+}
+}  // namespace
+
+int nscale_launch(const _Float16* mod, int W1, int NM, int steps, int norm_lo, int norms_n, float* out,
+                  hipStream_t st) {
+  MLCV_REQUIRE(steps > 0 && norms_n > 0 && W1 > 0 && norm_lo >= 0 && norm_lo + norms_n <= NM, "norm scale arguments");
+  nscale_kernel<<<steps * norms_n, 256, 0, st>>>(mod, W1, NM, norm_lo, norms_n, out);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

@@ -16,7 +16,7 @@ namespace mlcv {
 namespace {
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int LDK = BK + 8;  // halfs per LDS row
-constexpr int NXCD = 8;
+constexpr int NXCD = TG_NXCD;
 
 __device__ __forceinline__ const _Float16* brow_ptr(const TgArgs& a, int n) {
   if (n < a.n1) return a.b0 + (size_t)n * a.ldb;
@@ -159,13 +159,12 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(TgArgs a, int mtiles, in
 // XCDs round-robin by linear id); each writes its fp32 partial in the MFMA register order
 // (1 KB per store), they meet (group_meet_gen: the grid is launched only when it fits on
 // the CUs at once, so the meeting completes), and each reduces a share of the tile's blocks
-// in split order (deterministic) before the epilogue.
-constexpr int GBM = 256, GBK = 64;
-constexpr unsigned GMEET_POLLS = 1u << 22;
+// in split order (deterministic) before the epilogue.  Should other work hold CUs so that a
+// split cannot start, the waiting workgroups give up after TgArgs::meet_polls polls: they
+// write NaN and raise the error word, which the entry point reports as a failed call.
+constexpr int GBM = TG_BM, GBK = TG_BK;
 
-struct GemmPlan {
-  int bn, splitk, kt_per;  // n tile, K slices, k tiles (of 64) per slice
-  int mtiles, ntiles;      // ntiles: n tiles of BN (GeGLU: of BN/2 outputs)
+struct GemmPlan : TilePlan {
   float* ws;               // split-K partials [tile][split][4 waves][blocks][4][64] f4
   unsigned* sync;          // per tile: 32 words (arrivals, generation)
 };
@@ -411,7 +410,10 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     __shared__ int met;
     wait_all_memory();
     __syncthreads();
-    if (tid == 0) met = group_meet_gen(p.sync + 32 * tile, (unsigned)S, GMEET_POLLS);
+    if (tid == 0) {
+      met = group_meet_gen(p.sync + 32 * tile, (unsigned)S, a.meet_polls);
+      if (!met && a.err) __hip_atomic_store(a.err, TG_ERR_MEET, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     __syncthreads();
     // blocks u = (wave role, nb, mb) of the tile, u % S == s, one wave each
     const f4* base = reinterpret_cast<const f4*>(p.ws) + (size_t)tile * S * TILE_F4;
@@ -439,33 +441,23 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 
 // 256-row tile plan; false = the shape needs the 128 x 128 kernel
 bool big_plan(const TgArgs& a, GemmPlan& p) {
-  if (a.small_tiles || a.K % 8 != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
-  if (a.epi == TG_GEGLU) {
-    if (a.F % 128 != 0) return false;
-    p.bn = 256;
-    p.ntiles = a.F / 128;
-  } else {
-    if (a.N % 4 != 0) return false;
-    if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
-    // long K (down_proj): 256 x 256 tiles over up to 8 K slices load a third less through
-    // L2 than 256 x 128 tiles over 4; shorter K keeps 256 x 128 tiles
-    p.bn = (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N))
-               ? 256 : 128;
-    p.ntiles = (a.N + p.bn - 1) / p.bn;
-  }
-  p.mtiles = (a.M + GBM - 1) / GBM;
-  const int tiles = p.mtiles * p.ntiles, kts = (a.K + GBK - 1) / GBK;
-  const int slots = ((tiles + NXCD - 1) / NXCD) * NXCD;  // tile slots of the XCD-major grid
-  int S = 1;
-  if (a.epi != TG_GEGLU && a.ws && a.sync && tiles <= a.sync_tiles) {
-    // every workgroup of a split grid resident at once (one per CU), at least 4 k tiles each
-    S = std::min({8, device_cus() / slots, kts / 4});
-    const size_t part_floats = (size_t)4 * (p.bn / 64) * 4 * 4 * 64 * 4;
-    while (S > 1 && (size_t)tiles * S * part_floats > a.ws_floats) --S;
-    S = std::max(S, 1);
-  }
-  p.kt_per = (kts + S - 1) / S;
-  p.splitk = (kts + p.kt_per - 1) / p.kt_per;
+  TilePlanIn in{};
+  in.M = a.M;
+  in.N = a.N;
+  in.K = a.K;
+  in.F = a.F;
+  in.n1 = a.n1;
+  in.n2 = a.n2;
+  in.lda = a.lda;
+  in.ldb = a.ldb;
+  in.ldc = a.ldc;
+  in.geglu = a.epi == TG_GEGLU;
+  in.small_tiles = a.small_tiles != 0;
+  in.split_ws = a.ws && a.sync;
+  in.ws_floats = a.ws_floats;
+  in.sync_tiles = a.sync_tiles;
+  in.cus = device_cus();
+  if (!tile_plan(in, p)) return false;
   p.ws = a.ws;
   p.sync = a.sync;
   return true;

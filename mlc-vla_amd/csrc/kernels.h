@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "plan.h"
 
 namespace mlcv {
 
@@ -116,6 +117,11 @@ struct SkOp {
   _Float16* xu_out;
   const _Float16* xu_scale;
   const _Float16* xu_shift;
+  // power-of-two prescale of that norm (nscale_launch), or null for 1: the pre-scaled copy
+  // is fp16(x * (1 + scale) * c) with |1 + scale| c <= 1, so it stays as finite as x itself;
+  // the consumer (prescaled, nsc) divides its row factor by the same c
+  const float* xu_nsc;
+  const float* nsc;
   // fragment-major operands (16-row tiles, M < 64, K % 128 == 0): X in the xf_index
   // layout, the weights pre-shuffled by wf_shuffle_launch
   bool frag;
@@ -148,13 +154,12 @@ struct SkOp {
   Prefetch pf;           // prefetch workgroups appended as grid rows y >= splitk
 };
 
-struct SkPlan {
-  int splitk, kper;
-};
-// splits > 0: that many K slices; 0: enough to fill one wave of workgroups (<= 8)
-SkPlan sk_plan(int ntiles, int K, int mblocks, int splits);
-size_t sk_ws_floats(int ntiles, int mblocks, const SkPlan& p, int tr);
 int sk_launch(const SkOp& op, bool q4, hipStream_t st);
+// Prescale of pre-scaled adaRMS inputs: for steps x norms_n modulation vectors [3 W1] (scale,
+// shift, gate) at mod + (step * NM + norm_lo + j) * 3 W1, out[step * NM + norm_lo + j] = 2^-e
+// with e >= 0 the least such that max_k |1 + scale_k| 2^-e <= 1 (1 for a non-finite scale).
+int nscale_launch(const _Float16* mod, int W1, int NM, int steps, int norm_lo, int norms_n, float* out,
+                  hipStream_t st);
 
 // fragment-major copies of the weights of 16-row slabs for the 16-row skinny tiles:
 // fp16 block (slab s, k step ks) = 1 KB, lane 16 g + r holding W[row(s, r)][32 ks + 8 g ..
@@ -205,8 +210,6 @@ struct AttnArgs {
   Prefetch pf;           // prefetch workgroups appended as grid rows y >= nsplit
 };
 // nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
-void attn_plan(int rows, int Sp, int Ts, int target_blocks, int* nsplit, int* kps);
-size_t attn_ws_floats(int KV, int rows, int hd, int nsplit);
 // prefix K (split hi/lo), V (transposed) and mask of `layers` consecutive layers (keys /
 // values [layers][KV][Sp][hd]) as per-chunk LDS images: attn_img_bytes(KV, Sp, hd) bytes per layer
 size_t attn_img_bytes(int KV, int Sp, int hd);
@@ -228,6 +231,8 @@ enum TgEpi : int {
   TG_RESIDUAL = 1,  // C = fp16(C + fp16(acc))
   TG_GEGLU = 2,     // B rows interleaved gate/up per 32-col block; C = h [M][F]
 };
+constexpr unsigned TG_MEET_POLLS = 1u << 22;
+constexpr unsigned TG_ERR_MEET = 2;
 struct TgArgs {
   const _Float16* a; int lda;
   const _Float16* b0; const _Float16* b1; const _Float16* b2;  // up to 3 stacked weight segments
@@ -244,6 +249,11 @@ struct TgArgs {
   unsigned* sync;
   int sync_tiles;
   int small_tiles;       // 1: the 128 x 128 tile kernel only
+  // the split-K meeting's bounded wait: polls before a workgroup gives up; it then writes NaN
+  // into its part of the output and stores TG_ERR_MEET into *err (pinned host memory that the
+  // entry points read back), when err is set
+  unsigned meet_polls = TG_MEET_POLLS;
+  unsigned* err = nullptr;
 };
 // out[t] = fp16(table[ids[t]] * fp16(sqrt(width))) for n tokens (ids clamped into the table)
 int embed_language_launch(const int32_t* ids, int n, const _Float16* table, int vocab, int width, _Float16* out,
@@ -259,7 +269,7 @@ struct VisionCfg {
 size_t vision_ws_bytes(const VisionCfg& v);
 int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _Float16* image, _Float16* out,
                         void* ws, size_t ws_bytes, float* gemm_ws, size_t gemm_ws_floats, unsigned* gemm_sync,
-                        int gemm_sync_tiles, hipStream_t st);
+                        int gemm_sync_tiles, unsigned* gemm_err, hipStream_t st);
 
 // compute units of the current device (cached per device; 0 if it cannot be queried)
 int device_cus();
@@ -340,8 +350,6 @@ struct PkArgs {
 // device-scope error codes of the persistent step
 constexpr unsigned PK_ERR_TIMEOUT = 1;
 int pk_launch(const PkArgs& p, bool q4, hipStream_t st);
-// per-norm power-of-two prescale of `steps` x `norms` modulation vectors [3 W1] each
-int pk_nscale_launch(const _Float16* mod, int W1, int count, float* out, hipStream_t st);
 // head dims the persistent step is built for
 bool pk_head_dim_ok(int hd);
 

@@ -342,7 +342,7 @@ __device__ __forceinline__ bool pk_splitk(f4& own, float* ws, unsigned* cnt, int
   return true;
 }
 
-// power-of-two prescale of norm n's pre-scaled input (computed by pk_nscale_kernel)
+// power-of-two prescale of norm n's pre-scaled input (computed by nscale_launch)
 __device__ __forceinline__ float pk_nsc(CPk& p, int n) { return load_global(p.nscale + n); }
 
 // ---- epilogues that produce the residual stream -----------------------------------------
@@ -856,25 +856,6 @@ __global__ __launch_bounds__(PK_THREADS) void pstep_kernel(PkArgs args) {
   }
 }
 
-// one norm per workgroup: c = 2^-e with e >= 0 the least with max_j |1 + scale_j| c <= 1
-__global__ __launch_bounds__(256) void pk_nscale_kernel(const _Float16* __restrict__ mod, int W1, float* __restrict__ out) {
-  __shared__ float red[4];
-  const _Float16* sc = mod + (size_t)pk_bid() * 3 * W1;
-  float mx = 0.f;
-  for (int j = pk_tid(); j < W1; j += 256) mx = fmaxf(mx, fabsf(1.0f + h2f(sc[j])));
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if ((pk_tid() & 63) == 0) red[pk_tid() >> 6] = mx;
-  __syncthreads();
-  if (pk_tid() == 0) {
-    const float v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float c = 1.0f;
-    if (v <= 3.0e38f) {  // finite (a NaN or inf modulation leaves c = 1)
-      while (v * c > 1.0f) c *= 0.5f;
-    }
-    out[pk_bid()] = c;
-  }
-}
-
 }  // namespace
 
 bool pk_head_dim_ok(int hd) { return hd == 64 || hd == 128 || hd == 256; }
@@ -888,13 +869,6 @@ extern "C" void* mlcv_pk_trace_ptr() {
 }
 namespace mlcv {
 #endif
-
-int pk_nscale_launch(const _Float16* mod, int W1, int count, float* out, hipStream_t st) {
-  MLCV_REQUIRE(count > 0 && W1 > 0, "norm scale arguments");
-  pk_nscale_kernel<<<count, 256, 0, st>>>(mod, W1, out);
-  MLCV_HIP(hipGetLastError());
-  return 0;
-}
 
 int pk_launch(const PkArgs& p, bool q4, hipStream_t st) {
   MLCV_REQUIRE(p.T >= 1 && p.T < 64, "persistent step: 1 <= T < 64");

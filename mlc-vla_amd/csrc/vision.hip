@@ -174,7 +174,7 @@ size_t vision_ws_bytes(const VisionCfg& v) {
 
 int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _Float16* image, _Float16* out,
                         void* ws, size_t ws_bytes, float* gemm_ws, size_t gemm_ws_floats, unsigned* gemm_sync,
-                        int gemm_sync_tiles, hipStream_t st) {
+                        int gemm_sync_tiles, unsigned* gemm_err, hipStream_t st) {
   MLCV_REQUIRE(v.image_size % v.patch_size == 0 && v.hidden % v.heads == 0, "vision config");
   MLCV_REQUIRE(vis_head_pad(v.hidden / v.heads) > 0, "vision head_dim above 256");
   MLCV_REQUIRE(v.hidden % 8 == 0 && v.inter % 8 == 0 && v.proj % 4 == 0, "vision widths must be multiples of 8");
@@ -250,6 +250,7 @@ int embed_image_enqueue(const VisionCfg& v, const _Float16* const* prm, const _F
     g.ws_floats = gemm_ws_floats;
     g.sync = gemm_sync;
     g.sync_tiles = gemm_sync_tiles;
+    g.err = gemm_err;
     return tg_launch(g, st);
   };
   auto epi = [&](_Float16* y, int ldy, const _Float16* b, int n, int mode, _Float16* xr, const _Float16* pos) {

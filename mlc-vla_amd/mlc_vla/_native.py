@@ -19,6 +19,7 @@ MLCV_OPT_USE_GRAPH = 1
 MLCV_OPT_HOIST_MODULATION = 2
 MLCV_OPT_PERSIST = 3
 MLCV_OPT_PERSIST_SPIN = 4
+MLCV_OPT_MEET_POLLS = 5
 PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7}
 
 _vp = ctypes.c_void_p
@@ -71,7 +72,7 @@ SIGNATURES = {
     "mlcv_q4_quantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_q4_dequantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
-    "mlcv_tile_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _vp]),
+    "mlcv_tile_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "mlcv_bench_op": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
 }
 

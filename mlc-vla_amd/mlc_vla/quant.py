@@ -52,16 +52,21 @@ class GroupQuantize:
     max_int_value: int = 0
 
     def __post_init__(self):
-        assert self.kind == "group-quant"
-        qbits = _BITS[self.quantize_dtype]
-        sbits = 32 if self.storage_dtype == "uint32" else int(self.storage_dtype[4:])
-        if sbits < qbits:
-            raise ValueError("Storage unit should be greater or equal to quantized element")
-        self.num_elem_per_storage = sbits // qbits
-        if self.group_size % self.num_elem_per_storage != 0:
-            raise ValueError("Group size should be divisible by numbers of elements per storage")
-        self.num_storage_per_group = self.group_size // self.num_elem_per_storage
-        self.max_int_value = (2 ** (qbits - 1)) - 1
+        if self.kind != "group-quant":
+            raise ValueError(f"GroupQuantize covers kind 'group-quant', got {self.kind!r}")
+        bits = _BITS[self.quantize_dtype]
+        word_bits = 32 if self.storage_dtype == "uint32" else int(self.storage_dtype[4:])
+        per_word = word_bits // bits
+        if per_word == 0:
+            raise ValueError(f"a {bits}-bit {self.quantize_dtype} value does not fit in one {self.storage_dtype}")
+        if self.group_size % per_word:
+            raise ValueError(f"group_size {self.group_size} is not a whole number of {self.storage_dtype} words "
+                             f"({per_word} values each)")
+        # derived sizes: values per storage word, words per group, and the offset that maps a
+        # signed code in [-offset, offset + 1] to the unsigned value stored
+        self.num_elem_per_storage = per_word
+        self.num_storage_per_group = self.group_size // per_word
+        self.max_int_value = (1 << (bits - 1)) - 1
         self.linear_quant_axis = 0 if self.linear_weight_layout == "KN" else 1
 
     @property

@@ -197,6 +197,11 @@ class VirtualMachine:
     def set_persist_spin(self, polls: int) -> None:
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST_SPIN, int(polls))
 
+    def set_meet_polls(self, polls: int) -> None:
+        """Polls of a prefill split-K meeting before it gives up (the call's outputs are then
+        invalid and reading them raises)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_MEET_POLLS, int(polls))
+
     def check(self) -> None:
         """Synchronize and raise if a persistent step of this VM ended early."""
         if self._ctx:

@@ -13,6 +13,7 @@ t = 1; v = velocity(x, t); x = x + dt*v; t += dt (python/mlc_vla/sample.py:1-14,
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import List, Optional, Tuple
 
 import numpy as np
@@ -73,6 +74,15 @@ def euler_loop(step_fn, x0: np.ndarray, num_steps: int) -> np.ndarray:
     return x
 
 
+@dataclass
+class _PrefixState:
+    keys: "runtime.Tensor"
+    values: "runtime.Tensor"
+    mask: "runtime.Tensor"
+    cos: "runtime.Tensor"
+    sin: "runtime.Tensor"
+
+
 class PiZeroRunner:
     """Prefill + denoise orchestration over the gfx950 kernels (sample.py:77-187)."""
 
@@ -92,58 +102,49 @@ class PiZeroRunner:
         """numpy weights (named_params order) -> device tensors."""
         return [runtime.tensor(a, self.dev) for a in arrays]
 
-    def _unpack(self, ret):
-        if hasattr(ret, "numpy"):
-            return [ret]
-        return [ret[i] for i in range(len(ret))]
-
-    def _prepare(self, params, prefix_embs: np.ndarray, prefix_pad):
-        """prefill + prefix mask + suffix RoPE (offset = number of valid prefix tokens)."""
+    def _prefix_state(self, params, prefix_embs: np.ndarray, prefix_pad) -> "_PrefixState":
+        """Everything the denoise steps of one chunk read: the prefix K/V cache from prefill,
+        the additive prefix mask and the suffix RoPE tables, whose positions start after the
+        valid prefix tokens (no pad mask: all of them)."""
         cfg = self.config
-        if prefix_pad is None:
-            num_valid = cfg.prefix_len
-            mask_np = make_prefix_mask_np(cfg.prefix_len)
-        else:
-            num_valid = int(np.asarray(prefix_pad).reshape(-1).sum())
-            mask_np = make_prefix_mask_np(cfg.prefix_len, pad_mask=prefix_pad)
-        prefix_mask = runtime.tensor(mask_np, self.dev)
-        cos_np, sin_np = make_rope_np(cfg.suffix_len, cfg.vlm.head_dim, cfg.rope_theta, offset=num_valid)
-        suffix_cos = runtime.tensor(cos_np, self.dev)
-        suffix_sin = runtime.tensor(sin_np, self.dev)
-        prefix_dev = runtime.tensor(np.asarray(prefix_embs).astype(cfg.dtype), self.dev)
-        keys, values = self._unpack(self.vm["prefill"](prefix_dev, prefix_mask, params))
-        return keys, values, prefix_mask, suffix_cos, suffix_sin, num_valid
+        on_dev = lambda a: runtime.tensor(a, self.dev)  # noqa: E731
+        mask_np = make_prefix_mask_np(cfg.prefix_len, pad_mask=prefix_pad)
+        first_suffix_pos = int(np.count_nonzero(mask_np == 0.0))
+        cos_np, sin_np = make_rope_np(cfg.suffix_len, cfg.vlm.head_dim, cfg.rope_theta, offset=first_suffix_pos)
+        mask = on_dev(mask_np)
+        keys, values = self.vm.prefill(on_dev(np.asarray(prefix_embs, dtype=cfg.dtype)), mask, params)
+        return _PrefixState(keys, values, mask, on_dev(cos_np), on_dev(sin_np))
 
-    def _noise(self, noise, seed):
+    def _start_noise(self, noise, seed: int) -> np.ndarray:
+        """x at t = 1: the caller's noise, else N(0, 1) from numpy's default_rng(seed)."""
         cfg = self.config
         if noise is None:
-            rng = np.random.default_rng(seed)
-            noise = rng.standard_normal((1, cfg.action_horizon, cfg.action_dim)).astype(np.float32)
-        return np.asarray(noise).astype(np.float32)
+            noise = np.random.default_rng(seed).standard_normal((1, cfg.action_horizon, cfg.action_dim))
+        return np.asarray(noise, dtype=np.float32)
 
     def sample(self, params, prefix_embs: np.ndarray, noise: Optional[np.ndarray] = None, num_steps: int = 10,
                seed: int = 0, prefix_pad: Optional[np.ndarray] = None) -> np.ndarray:
         """Host Euler loop: one denoise_step_kv per step, host<->device each step."""
         cfg = self.config
         dt = cfg.dtype
-        keys, values, pmask, scos, ssin, _ = self._prepare(params, prefix_embs, prefix_pad)
-        noise = self._noise(noise, seed)
+        st = self._prefix_state(params, prefix_embs, prefix_pad)
         te_dev = [runtime.tensor(te.astype(dt), self.dev) for te in make_time_embs(num_steps, cfg.action_expert.width)]
 
         def step_fn(x_np, i):
             x_dev = runtime.tensor(x_np.astype(dt), self.dev)
-            v = self.vm["denoise_step_kv"](keys, values, x_dev, te_dev[i], scos, ssin, pmask, params)
+            v = self.vm["denoise_step_kv"](st.keys, st.values, x_dev, te_dev[i], st.cos, st.sin, st.mask, params)
             return v.numpy()
 
-        return euler_loop(step_fn, noise, num_steps)
+        return euler_loop(step_fn, self._start_noise(noise, seed), num_steps)
 
     def sample_graph(self, params, prefix_embs: np.ndarray, noise: Optional[np.ndarray] = None, seed: int = 0,
                      prefix_pad: Optional[np.ndarray] = None) -> np.ndarray:
         """Device Euler loop (denoise_loop_kv): config.num_denoise_steps steps in one call."""
         cfg = self.config
         n = cfg.num_denoise_steps
-        keys, values, pmask, scos, ssin, _ = self._prepare(params, prefix_embs, prefix_pad)
-        x0 = runtime.tensor(self._noise(noise, seed), self.dev)
+        st = self._prefix_state(params, prefix_embs, prefix_pad)
+        x0 = runtime.tensor(self._start_noise(noise, seed), self.dev)
         tes = np.concatenate(make_time_embs(n, cfg.action_expert.width), axis=0).astype(cfg.dtype)
-        out = self.vm["denoise_loop_kv"](keys, values, x0, runtime.tensor(tes, self.dev), scos, ssin, pmask, params)
+        out = self.vm["denoise_loop_kv"](st.keys, st.values, x0, runtime.tensor(tes, self.dev), st.cos, st.sin,
+                                         st.mask, params)
         return out.numpy()

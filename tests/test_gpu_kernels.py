@@ -94,7 +94,7 @@ def test_tile_linear_vs_exact(m, k, n, epi, small):
     w = (torch.randn((rows, k), generator=g, device="cuda") / k ** 0.5).half()
     y0 = torch.randn((m, n), generator=g, device="cuda").half()
     y = y0.clone() if epi == 1 else torch.empty((m, n), dtype=torch.float16, device="cuda")
-    N.call("mlcv_tile_linear", _p(x), m, k, _p(w), n, _p(y), epi, small, _st())
+    N.call("mlcv_tile_linear", _p(x), m, k, _p(w), n, _p(y), epi, small, -1, _st())
     exact = x.double() @ w.double().T
     slack = 8 * 2.0 ** -24 * k ** 0.5 * ((x.double() ** 2) @ (w.double() ** 2).T).sqrt()
     got = y.double()

@@ -91,4 +91,4 @@ def test_vision_and_embedding_queries_and_argument_checks():
     with pytest.raises(N.MlcvError, match="null"):
         N.call("mlcv_denoise_step", None, None, None, None, None, None)
     with pytest.raises(N.MlcvError, match="bad argument"):
-        N.call("mlcv_tile_linear", None, 4, 8, None, 8, None, 0, 0, None)
+        N.call("mlcv_tile_linear", None, 4, 8, None, 8, None, 0, 0, -1, None)
