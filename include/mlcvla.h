@@ -103,15 +103,19 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
  * the reference would synchronize. */
 int mlcv_sync(mlcv_ctx* ctx, void* stream);
 
-/* Copy one intermediate of the last persistent step on this context to host memory `out`
- * (testing only; no counterpart in the reference): synchronizes `stream` first.
+/* Copy one intermediate of the last step on this context to host memory `out` (testing
+ * only; no counterpart in the reference): synchronizes `stream` first.  The persistent step
+ * keeps every layer's intermediates; the launch chain (fragment-major form, T < 64) reuses
+ * one set of buffers, which hold the outputs of the last operation run (mlcv_bench_op): there
+ * `layer` must be 0.
  *   MLCV_PROBE_X      residual stream entering layer `layer` (layer == depth: after the last) [T][W1] f16
  *   MLCV_PROBE_Q      q roped and scaled by 1/sqrt(hd) [T][H*hd] f32 (the attention's operand)
  *   MLCV_PROBE_K      suffix k roped [T][KV*hd] f32;  MLCV_PROBE_V  suffix v [T][KV*hd] f16
  *   MLCV_PROBE_ATTN   joint attention output [T][H*hd] f16
  *   MLCV_PROBE_X_MID  residual stream after the attention's gated residual [T][W1] f16
  *   MLCV_PROBE_H      GeGLU output [T][ae_mlp] f16
- *   MLCV_PROBE_MOD    adaRMS modulations [2 depth + 1][3 W1] f16 (layer 0) */
+ *   MLCV_PROBE_MOD    adaRMS modulations [2 depth + 1][3 W1] f16 (layer 0)
+ *   MLCV_PROBE_VOUT   the velocity of the last head [T][A] f32 (layer 0) */
 #define MLCV_PROBE_X 0
 #define MLCV_PROBE_Q 1
 #define MLCV_PROBE_K 2
@@ -120,6 +124,7 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream);
 #define MLCV_PROBE_X_MID 5
 #define MLCV_PROBE_H 6
 #define MLCV_PROBE_MOD 7
+#define MLCV_PROBE_VOUT 8
 int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream);
 
 /* prefill -- Pi0Model.prefill (pi0_model.py:128-140).
@@ -198,6 +203,15 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
                          int32_t k_f32, const void* vp, int32_t Sp, const float* mask, const void* ks,
                          const void* vs, int32_t Ts, void* out, void* stream);
 
+/* The prefill's attention kernel as prefill runs it (attn_prefill_e0, gemma_dual.py:236-253,
+ * 334-341; testing): q [P][q_ld] f16 as the q/k/v projection leaves it (heads of hd columns
+ * from column 0, not yet roped), roped with cos / sin [P][hd/2] f32 and scaled by 1/sqrt(hd)
+ * in the kernel; keys [KV][P][hd] f32 roped and values [KV][P][hd] f16 (one layer of the
+ * cache), mask [P] f32 additive -> out [P][H*hd] f16.  The same split plan as prefill. */
+int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const float* sin, int32_t P, int32_t H,
+                           int32_t KV, int32_t hd, const float* keys, const void* values, const float* mask, void* out,
+                           void* stream);
+
 /* Group quantization q4f16_1 (quant.py:217-266 + pack_weight :65-86):
  * w [N,K] f16 -> q_weight [N, K/8] u32, q_scale [N, K/32] f16. */
 int mlcv_q4_quantize(const void* w, uint32_t* q_weight, void* q_scale, int32_t N, int32_t K, void* stream);
@@ -241,6 +255,7 @@ int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t
 #define MLCV_OP_DOWN 6       /* down + gated residual */
 #define MLCV_OP_HEAD 7       /* final adaRMS + action_out_proj */
 #define MLCV_OP_ATTENTION_ONLY 8 /* MLCV_OP_ATTENTION without the workgroups that prefetch the next ops' weights */
+#define MLCV_OP_ACTION_IN 9  /* action_in_proj: the residual stream entering layer 0 */
 int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
                   void* stream);
 

@@ -258,6 +258,17 @@ namespace {
 
 size_t kv_slice(const Ctx& c) { return (size_t)c.KV * c.P * c.HD; }
 
+// Workgroup target of the prefill's attention plan: as many key splits as let every workgroup
+// (one per CU) run in one round -- at P = 968, 121 row blocks x 2 splits on 256 CUs (-0.18 ms
+// against 3 splits in 1.4 rounds); MLCV_PF_ATTN_TARGET sets it instead (tuning).
+int prefill_attn_target(int rows) {
+  const int rb = (rows + 63) / 64;
+  int target = std::max(1, std::max(device_cus(), 1) / rb) * rb;
+  if (const char* e = std::getenv("MLCV_PF_ATTN_TARGET"))
+    if (std::atoi(e) > 0) target = std::atoi(e);
+  return target;
+}
+
 SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   SkOp op{};
   op.x = x;
@@ -505,6 +516,13 @@ int enqueue_head(Ctx& c, const _Float16* modp, bool euler, hipStream_t st) {  //
   return run_op(c, c.op_aout, op, st);
 }
 
+int enqueue_action_in(Ctx& c, const _Float16* modp, hipStream_t st) {  // action_in_proj -> x, layer 0's norm input
+  SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
+  ain.rowss_out = c.rowss;
+  set_next_norm(c, ain, mod_of(c, modp, 0));
+  return run_op(c, c.op_ain, ain, st);
+}
+
 // ---- one suffix-only velocity evaluation (modulations already in modp) -------
 // forked: the modulation pieces run on the side stream (enqueue_time_mod with fork)
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
@@ -528,10 +546,7 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
     return pk_launch(p, c.q4, st);
   }
   MLCV_TRY(wait_mod(c, 0, forked, st));
-  SkOp ain = make_op(c, c.op_ain, c.xin16, c.A, c.T);
-  ain.rowss_out = c.rowss;
-  set_next_norm(c, ain, mod_of(c, modp, 0));
-  MLCV_TRY(run_op(c, c.op_ain, ain, st));
+  MLCV_TRY(enqueue_action_in(c, modp, st));
   for (int L = 0; L < c.D; ++L) {
     MLCV_TRY(enqueue_qkv(c, L, modp, st, keys, values));
     MLCV_TRY(enqueue_attn(c, L, keys, values, st));
@@ -541,6 +556,39 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
     MLCV_TRY(enqueue_down(c, L, modp, st));
   }
   return enqueue_head(c, modp, euler, st);
+}
+
+// The prefill's attention (attn_prefill_e0, gemma_dual.py:236-253,334-341): q straight from
+// the q/k/v GEMM (roped and scaled in the attention's loader), the layer's roped fp32 keys and
+// fp16 values from the cache, the prefix pad mask, no suffix block.
+AttnArgs prefill_attn_args(const _Float16* q, int q_ld, const float* cos, const float* sin, int P, int H, int KV,
+                           int HD, const float* keys, const _Float16* values, const float* mask, _Float16* out,
+                           int nsplit, int kps, float* ws) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_ld = q_ld;
+  a.cos = cos;
+  a.sin = sin;
+  a.q_scale = 1.0f / std::sqrt((float)HD);
+  a.Tq = P;
+  a.H = H;
+  a.KV = KV;
+  a.hd = HD;
+  a.kp = keys;
+  a.kp_f32 = 1;
+  a.vp = values;
+  a.Sp = P;
+  a.mask = mask;
+  a.Ts = 0;
+  a.out = out;
+  a.out_ld = H * HD;
+  a.nsplit = nsplit;
+  a.kps = kps;
+  a.rows = P * (H / KV);
+  a.rpad = ((a.rows + 63) / 64) * 64;
+  a.part_o = ws;
+  a.part_ml = ws + (size_t)KV * nsplit * a.rpad * HD;
+  return a;
 }
 
 // the prefill GEMMs' split-K workspace (shared: the launches are ordered on one stream)
@@ -582,31 +630,9 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     MLCV_TRY(tg_launch(g, st));
     MLCV_TRY(kv_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.KV, HD, kL, vL, st));
     if (L == c.D - 1) break;  // the last layer's attention / MLP feed no output
-    AttnArgs a{};
-    a.q = c.pqkv;
-    a.q_ld = nqkv;
-    a.cos = c.pcos;
-    a.sin = c.psin;
-    a.q_scale = 1.0f / std::sqrt((float)HD);
-    a.Tq = P;
-    a.H = c.H;
-    a.KV = c.KV;
-    a.hd = HD;
-    a.kp = kL;
-    a.kp_f32 = 1;
-    a.vp = vL;
-    a.Sp = P;
-    a.mask = c.mask;
-    a.Ts = 0;
-    a.out = c.pctx;
-    a.out_ld = nq;
-    a.nsplit = c.pf_nsplit;
-    a.kps = c.pf_kps;
-    a.rows = P * (c.H / c.KV);
-    a.rpad = ((a.rows + 63) / 64) * 64;
-    a.part_o = c.attn_ws;
-    a.part_ml = c.attn_ws + (size_t)c.KV * a.nsplit * a.rpad * HD;
-    MLCV_TRY(attn_launch(a, st));
+    MLCV_TRY(attn_launch(prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
+                                           c.pf_nsplit, c.pf_kps, c.attn_ws),
+                         st));
     TgArgs o{};
     o.a = c.pctx;
     o.lda = nq;
@@ -880,14 +906,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // the step's attention: about ATTN_TARGET workgroups (MLCV_ATTN_TARGET overrides, tuning)
   const int attn_target = std::getenv("MLCV_ATTN_TARGET") ? std::atoi(std::getenv("MLCV_ATTN_TARGET")) : ATTN_TARGET;
   attn_plan(st_rows, c.P, T, attn_target > 0 ? attn_target : ATTN_TARGET, &c.st_nsplit, &c.st_kps);
-  // the prefill's attention: as many key splits as let every workgroup (one per CU) run in
-  // one round: at P = 968, 121 row blocks x 2 splits on 256 CUs (-0.18 ms against 3 splits
-  // in 1.4 rounds); MLCV_PF_ATTN_TARGET sets the workgroup target instead (tuning)
-  const int pf_rb = (pf_rows + 63) / 64;
-  int pf_target = std::max(1, std::max(device_cus(), 1) / pf_rb) * pf_rb;
-  if (const char* e = std::getenv("MLCV_PF_ATTN_TARGET"))
-    if (std::atoi(e) > 0) pf_target = std::atoi(e);
-  attn_plan(pf_rows, c.P, 0, pf_target, &c.pf_nsplit, &c.pf_kps);
+  attn_plan(pf_rows, c.P, 0, prefill_attn_target(pf_rows), &c.pf_nsplit, &c.pf_kps);
   c.attn_ws_floats_n = std::max(attn_ws_floats(c.KV, st_rows, hd, c.st_nsplit),
                                 attn_ws_floats(c.KV, pf_rows, hd, c.pf_nsplit));
   ALLOC(c.attn_ws, c.attn_ws_floats_n);
@@ -1434,10 +1453,13 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
 int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream) {
   MLCV_REQUIRE(ctx && out, "null argument");
   Ctx& c = ctx->c;
-  MLCV_REQUIRE(c.pk_on, "probes need the persistent step (off or not built for this configuration)");
+  // the persistent step keeps every layer's intermediates; the launch chain reuses one set of
+  // buffers, which hold the outputs of the last operation run (layer 0 names them)
+  const bool chain = !c.pk_on;
+  MLCV_REQUIRE(!chain || c.frag, "probes of the launch chain need its fragment-major form (T < 64)");
   const PkArgs& p = c.pk;
   const int T = c.T, W1 = c.W1, nq = c.H * c.HD, nkv = c.KV * c.HD;
-  const int last = what == MLCV_PROBE_X ? c.D : c.D - 1;
+  const int last = chain ? 0 : what == MLCV_PROBE_X ? c.D : c.D - 1;
   MLCV_REQUIRE(layer >= 0 && layer <= last, "probe layer out of range");
   MLCV_TRY(mlcv_sync(ctx, stream));
   auto fetch = [&](const void* src, size_t n, std::vector<char>& h) -> int {
@@ -1456,28 +1478,33 @@ int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_
       for (int k = 0; k < K; ++k) o[(size_t)m * K + k] = f[xf_index(m, k)];
     return 0;
   };
+  const size_t qf_halfs = (size_t)c.KV * c.attn_rpad * ((c.HD + 31) / 32) * 64;
   switch (what) {
     case MLCV_PROBE_X:
       MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");
-      MLCV_HIP(hipMemcpy(out, p.xres + L * p.s_x, bytes, hipMemcpyDeviceToHost));
+      MLCV_HIP(hipMemcpy(out, chain ? c.x16 : p.xres + L * p.s_x, bytes, hipMemcpyDeviceToHost));
       return 0;
     case MLCV_PROBE_X_MID:
       MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");
-      MLCV_HIP(hipMemcpy(out, p.xmid + L * p.s_x, bytes, hipMemcpyDeviceToHost));
+      MLCV_HIP(hipMemcpy(out, chain ? c.x16 : p.xmid + L * p.s_x, bytes, hipMemcpyDeviceToHost));
       return 0;
     case MLCV_PROBE_K:
       MLCV_REQUIRE(bytes == (size_t)T * nkv * 4, "probe output size");
-      MLCV_HIP(hipMemcpy(out, p.k32 + L * p.s_k, bytes, hipMemcpyDeviceToHost));
+      MLCV_HIP(hipMemcpy(out, chain ? c.k32 : p.k32 + L * p.s_k, bytes, hipMemcpyDeviceToHost));
       return 0;
     case MLCV_PROBE_V:
       MLCV_REQUIRE(bytes == (size_t)T * nkv * 2, "probe output size");
-      MLCV_HIP(hipMemcpy(out, p.vs + L * p.s_k, bytes, hipMemcpyDeviceToHost));
+      MLCV_HIP(hipMemcpy(out, chain ? c.v : p.vs + L * p.s_k, bytes, hipMemcpyDeviceToHost));
       return 0;
-    case MLCV_PROBE_ATTN: return frag_rows(p.attn + L * p.s_attn, nq);
-    case MLCV_PROBE_H: return frag_rows(p.h + L * p.s_h, c.F1);
+    case MLCV_PROBE_ATTN: return frag_rows(chain ? c.attn : p.attn + L * p.s_attn, nq);
+    case MLCV_PROBE_H: return frag_rows(chain ? c.h : p.h + L * p.s_h, c.F1);
+    case MLCV_PROBE_VOUT:
+      MLCV_REQUIRE(layer == 0 && bytes == (size_t)T * c.A * 4, "probe output size");
+      MLCV_HIP(hipMemcpy(out, c.vout, bytes, hipMemcpyDeviceToHost));
+      return 0;
     case MLCV_PROBE_Q: {  // hi + lo of the roped, scaled q fragments -> [T][H*hd] f32
       MLCV_REQUIRE(bytes == (size_t)T * nq * 4, "probe output size");
-      MLCV_TRY(fetch(p.qf + L * p.s_qf, p.s_qf * 2, raw));
+      MLCV_TRY(fetch(chain ? c.qf : p.qf + L * p.s_qf, qf_halfs * 2, raw));
       const _Float16* f = reinterpret_cast<const _Float16*>(raw.data());
       float* o = static_cast<float*>(out);
       const int grp = c.H / c.KV, ntiles = c.attn_rpad / 16, nks = (c.HD + 31) / 32;
@@ -1536,6 +1563,7 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
       case MLCV_OP_GATEUP: MLCV_TRY(enqueue_gateup(c, layer, c.mod, st)); break;
       case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;
       case MLCV_OP_HEAD: MLCV_TRY(enqueue_head(c, c.mod, false, st)); break;
+      case MLCV_OP_ACTION_IN: MLCV_TRY(enqueue_action_in(c, c.mod, st)); break;
       default: MLCV_REQUIRE(false, "unknown op");
     }
   }
@@ -1622,6 +1650,22 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
     a.img_chunks = (Sp + 31) / 32;
   }
   return attn_launch(a, st);
+}
+
+int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const float* sin, int32_t P, int32_t H,
+                           int32_t KV, int32_t hd, const float* keys, const void* values, const float* mask, void* out,
+                           void* stream) {
+  MLCV_REQUIRE(q && cos && sin && keys && values && out && P > 0 && H > 0 && KV > 0 && hd > 0, "bad argument");
+  MLCV_REQUIRE(q_ld >= H * hd && q_ld % 8 == 0, "q row stride");
+  const int rows = P * (H / KV);
+  int nsplit = 1, kps = 32;
+  attn_plan(rows, P, 0, prefill_attn_target(rows), &nsplit, &kps);
+  std::lock_guard<std::mutex> lk(g_scratch.mu);
+  MLCV_TRY(scratch_reserve(attn_ws_floats(KV, rows, hd, nsplit) + 4, 1));
+  return attn_launch(prefill_attn_args(reinterpret_cast<const _Float16*>(q), q_ld, cos, sin, P, H, KV, hd, keys,
+                                       reinterpret_cast<const _Float16*>(values), mask,
+                                       reinterpret_cast<_Float16*>(out), nsplit, kps, g_scratch.ws),
+                     reinterpret_cast<hipStream_t>(stream));
 }
 
 int mlcv_q4_quantize(const void* w, uint32_t* q_weight, void* q_scale, int32_t N, int32_t K, void* stream) {

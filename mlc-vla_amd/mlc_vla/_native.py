@@ -20,7 +20,7 @@ MLCV_OPT_HOIST_MODULATION = 2
 MLCV_OPT_PERSIST = 3
 MLCV_OPT_PERSIST_SPIN = 4
 MLCV_OPT_MEET_POLLS = 5
-PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7}
+PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7, "vout": 8}
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -69,6 +69,8 @@ SIGNATURES = {
     "mlcv_chunk": (ctypes.c_int, [_vp] * 9),
     "mlcv_joint_attention": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp,
                                             _i32, _vp, _vp]),
+    "mlcv_prefill_attention": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                              _vp]),
     "mlcv_q4_quantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_q4_dequantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),

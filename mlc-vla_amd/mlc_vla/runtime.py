@@ -203,12 +203,23 @@ class VirtualMachine:
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_MEET_POLLS, int(polls))
 
     def check(self) -> None:
-        """Synchronize and raise if a persistent step of this VM ended early."""
+        """Synchronize and raise if a bounded device-side wait of this VM gave up."""
         if self._ctx:
             N.call("mlcv_sync", self._ctx, self._stream())
 
+    # the op codes of mlcv_bench_op (include/mlcvla.h)
+    STEP_OPS = {"time_mod": 0, "modulation": 1, "qkv": 2, "attention": 3, "o_proj": 4, "gate_up": 5, "down": 6,
+                "head": 7, "attention_only": 8, "action_in": 9}
+
+    def run_op(self, op: str, layer: int = 0, keys=None, values=None) -> None:
+        """Enqueue one operation of denoise_step_kv on this VM's current buffers (testing):
+        the launch chain's kernels with the arguments the step gives them."""
+        kp = _ptr(keys) if keys is not None else None
+        vp = _ptr(values) if values is not None else None
+        N.call("mlcv_bench_op", self._ctx, self.STEP_OPS[op], int(layer), 1, kp, vp, self._stream())
+
     def probe(self, what: str, layer: int, shape, dtype) -> np.ndarray:
-        """An intermediate of the last persistent step (testing): see mlcv_step_probe."""
+        """An intermediate of the last step (testing): see mlcv_step_probe."""
         out = np.empty(shape, dtype)
         N.call("mlcv_step_probe", self._ctx, N.PROBES[what], int(layer), out.ctypes.data_as(ctypes.c_void_p),
                out.nbytes, self._stream())

@@ -11,7 +11,9 @@ import pytest
 import torch
 
 from conftest import cosine, max_abs
+from gates import kernel_gate
 from mlc_vla import _native as N
+from mlc_vla.sample import make_prefix_mask_np, make_rope_np
 from oracle import pi0_oracle as O
 from oracle import q4_oracle as Q
 
@@ -244,3 +246,36 @@ def test_joint_attention_logits_are_fp32_accurate():
     k16 = kp32.astype(np.float16).astype(np.float64).transpose(1, 0, 2)
     ref16 = O.sdpa(q64, k16, v64, None, O.Prec("f64"))
     assert np.any(np.abs(ref16 - ref) > bound)
+
+
+@pytest.mark.parametrize("P,h,kv,hd,valid", [
+    (968, 8, 1, 256, 800),   # the pi0.5 prefix: 968 tokens, 800 valid
+    (968, 8, 1, 256, 968),   # no padding
+    (100, 2, 1, 64, 77),     # a small ragged case: partial row blocks and chunks
+])
+def test_prefill_attention_vs_fp64(P, h, kv, hd, valid):
+    """The prefill's attention instantiation (q roped and scaled in the loader, fp32 roped
+    keys from the cache, the prefix pad mask, no suffix block) through mlcv_prefill_attention,
+    which builds the arguments and split plan the prefill uses, against float64 SDPA
+    (gemma_dual.py:236-253,334-341; :97-122)."""
+    print(f"prefill attention P={P} H={h} KV={kv} hd={hd} valid={valid}", flush=True)
+    rng = np.random.default_rng(P + valid + hd)
+    nq, nkv = h * hd, kv * hd
+    qkv = rng.standard_normal((P, nq + 2 * nkv)).astype(np.float16)  # the q/k/v GEMM output row layout
+    keys = rng.standard_normal((kv, P, hd)).astype(np.float32) * 2.0
+    vals = rng.standard_normal((kv, P, hd)).astype(np.float16)
+    cos, sin = (a.reshape(P, hd // 2) for a in make_rope_np(P, hd, 10000.0))
+    mask = make_prefix_mask_np(P, num_valid=valid).reshape(P)
+    out = torch.empty((P, nq), dtype=torch.float16, device="cuda")
+    qd, cd, sd, kd, vd, md = _dev(qkv), _dev(cos), _dev(sin), _dev(keys), _dev(vals), _dev(mask)
+    N.call("mlcv_prefill_attention", _p(qd), nq + 2 * nkv, _p(cd), _p(sd), P, h, kv, hd, _p(kd), _p(vd), _p(md),
+           _p(out), _st())
+    got = _host(out)
+    F64 = O.Prec("f64")
+    q = O.apply_rope(qkv[:, :nq].astype(np.float64).reshape(P, h, hd), cos, sin, F64) * hd ** -0.5
+    ref = O.sdpa(q, keys.astype(np.float64).transpose(1, 0, 2), vals.astype(np.float64).transpose(1, 0, 2),
+                 mask.astype(np.float64), F64)
+    assert np.all(np.isfinite(got))
+    ok, st = kernel_gate(got, ref)
+    print("prefill attention", st, flush=True)
+    assert ok, st
