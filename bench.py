@@ -402,6 +402,13 @@ def main():
     a_stack = per_cold(lambda: [attn_one(L) for L in range(18)], 10)
     a_bytes, _ = op_bytes_flops(cfg, "attention")
 
+    # ---- measured HBM copy bandwidth (1 GiB device-to-device copies) -------------
+    csrc = torch.ones(1 << 28, device="cuda", dtype=torch.float32)
+    cdst = torch.empty_like(csrc)
+    copy_ms, _ = timed(lambda: cdst.copy_(csrc), 20, 3)
+    copy_gbs = 2 * csrc.numel() * 4 / (copy_ms * 1e-3) / 1e9
+    del csrc, cdst
+
     # ---- per-op launch times (the step's kernels one op at a time) ------------
     per_op = {}
     for name, cnt in OPS_PER_STEP.items():
@@ -448,6 +455,11 @@ def main():
                       "iters": len(cold_ts), "protocol": "512 MiB scratch written between steps, outside the timed region"},
         "attention_isolated": {
             "workload": "joint attention of one layer, P=968 prefix keys (fp32) + 50 suffix keys, 8 q heads, hd 256",
+            "instance": "the step's own attention (q as hi/lo fragments from the q/k/v epilogue, roped fp32 suffix "
+                        "keys, fp32 prefix K cache) + split combine, without prefetch workgroups; the prefix K is "
+                        "fp32 because prefill writes the roped cache in fp32 (a config naming fp16 K/V is timed "
+                        "on this fp32-K instance); its oracle check is the attention gate of "
+                        "tests/test_gpu_chain_ops.py at this shape",
             "single_cold_p50_us": round(_pct(a_single, 0.5), 2),
             "stacked18_cold_us_per_layer": round(_pct(a_stack, 0.5) / 18, 2),
             "bytes_per_launch": int(a_bytes),
@@ -461,13 +473,22 @@ def main():
                           "bytes_per_step": int(sbytes), "flops_per_step": int(step_flops(cfg))},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": per_op[dom]["bytes"], "avg_launch_us": per_op[dom]["us"]},
+                     "bytes_per_launch": per_op[dom]["bytes"], "avg_launch_us": per_op[dom]["us"],
+                     "measured_copy_GBps": round(copy_gbs, 1),
+                     "frac_of_measured_copy": round(per_op[dom]["GBps"] / copy_gbs, 4)},
+        "hbm_measured": {"copy_GBps": round(copy_gbs, 1), "spec_GBps": HBM_PEAK_GBS,
+                         "protocol": "torch copy_ of 1 GiB fp32 device to device, 20 timed after 3 warm-ups; "
+                                     "GB/s counts bytes read + written"},
         "per_op": per_op,
     }
-    pf_flops = 2 * 968 * 2048 * (2560 + 2048 + 2 * 16384) * 18 + 2 * 968 * 16384 * 2048 * 17 + \
-        4 * 8 * 968 * 968 * 256 * 17
+    # executed prefill flops: q/k/v of all 18 layers (their K/V are the output); attention,
+    # o_proj, gate_up and down of the first 17 (the last layer's feed nothing)
+    P0, W0, F0, NQ = 968, 2048, 16384, 2048
+    pf_flops = 2 * P0 * W0 * 2560 * 18 + (2 * P0 * NQ * W0 + 2 * P0 * W0 * 2 * F0 + 2 * P0 * F0 * W0 +
+                                          4 * 8 * P0 * P0 * 256) * 17
     out["prefill_mfma"] = {"tflops": round(pf_flops / (prefill_ms * 1e-3) / 1e12, 1),
-                           "frac": round(pf_flops / (prefill_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+                           "frac": round(pf_flops / (prefill_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                           "flops": int(pf_flops), "counted": "executed: q/k/v x 18 layers, the rest x 17"}
 
     if not args.no_q4:
         exq, qnp, qmap, quant = compile_model_quant(cfg, "rocm", None, "q4f16_1", cuda_graph=True)
