@@ -225,6 +225,16 @@ int mlcv_q4_dequantize(const uint32_t* q_weight, const void* q_scale, void* w, i
 int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight, const void* q_scale,
                 const void* bias, void* y, int32_t N, void* stream);
 
+/* mlcv_linear without any allocation (no counterpart in the reference): for callers that
+ * cannot allocate device memory -- code under hipGraph capture, tight serving loops, hosts
+ * that forbid it.  Same arguments, kernels and results as mlcv_linear, but asynchronous on
+ * `stream`; its split-K partials, arrival counters and zero page live in one static device
+ * array of about 8.3 MiB per GPU (held until the process ends), so it accepts at most 65536
+ * output tiles of 64 x 64 (returns -2 beyond).  Calls that overlap on one GPU race on that
+ * array: order them on one stream. */
+int mlcv_linear_noalloc(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight,
+                        const void* q_scale, const void* bias, void* y, int32_t N, void* stream);
+
 /* Prefill linear on the long-M tile GEMM (testing / benchmarking; no counterpart in the
  * reference): x [M,K] f16, w [N,K] f16 (MLCV_TILE_GEGLU: [2N,K], gate rows then up rows),
  * y [M,N] f16 with f32 accumulation:

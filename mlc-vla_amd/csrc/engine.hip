@@ -766,6 +766,48 @@ struct mlcv_ctx {
   Ctx c;
 };
 
+// ---- scratch of mlcv_linear_noalloc -------------------------------------------------------
+// One static device array per GPU, laid out as the zero page the skinny GEMM clamps its
+// padding loads to, the split-K arrival counters (one per output tile; the last arrival
+// resets its counter, so they are zero between calls) and the split-K partials.  8 MiB of
+// partials hold every split plan of sk_plan for 64-row tiles (ceil(256 / tiles) splits of
+// fewer than 256 tiles: under 512 x 4096 floats).
+namespace {
+constexpr size_t NA_ZERO_FLOATS = 64 * 64;
+constexpr size_t NA_COUNTERS = (size_t)1 << 16;
+constexpr size_t NA_PART_FLOATS = (size_t)1 << 21;
+constexpr size_t NA_SCRATCH_BYTES = (NA_ZERO_FLOATS + NA_COUNTERS + NA_PART_FLOATS) * 4;
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[NA_SCRATCH_BYTES];
+
+namespace {
+__global__ __launch_bounds__(256) void na_clear_kernel(unsigned* p, unsigned n) {
+  for (unsigned i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) p[i] = 0u;
+}
+
+// This device's address of `scratch` (host code only ever passes this address to kernels);
+// at the first call on a device its zero page and counters are cleared on `st`, ahead of
+// the call's own kernels.
+int noalloc_scratch(hipStream_t st, char** base) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  MLCV_HIP(hipGetDevice(&dev));
+  MLCV_REQUIRE(dev >= 0 && dev < 64, "device index");
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    MLCV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MLCV_REQUIRE(p != nullptr, "no device address for the linear scratch");
+    na_clear_kernel<<<64, 256, 0, st>>>(static_cast<unsigned*>(p), (unsigned)(NA_ZERO_FLOATS + NA_COUNTERS));
+    MLCV_HIP(hipGetLastError());
+    addr[dev] = p;
+  }
+  *base = static_cast<char*>(addr[dev]);
+  return 0;
+}
+}  // namespace
+
 extern "C" {
 
 const char* mlcv_last_error(void) { return get_error(); }
@@ -1896,6 +1938,48 @@ int mlcv_linear(const void* x, int32_t M, int32_t K, const void* w, const uint32
   MLCV_TRY(sk_launch(op, q_weight != nullptr, st));
   MLCV_HIP(hipStreamSynchronize(st));
   return 0;
+}
+
+int mlcv_linear_noalloc(const void* x, int32_t M, int32_t K, const void* w, const uint32_t* q_weight,
+                        const void* q_scale, const void* bias, void* y, int32_t N, void* stream) {
+  MLCV_REQUIRE(x && y && M > 0 && K > 0 && N > 0, "bad argument");
+  MLCV_REQUIRE((w != nullptr) != (q_weight != nullptr && q_scale != nullptr), "pass either w or q_weight+q_scale");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int ntiles = (N + 63) / 64, mb = (M + 63) / 64;
+  const SkPlan p = sk_plan(ntiles, K, mb, 0);
+  MLCV_REQUIRE((size_t)ntiles * mb <= NA_COUNTERS,
+               "mlcv_linear_noalloc: ceil(M/64) * ceil(N/64) = " + std::to_string((size_t)ntiles * mb) +
+                   " output tiles, above its maximum of " + std::to_string(NA_COUNTERS));
+  MLCV_REQUIRE(sk_ws_floats(ntiles, mb, p, 64) <= NA_PART_FLOATS,
+               "mlcv_linear_noalloc: the split-K partials exceed its scratch of " + std::to_string(NA_PART_FLOATS * 4) +
+                   " bytes");
+  char* base = nullptr;
+  MLCV_TRY(noalloc_scratch(st, &base));
+  SkSeg s{};
+  s.w = reinterpret_cast<const _Float16*>(w);
+  s.qw = q_weight;
+  s.qs = reinterpret_cast<const _Float16*>(q_scale);
+  s.bias = reinterpret_cast<const _Float16*>(bias);
+  s.out = y;
+  s.n = N;
+  s.ldo = N;
+  s.tile0 = 0;
+  SkOp op{};
+  op.x = reinterpret_cast<const _Float16*>(x);
+  op.ldx = K;
+  op.M = M;
+  op.K = K;
+  op.epi = EPI_STORE;
+  op.nseg = 1;  // one segment: passed inline, no segment table
+  op.inl[0] = s;
+  op.ntiles = ntiles;
+  op.tr = 64;
+  op.splitk = p.splitk;
+  op.kper = p.kper;
+  op.zero = reinterpret_cast<float*>(base);
+  op.counters = reinterpret_cast<unsigned*>(base + NA_ZERO_FLOATS * 4);
+  op.ws = reinterpret_cast<float*>(base + (NA_ZERO_FLOATS + NA_COUNTERS) * 4);
+  return sk_launch(op, q_weight != nullptr, st);
 }
 
 }  // extern "C"

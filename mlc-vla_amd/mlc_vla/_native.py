@@ -74,6 +74,7 @@ SIGNATURES = {
     "mlcv_q4_quantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_q4_dequantize": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "mlcv_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "mlcv_linear_noalloc": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "mlcv_tile_linear": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "mlcv_bench_op": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
 }
