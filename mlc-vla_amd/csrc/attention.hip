@@ -4,6 +4,14 @@
 #include <algorithm>
 #include <type_traits>
 
+#ifdef MLCV_ATTN_TRACE
+// timeline of the last standalone attention launch (trace build): [workgroup][stage]
+__device__ unsigned long long attn_trace[1024 * 8];
+#define ATTN_STAMP(k)                                                                                     \
+  do {                                                                                                    \
+    if (tid == 0) attn_trace[(blockIdx.x + gridDim.x * blockIdx.y) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#endif
 #include "attn_impl.h"
 
 namespace mlcv {
@@ -384,3 +392,11 @@ int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStre
 }
 
 }  // namespace mlcv
+
+#ifdef MLCV_ATTN_TRACE
+extern "C" void* mlcv_attn_trace_ptr() {
+  void* p = nullptr;
+  (void)hipGetSymbolAddress(&p, HIP_SYMBOL(attn_trace));
+  return p;
+}
+#endif

@@ -31,6 +31,13 @@
 
 #include "kernels.h"
 
+// cache policy of the q fragments written by the previous launch (the persistent step, which
+// writes them in the same launch, always reads them at device scope)
+#ifndef MLCV_ATTN_Q_AUX
+#define MLCV_ATTN_Q_AUX 16
+#endif
+constexpr int ATTN_Q_AUX = MLCV_ATTN_Q_AUX;
+
 // timeline stamps of the trace build of the persistent step (empty otherwise)
 #ifndef ATTN_STAMP
 #define ATTN_STAMP(k) \
@@ -99,8 +106,9 @@ __device__ __forceinline__ void cvt8(const h8 x, float* o) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = h2f(x[e]);
 }
+template <int AUX>
 __device__ __forceinline__ void ld8f(__amdgpu_buffer_rsrc_t r, int byte_off, float* o) {
-  const f4 a = load_dev<f4, KV_AUX>(r, byte_off), b = load_dev<f4, KV_AUX>(r, byte_off + 16);
+  const f4 a = load_dev<f4, AUX>(r, byte_off), b = load_dev<f4, AUX>(r, byte_off + 16);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     o[e] = a[e];
@@ -123,8 +131,8 @@ __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a,
     kitem<HD>(i, tid, j, dp);
     const int off = min(c0 + j, kend - 1) * HD + dp;
     if constexpr (KF32) {
-      ld8f(rk, off * 4, r.k[i]);
-      ld8f(rk, (off + HALF) * 4, r.k[i] + 8);
+      ld8f<KV_AUX>(rk, off * 4, r.k[i]);
+      ld8f<KV_AUX>(rk, (off + HALF) * 4, r.k[i] + 8);
     } else {
       cvt8(load_dev<h8, KV_AUX>(rk, off * 2), r.k[i]);
       cvt8(load_dev<h8, KV_AUX>(rk, (off + HALF) * 2), r.k[i] + 8);
@@ -191,7 +199,8 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
 
 // suffix keys handed over roped in fp32 ([Ts][ks_ld], the qkv epilogue's output) and the
 // suffix v: the prefix loader's chunk layout with the suffix row strides
-template <int HD>
+// AUX: the cache policy (device scope when the suffix k/v were written in the same launch)
+template <int HD, int AUX>
 __device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
   // the previous kernel's output: device-scope loads
@@ -202,15 +211,15 @@ __device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& 
     int j, dp;
     kitem<HD>(i, tid, j, dp);
     const int off = min(c0 + j, kend - 1) * a.ks_ld + kvh * HD + dp;
-    ld8f(rk, off * 4, r.k[i]);
-    ld8f(rk, (off + HALF) * 4, r.k[i] + 8);
+    ld8f<AUX>(rk, off * 4, r.k[i]);
+    ld8f<AUX>(rk, (off + HALF) * 4, r.k[i] + 8);
   }
 #pragma unroll
   for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
     int jp, d0;
     vitem<HD>(i, tid, jp, d0);
-    r.v[i][0] = load_dev<h8>(rv, (min(c0 + 2 * jp, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
-    r.v[i][1] = load_dev<h8>(rv, (min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
+    r.v[i][0] = load_dev<h8, AUX>(rv, (min(c0 + 2 * jp, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
+    r.v[i][1] = load_dev<h8, AUX>(rv, (min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
   }
   r.msk = 0.f;
   r.mok = c0 + (tid & (KCH - 1)) < kend;
@@ -578,8 +587,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const int qb = (((tile * NKS + ks) * 2) * 512 + lane * 8) * 2;
-        qh[ks] = load_dev<h8>(rq, qb);
-        ql[ks] = load_dev<h8>(rq, qb + 1024);
+        qh[ks] = load_dev<h8, COH ? 16 : ATTN_Q_AUX>(rq, qb);
+        ql[ks] = load_dev<h8, COH ? 16 : ATTN_Q_AUX>(rq, qb + 1024);
       }
     } else {
       QRaw<HD> qa, qb;
@@ -616,7 +625,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
   if (QF && suffix) {
     ChunkRegs<HD> R0, R1;
     pipeline(
-        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_suffix32<HD>(R, a, kvh, c * KCH, kend, tid); },
+        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_suffix32<HD, COH ? 16 : ATTN_Q_AUX>(R, a, kvh, c * KCH, kend, tid); },
         [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
   } else if (suffix) {
     SufRegs<HD> R0, R1;
