@@ -82,14 +82,14 @@ __global__ __launch_bounds__(256) void attn_img_prep_kernel(const void* __restri
     *reinterpret_cast<h8*>(&sv[j * HD + d8]) = v;
   }
   __syncthreads();
-  for (int i = tid; i < HD * (VLD / 8); i += 256) {
-    const int d = i / (VLD / 8), j8 = (i % (VLD / 8)) * 8;
-    h8 o = zero8;
-    if (j8 < KCH) {
+  for (int i = tid; i < HD * (VLD / 4); i += 256) {  // 8-byte pieces (V^T rows are 8-byte aligned)
+    const int d = i / (VLD / 4), j4 = (i % (VLD / 4)) * 4;
+    h4 o = (h4){0, 0, 0, 0};
+    if (j4 < KCH) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = sv[(j8 + e) * HD + d];
+      for (int e = 0; e < 4; ++e) o[e] = sv[(j4 + e) * HD + d];
     }
-    *reinterpret_cast<h8*>(&im->vt[d * VLD + j8]) = o;
+    *reinterpret_cast<h4*>(&im->vt[d * VLD + j4]) = o;
   }
   if (tid < KCH) im->msk[tid] = c0 + tid < Sp ? (mask ? mask[c0 + tid] : 0.f) : -INFINITY;
 }

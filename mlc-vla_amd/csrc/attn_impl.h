@@ -49,7 +49,8 @@ namespace mlcv {
 namespace {
 constexpr int KCH = 32;        // keys per chunk
 constexpr int ROWS = 64;       // query rows per workgroup (4 waves x 16)
-constexpr int VLD = KCH + 8;   // halfs per V^T row
+constexpr int VLD = KCH + 8;  // halfs per V^T row (a multiple of 4, at least KCH)
+static_assert(VLD % 4 == 0 && VLD >= KCH, "V^T rows hold a chunk's keys in 8-byte pieces");
 constexpr int NT = 256;        // threads per workgroup (4 waves, one 16-row query tile each)
 static_assert(ROWS == ATTN_ROWS && KCH == ATTN_KCH, "the planner's rows and chunk (plan.h)");
 

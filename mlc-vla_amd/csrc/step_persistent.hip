@@ -86,9 +86,19 @@ __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
   return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Every wave's stores are complete, then the workgroup meets: s_barrier (__syncthreads) alone
+// does not wait for outstanding global stores on this part, so each wave first waits for its
+// own.  Every store another workgroup reads is a device-scope (write-through) store, visible
+// device-wide once complete, so the word that announces them needs no L2 write-back (a release
+// fence there, buffer_wbl2, cost about 300 us per step) and is stored relaxed.
+__device__ __forceinline__ void pk_stores_done() {
+  wait_all_memory();
+  __syncthreads();
+}
+
 // every store of this workgroup's tasks is complete; then the progress word
 __device__ __forceinline__ void pk_publish(CPk& p, unsigned value) {
-  __syncthreads();  // waits for every wave's outstanding stores, then meets
+  pk_stores_done();
   if (pk_tid() == 0) __hip_atomic_store(p.prog + pk_bid(), value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -323,7 +333,7 @@ __device__ __forceinline__ bool pk_splitk(f4& own, float* ws, unsigned* cnt, int
   if (S == 1) return true;
   const __amdgpu_buffer_rsrc_t rw = dev_rsrc(ws, 0x7FFFFF00);
   store_dev<f4>(rw, ((((tile * S + s) * 4 + w) * 64) + lane) * 16, own);
-  __syncthreads();  // every wave's partial store is complete
+  pk_stores_done();  // every wave's partial store is complete
   if (pk_tid() == 0) {
     const unsigned old = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sh.is_last = (int)((old & (unsigned)(S - 1)) == (unsigned)(S - 1));
@@ -627,7 +637,7 @@ __device__ __forceinline__ bool phase_attn(CPk& p, int L, unsigned target, unsig
   for (int t = pk_bid(); t < n; t += p.G) {
     const int rbi = t % rb, rest = t / rb, split = rest % p.nsplit, kvh = rest / p.nsplit;
     attn_block<HD, true, false, false, true, true>(a, rbi, split, kvh, smem, pk_tid());
-    __syncthreads();  // the partial stores are complete; the chunk buffers are free again
+    pk_stores_done();  // the partial stores are complete; the chunk buffers are free again
     if (p.merge_comb && p.nsplit > 1) {
       unsigned* ctr = p.cntm + ((size_t)L * p.KV + kvh) * rb + rbi;
       if (pk_tid() == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
