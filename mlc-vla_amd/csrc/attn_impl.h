@@ -253,10 +253,9 @@ __device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>
   r.mok = in.mok;
 }
 
-// Workgroup barrier for LDS hand-off only: waits for this wave's LDS accesses, not for
-// its outstanding global loads (__syncthreads also drains vmcnt, which would expose the
-// latency of every prefetch issued before it).  The empty asm statements keep the
-// compiler from moving memory accesses across the barrier.
+// Workgroup barrier for LDS hand-off: waits for this wave's LDS accesses (lgkmcnt), not for
+// its outstanding global loads, whose latency the prefetches hide.  The explicit wait and the
+// empty asm statements keep the compiler from moving memory accesses across the barrier.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt not waited
