@@ -18,14 +18,14 @@ namespace mlcv {
 
 namespace {
 
-template <int HD, bool KF32, bool ROPE, bool IMG, bool QF>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+template <int HD, bool KF32, bool ROPE, bool IMG, bool QF, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds_raw[2 * attn_buf_bytes<HD, IMG>()];
   if (blockIdx.y >= a.nsplit) {  // prefetch workgroups (grid rows past the key splits)
     if (blockIdx.z == 0) prefetch_run(a.pf, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * a.nsplit);
     return;
   }
-  attn_block<HD, KF32, ROPE, IMG, QF, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds_raw, threadIdx.x);
+  attn_block<HD, KF32, ROPE, IMG, QF, false, NW>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds_raw, threadIdx.x);
 }
 
 // chunk images of the prefix K/V of `layers` layers: grid (chunks, KV, layers)
@@ -281,21 +281,23 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   const int pf_rows = a.pf.nreg > 0 && a.pf.nblocks > 0 ? (a.pf.nblocks + rb - 1) / rb : 0;
   ka.pf.nblocks = pf_rows * rb;
   dim3 grid(rb, a.nsplit + pf_rows, a.KV);
-#define MLCV_ATTN_CASE(HDV)                                                                 \
-  case HDV:                                                                                 \
-    if (a.qf) {                                                                             \
-      if (a.kimg) attn_kernel<HDV, true, false, true, true><<<grid, 256, 0, st>>>(ka);       \
-      else attn_kernel<HDV, true, false, false, true><<<grid, 256, 0, st>>>(ka);             \
-    } else if (a.kimg) {                                                                    \
-      if (a.cos) attn_kernel<HDV, true, true, true, false><<<grid, 256, 0, st>>>(ka);        \
-      else attn_kernel<HDV, true, false, true, false><<<grid, 256, 0, st>>>(ka);             \
-    } else if (a.kp_f32) {                                                                  \
-      if (a.cos) attn_kernel<HDV, true, true, false, false><<<grid, 256, 0, st>>>(ka);       \
-      else attn_kernel<HDV, true, false, false, false><<<grid, 256, 0, st>>>(ka);            \
-    } else {                                                                                \
-      if (a.cos) attn_kernel<HDV, false, true, false, false><<<grid, 256, 0, st>>>(ka);      \
-      else attn_kernel<HDV, false, false, false, false><<<grid, 256, 0, st>>>(ka);           \
-    }                                                                                       \
+// the step's form (q fragments, converted chunks) runs on 8 waves (attn_block): 868 vs 871 us
+// per step; the others on 4 (the prefill's form spills at 8 waves: +20 us per prefill)
+#define MLCV_ATTN_CASE(HDV)                                                                        \
+  case HDV:                                                                                        \
+    if (a.qf) {                                                                                    \
+      if (a.kimg) attn_kernel<HDV, true, false, true, true, 4><<<grid, 256, 0, st>>>(ka);           \
+      else attn_kernel<HDV, true, false, false, true, 8><<<grid, 512, 0, st>>>(ka);                 \
+    } else if (a.kimg) {                                                                           \
+      if (a.cos) attn_kernel<HDV, true, true, true, false, 4><<<grid, 256, 0, st>>>(ka);            \
+      else attn_kernel<HDV, true, false, true, false, 4><<<grid, 256, 0, st>>>(ka);                 \
+    } else if (a.kp_f32) {                                                                         \
+      if (a.cos) attn_kernel<HDV, true, true, false, false, 4><<<grid, 256, 0, st>>>(ka);           \
+      else attn_kernel<HDV, true, false, false, false, 4><<<grid, 256, 0, st>>>(ka);                \
+    } else {                                                                                       \
+      if (a.cos) attn_kernel<HDV, false, true, false, false, 4><<<grid, 256, 0, st>>>(ka);          \
+      else attn_kernel<HDV, false, false, false, false, 4><<<grid, 256, 0, st>>>(ka);               \
+    }                                                                                              \
     break;
   switch (a.hd) {
     MLCV_ATTN_CASE(16)

@@ -76,29 +76,29 @@ constexpr int img_bytes() {
 //   K item (key j, dims dp..dp+7 and dp+HD/2..+7) as fp32 (the RoPE pair of the suffix
 //   loader is one item); V item (keys 2jp, 2jp+1; dims d0..d0+7).  Items past the
 //   chunk's item count are repeats of earlier ones (identical LDS stores).
-template <int HD>
+template <int HD, int NTH = NT>
 struct ChunkRegs {
   static constexpr int HALF = HD / 2;
   static constexpr int KITEMS = KCH * (HALF / 8);
   static constexpr int VITEMS = (KCH / 2) * (HD / 8);
-  static constexpr int NK = (KITEMS + NT - 1) / NT;
-  static constexpr int NV = (VITEMS + NT - 1) / NT;
+  static constexpr int NK = (KITEMS + NTH - 1) / NTH;
+  static constexpr int NV = (VITEMS + NTH - 1) / NTH;
   float k[NK][16];
   h8 v[NV][2];
   float msk;  // the mask value as loaded; keys past the range get -inf when stored (mok)
   bool mok;
 };
 
-template <int HD>
+template <int HD, int NTH>
 __device__ __forceinline__ void kitem(int i, int tid, int& j, int& dp) {
   constexpr int HALF = HD / 2;
-  const int it = (tid + NT * i) % ChunkRegs<HD>::KITEMS;
+  const int it = (tid + NTH * i) % ChunkRegs<HD, NTH>::KITEMS;
   j = it / (HALF / 8);
   dp = (it % (HALF / 8)) * 8;
 }
-template <int HD>
+template <int HD, int NTH>
 __device__ __forceinline__ void vitem(int i, int tid, int& jp, int& d0) {
-  const int it = (tid + NT * i) % ChunkRegs<HD>::VITEMS;
+  const int it = (tid + NTH * i) % ChunkRegs<HD, NTH>::VITEMS;
   jp = it % (KCH / 2);
   d0 = (it / (KCH / 2)) * 8;
 }
@@ -118,8 +118,8 @@ __device__ __forceinline__ void ld8f(__amdgpu_buffer_rsrc_t r, int byte_off, flo
 }
 
 // prefix keys [c0, c0+32) of this split (cached, roped; fp32 or fp16), clamped below kend
-template <int HD, bool KF32>
-__device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
+template <int HD, bool KF32, int NTH>
+__device__ __forceinline__ void load_prefix(ChunkRegs<HD, NTH>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
   // this kv head's keys and values (element offsets below are within one head: < 2^31 bytes)
   const size_t head = (size_t)kvh * a.Sp * HD, hbytes = (size_t)a.Sp * HD;
@@ -127,9 +127,9 @@ __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a,
                                              (uint32_t)(hbytes * (KF32 ? 4 : 2)));
   const __amdgpu_buffer_rsrc_t rv = dev_rsrc(a.vp + head, (uint32_t)(hbytes * 2));
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NK; ++i) {
     int j, dp;
-    kitem<HD>(i, tid, j, dp);
+    kitem<HD, NTH>(i, tid, j, dp);
     const int off = min(c0 + j, kend - 1) * HD + dp;
     if constexpr (KF32) {
       ld8f<KV_AUX>(rk, off * 4, r.k[i]);
@@ -140,9 +140,9 @@ __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a,
     }
   }
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NV; ++i) {
     int jp, d0;
-    vitem<HD>(i, tid, jp, d0);
+    vitem<HD, NTH>(i, tid, jp, d0);
     r.v[i][0] = load_dev<h8, KV_AUX>(rv, (min(c0 + 2 * jp, kend - 1) * HD + d0) * 2);
     r.v[i][1] = load_dev<h8, KV_AUX>(rv, (min(c0 + 2 * jp + 1, kend - 1) * HD + d0) * 2);
   }
@@ -156,9 +156,9 @@ __device__ __forceinline__ void load_prefix(ChunkRegs<HD>& r, const AttnArgs& a,
 
 // Suffix keys [c0, c0+32): the raw fp16 k of the suffix rows and their rope tables stay
 // in registers as loaded (no arithmetic on in-flight loads), roped at store time.
-template <int HD>
+template <int HD, int NTH = NT>
 struct SufRegs {
-  static constexpr int NK = ChunkRegs<HD>::NK, NV = ChunkRegs<HD>::NV;
+  static constexpr int NK = ChunkRegs<HD, NTH>::NK, NV = ChunkRegs<HD, NTH>::NV;
   h8 x1[NK], x2[NK];
   f4 c[NK][2], s[NK][2];
   h8 v[NV][2];
@@ -166,13 +166,13 @@ struct SufRegs {
   bool mok;
 };
 
-template <int HD, bool ROPE>
-__device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
+template <int HD, bool ROPE, int NTH>
+__device__ __forceinline__ void load_suffix(SufRegs<HD, NTH>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
 #pragma unroll
-  for (int i = 0; i < SufRegs<HD>::NK; ++i) {
+  for (int i = 0; i < SufRegs<HD, NTH>::NK; ++i) {
     int j, dp;
-    kitem<HD>(i, tid, j, dp);
+    kitem<HD, NTH>(i, tid, j, dp);
     const int ts = min(c0 + j, kend - 1);
     const _Float16* kr = a.ks + (size_t)ts * a.ks_ld + (size_t)kvh * HD + dp;
     r.x1[i] = load_global(reinterpret_cast<const h8*>(kr));
@@ -187,9 +187,9 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
     }
   }
 #pragma unroll
-  for (int i = 0; i < SufRegs<HD>::NV; ++i) {
+  for (int i = 0; i < SufRegs<HD, NTH>::NV; ++i) {
     int jp, d0;
-    vitem<HD>(i, tid, jp, d0);
+    vitem<HD, NTH>(i, tid, jp, d0);
     const _Float16* vb = a.vs + (size_t)kvh * HD + d0;
     r.v[i][0] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp, kend - 1) * a.vs_ld));
     r.v[i][1] = load_global(reinterpret_cast<const h8*>(vb + (size_t)min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld));
@@ -201,24 +201,24 @@ __device__ __forceinline__ void load_suffix(SufRegs<HD>& r, const AttnArgs& a, i
 // suffix keys handed over roped in fp32 ([Ts][ks_ld], the qkv epilogue's output) and the
 // suffix v: the prefix loader's chunk layout with the suffix row strides
 // AUX: the cache policy (device scope when the suffix k/v were written in the same launch)
-template <int HD, int AUX>
-__device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
+template <int HD, int AUX, int NTH>
+__device__ __forceinline__ void load_suffix32(ChunkRegs<HD, NTH>& r, const AttnArgs& a, int kvh, int c0, int kend, int tid) {
   constexpr int HALF = HD / 2;
   // the previous kernel's output: device-scope loads
   const __amdgpu_buffer_rsrc_t rk = dev_rsrc(a.ks32, (uint32_t)kend * a.ks_ld * 4);
   const __amdgpu_buffer_rsrc_t rv = dev_rsrc(a.vs, (uint32_t)kend * a.vs_ld * 2);
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NK; ++i) {
     int j, dp;
-    kitem<HD>(i, tid, j, dp);
+    kitem<HD, NTH>(i, tid, j, dp);
     const int off = min(c0 + j, kend - 1) * a.ks_ld + kvh * HD + dp;
     ld8f<AUX>(rk, off * 4, r.k[i]);
     ld8f<AUX>(rk, (off + HALF) * 4, r.k[i] + 8);
   }
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NV; ++i) {
     int jp, d0;
-    vitem<HD>(i, tid, jp, d0);
+    vitem<HD, NTH>(i, tid, jp, d0);
     r.v[i][0] = load_dev<h8, AUX>(rv, (min(c0 + 2 * jp, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
     r.v[i][1] = load_dev<h8, AUX>(rv, (min(c0 + 2 * jp + 1, kend - 1) * a.vs_ld + kvh * HD + d0) * 2);
   }
@@ -227,10 +227,10 @@ __device__ __forceinline__ void load_suffix32(ChunkRegs<HD>& r, const AttnArgs& 
 }
 
 // rope the suffix keys (unless handed over roped) into the fp32 chunk layout
-template <int HD, bool ROPE>
-__device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>& r, bool roped) {
+template <int HD, bool ROPE, int NTH>
+__device__ __forceinline__ void rope_suffix(const SufRegs<HD, NTH>& in, ChunkRegs<HD, NTH>& r, bool roped) {
 #pragma unroll
-  for (int i = 0; i < SufRegs<HD>::NK; ++i) {
+  for (int i = 0; i < SufRegs<HD, NTH>::NK; ++i) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x1 = h2f(in.x1[i][e]), x2 = h2f(in.x2[i][e]);
@@ -245,7 +245,7 @@ __device__ __forceinline__ void rope_suffix(const SufRegs<HD>& in, ChunkRegs<HD>
     }
   }
 #pragma unroll
-  for (int i = 0; i < SufRegs<HD>::NV; ++i) {
+  for (int i = 0; i < SufRegs<HD, NTH>::NV; ++i) {
     r.v[i][0] = in.v[i][0];
     r.v[i][1] = in.v[i][1];
   }
@@ -263,13 +263,13 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int HD>
-__device__ __forceinline__ void store_chunk(const ChunkRegs<HD>& r, AttnSmem<HD>& sm, int tid) {
+template <int HD, int NTH>
+__device__ __forceinline__ void store_chunk(const ChunkRegs<HD, NTH>& r, AttnSmem<HD>& sm, int tid) {
   constexpr int KLD = AttnSmem<HD>::KLD, HALF = HD / 2;
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NK; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NK; ++i) {
     int j, dp;
-    kitem<HD>(i, tid, j, dp);
+    kitem<HD, NTH>(i, tid, j, dp);
 #pragma unroll
     for (int hpart = 0; hpart < 2; ++hpart) {
       h8 hi8, lo8;
@@ -285,9 +285,9 @@ __device__ __forceinline__ void store_chunk(const ChunkRegs<HD>& r, AttnSmem<HD>
     }
   }
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<HD>::NV; ++i) {
+  for (int i = 0; i < ChunkRegs<HD, NTH>::NV; ++i) {
     int jp, d0;
-    vitem<HD>(i, tid, jp, d0);
+    vitem<HD, NTH>(i, tid, jp, d0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const h2 pair = {r.v[i][0][e], r.v[i][1][e]};
@@ -453,9 +453,15 @@ constexpr int attn_buf_bytes() {
 // the memory side), for a consumer in the same launch on another XCD.
 // tid: this thread's index in the workgroup (threadIdx.x; the persistent step passes a copy
 // the compiler cannot hoist)
-template <int HD, bool KF32, bool ROPE, bool IMG, bool QF, bool COH>
+// NW: waves per workgroup.  4: wave w computes query tile w over every chunk.  8: the two waves
+// of query tile w & 3 take alternate chunks (wave w >> 2 == chunk parity), so both LDS buffers
+// are computed at once and each SIMD runs two waves, whose LDS reads and softmax hide each
+// other's latency; their online-softmax states merge through LDS at the end.
+template <int HD, bool KF32, bool ROPE, bool IMG, bool QF, bool COH, int NW = 4>
 __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, const int split, const int kvh,
                                            char* lds_raw, const int tid) {
+  static_assert(NW == 4 || (NW == 8 && !IMG), "8 waves read converted chunks, not images");
+  constexpr int NTH = 64 * NW;  // threads of the workgroup
   constexpr int BUFB = attn_buf_bytes<HD, IMG>();
   constexpr int IMGB = img_bytes<HD>();
   constexpr int KLD = AttnSmem<HD>::KLD;
@@ -463,9 +469,11 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
   constexpr int NDT = HD / 16;         // output d tiles
 
   const int lane = tid & 63, w = tid >> 6;
+  const int rt = w & 3;   // this wave's 16-row query tile
+  const int cp = w >> 2;  // 8 waves: the parity of the chunks this wave computes
   const int g = lane >> 4, r16 = lane & 15;
   const int grp = a.H / a.KV;
-  const int row = bx * ROWS + 16 * w + r16;   // this lane's query row (B-operand column)
+  const int row = bx * ROWS + 16 * rt + r16;  // this lane's query row (B-operand column)
   const bool row_ok = row < a.rows;
   const int rowc = min(row, a.rows - 1);
   const int hl = rowc / a.Tq, t = rowc % a.Tq;
@@ -583,7 +591,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
     if constexpr (QF) {
       // q fragments from the q/k/v epilogue of the previous kernel: device-scope loads
       const __amdgpu_buffer_rsrc_t rq = dev_rsrc(a.qf, (uint32_t)a.KV * a.rpad * NKS * 128);
-      const int tile = kvh * (a.rpad / 16) + (bx * ROWS + 16 * w) / 16;
+      const int tile = kvh * (a.rpad / 16) + (bx * ROWS + 16 * rt) / 16;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const int qb = (((tile * NKS + ks) * 2) * 512 + lane * 8) * 2;
@@ -602,6 +610,21 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
     if (nch > 1) store(R1, 1);
     lds_barrier();
     ATTN_STAMP(1);
+    if constexpr (NW == 8) {
+      // chunks c and c + 1 at once, one per wave group; the next pair's loads in flight
+      for (int c = 0; c < nch; c += 2) {
+        if (c + 2 < nch) load(c + 2, R0);
+        if (c + 3 < nch) load(c + 3, R1);
+        if (c + cp < nch) chunk_math(buf(cp));
+        lds_barrier();
+        if (c + 2 < nch) {
+          store(R0, 0);
+          if (c + 3 < nch) store(R1, 1);
+          lds_barrier();
+        }
+      }
+      return;
+    }
     if (nch > 2) load(2, R0);
     if (nch > 3) load(3, R1);
     for (int c = 0; c < nch; c += 2) {
@@ -623,18 +646,21 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
   };
   ATTN_STAMP(0);
   if (QF && suffix) {
-    ChunkRegs<HD> R0, R1;
+    ChunkRegs<HD, NTH> R0, R1;
     pipeline(
-        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_suffix32<HD, COH ? 16 : ATTN_Q_AUX>(R, a, kvh, c * KCH, kend, tid); },
-        [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
+        R0, R1,
+        [&](int c, ChunkRegs<HD, NTH>& R) {
+          load_suffix32<HD, COH ? 16 : ATTN_Q_AUX, NTH>(R, a, kvh, c * KCH, kend, tid);
+        },
+        [&](const ChunkRegs<HD, NTH>& R, int b) { store_chunk<HD, NTH>(R, wbuf(b), tid); });
   } else if (suffix) {
-    SufRegs<HD> R0, R1;
+    SufRegs<HD, NTH> R0, R1;
     pipeline(
-        R0, R1, [&](int c, SufRegs<HD>& R) { load_suffix<HD, ROPE>(R, a, kvh, c * KCH, kend, tid); },
-        [&](const SufRegs<HD>& R, int b) {
-          ChunkRegs<HD> k32;
-          rope_suffix<HD, ROPE>(R, k32, a.ks_roped != 0);
-          store_chunk<HD>(k32, wbuf(b), tid);
+        R0, R1, [&](int c, SufRegs<HD, NTH>& R) { load_suffix<HD, ROPE, NTH>(R, a, kvh, c * KCH, kend, tid); },
+        [&](const SufRegs<HD, NTH>& R, int b) {
+          ChunkRegs<HD, NTH> k32;
+          rope_suffix<HD, ROPE, NTH>(R, k32, a.ks_roped != 0);
+          store_chunk<HD, NTH>(k32, wbuf(b), tid);
         });
   } else if constexpr (IMG) {
     constexpr int NI = IMGB / (NT * 16);
@@ -655,10 +681,36 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
           for (int i = 0; i < NI; ++i) *reinterpret_cast<u4*>(lds_raw + b * BUFB + (i * NT + tid) * 16) = R.v[i];
         });
   } else {
-    ChunkRegs<HD> R0, R1;
+    ChunkRegs<HD, NTH> R0, R1;
     pipeline(
-        R0, R1, [&](int c, ChunkRegs<HD>& R) { load_prefix<HD, KF32>(R, a, kvh, kbeg + c * KCH, kend, tid); },
-        [&](const ChunkRegs<HD>& R, int b) { store_chunk<HD>(R, wbuf(b), tid); });
+        R0, R1,
+        [&](int c, ChunkRegs<HD, NTH>& R) { load_prefix<HD, KF32, NTH>(R, a, kvh, kbeg + c * KCH, kend, tid); },
+        [&](const ChunkRegs<HD, NTH>& R, int b) { store_chunk<HD, NTH>(R, wbuf(b), tid); });
+  }
+
+  if constexpr (NW == 8) {
+    // the odd-chunk wave of each query tile hands (O, m, l) to the even-chunk wave through LDS
+    // (the chunk buffers are free after the loop's last barrier); that wave merges the two
+    // online-softmax states and writes the tile
+    f4* mo = reinterpret_cast<f4*>(lds_raw) + (size_t)rt * (NDT + 1) * 64;
+    static_assert(4 * (NDT + 1) * 64 * 16 <= 2 * BUFB, "merge area");
+    if (cp == 1) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) mo[dt * 64 + lane] = oacc[dt];
+      mo[NDT * 64 + lane] = (f4){m_run, l_run, 0.f, 0.f};
+    }
+    lds_barrier();
+    if (cp == 0) {
+      const f4 ml = mo[NDT * 64 + lane];
+      const float m_new = fmaxf(m_run, ml[0]);
+      const float a0 = exp_hw(m_run - m_new), a1 = exp_hw(ml[0] - m_new);
+      l_run = l_run * a0 + ml[1] * a1;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] = oacc[dt] * a0 + mo[dt * 64 + lane] * a1;
+      m_run = m_new;
+    }
+    lds_barrier();  // every merge read is done before the partial rows are staged over it
+    if (cp == 1) return;
   }
 
   ATTN_STAMP(2);
@@ -668,7 +720,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
     // through its own LDS rows (free after the last chunk's barrier) so that every store
     // writes two whole rows of the partial (1 KB contiguous) instead of 16 pieces of 32 B.
     constexpr int PLD = HD + 8;  // halfs per LDS row
-    _Float16* pl = reinterpret_cast<_Float16*>(lds_raw) + (size_t)w * 16 * PLD;
+    _Float16* pl = reinterpret_cast<_Float16*>(lds_raw) + (size_t)rt * 16 * PLD;
     const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -681,13 +733,13 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
     __builtin_amdgcn_wave_barrier();
     constexpr int LPR = HD / 8;           // 8-half pieces per row
     constexpr int ITEMS = 16 * LPR;       // pieces of the wave's 16 rows, 64 per store
-    const size_t pr0 = ((size_t)kvh * a.nsplit + split) * a.rpad + bx * ROWS + 16 * w;
+    const size_t pr0 = ((size_t)kvh * a.nsplit + split) * a.rpad + bx * ROWS + 16 * rt;
     _Float16* po = reinterpret_cast<_Float16*>(a.part_o);
     const __amdgpu_buffer_rsrc_t rpo = dev_rsrc(po, 0x7FFFFFF0), rpml = dev_rsrc(a.part_ml, 0x7FFFFFF0);
 #pragma unroll
     for (int it = 0; it < (ITEMS + 63) / 64; ++it) {
       const int idx = 64 * it + lane, rr = idx / LPR, cc = (idx % LPR) * 8;
-      if (idx < ITEMS && bx * ROWS + 16 * w + rr < a.rows) {
+      if (idx < ITEMS && bx * ROWS + 16 * rt + rr < a.rows) {
         const h8 v = *reinterpret_cast<const h8*>(pl + rr * PLD + cc);
         if constexpr (COH) store_dev<h8>(rpo, (int)(((pr0 + rr) * HD + cc) * 2), v);
         else *reinterpret_cast<h8*>(po + (pr0 + rr) * HD + cc) = v;
