@@ -471,6 +471,14 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   else if (p.bn == 256) {
     if (a.epi == TG_RESIDUAL) big_gemm_kernel<256, 32, 4, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
     else big_gemm_kernel<256, 32, 4, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+  } else if (p.bn == 64) {
+    if (p.splitk > 1) {
+      if (a.epi == TG_RESIDUAL) big_gemm_kernel<64, 64, 3, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
+      else big_gemm_kernel<64, 64, 3, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+    } else {
+      if (a.epi == TG_RESIDUAL) big_gemm_kernel<64, 64, 3, TG_RESIDUAL, false><<<blocks, 256, 0, st>>>(a, p);
+      else big_gemm_kernel<64, 64, 3, TG_STORE, false><<<blocks, 256, 0, st>>>(a, p);
+    }
   } else if (p.splitk > 1) {
     if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, 64, 3, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
     else big_gemm_kernel<128, 64, 3, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);

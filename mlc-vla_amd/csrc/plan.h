@@ -106,16 +106,23 @@ inline bool tile_plan(const TilePlanIn& a, TilePlan& p) {
     if (a.N % 4 != 0) return false;
     if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
     // long K (down_proj): 256 x 256 tiles over up to 8 K slices load a third less through
-    // L2 than 256 x 128 tiles over 4; shorter K keeps 256 x 128 tiles
-    p.bn = (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N))
-               ? 256 : 128;
+    // L2 than 256 x 128 tiles over 4.  Shorter K: 256 x 64 tiles over the whole K when they
+    // give at least half a workgroup per CU (the prefill's q/k/v and o_proj at P = 968: 6.11
+    // vs 6.25 ms per prefill against 256 x 128 tiles over 3 / 4 K slices), else 256 x 128.
+    const int mt = (a.M + TG_BM - 1) / TG_BM;
+    if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N))
+      p.bn = 256;
+    else if (a.K < 8192 && 2 * mt * ((a.N + 63) / 64) >= a.cus && a.cus > 0)
+      p.bn = 64;
+    else
+      p.bn = 128;
     p.ntiles = (a.N + p.bn - 1) / p.bn;
   }
   p.mtiles = (a.M + TG_BM - 1) / TG_BM;
   const int tiles = p.mtiles * p.ntiles, kts = (a.K + TG_BK - 1) / TG_BK;
   const int slots = tile_slots(tiles);
   int S = 1;
-  if (!a.geglu && a.split_ws && tiles <= a.sync_tiles && a.cus > 0) {
+  if (!a.geglu && p.bn != 64 && a.split_ws && tiles <= a.sync_tiles && a.cus > 0) {
     // at least 4 k tiles per slice
     S = std::min({8, a.cus / slots, kts / 4});
     const size_t part = tile_part_floats(p.bn);

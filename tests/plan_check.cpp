@@ -117,6 +117,8 @@ static void check_tile() {
               CHECK(p.splitk >= 1 && p.kt_per >= 1, "splitk %d kt_per %d", p.splitk, p.kt_per);
               CHECK((long)p.kt_per * p.splitk >= kts && (long)(p.splitk - 1) * p.kt_per < kts,
                     "K %d: %d slices of %d k tiles", K, p.splitk, p.kt_per);
+              CHECK(p.bn == 64 || p.bn == 128 || p.bn == 256, "n tile %d", p.bn);
+              if (p.bn == 64) CHECK(p.splitk == 1 && 2 * tiles >= cus, "256 x 64 tiles: %d tiles, %d splits", tiles, p.splitk);
               if (p.splitk > 1) {
                 CHECK(!geglu && ws_given, "split-K without a workspace or with the GeGLU epilogue");
                 CHECK(tiles <= in.sync_tiles, "%d tiles, %d meeting counters", tiles, in.sync_tiles);
