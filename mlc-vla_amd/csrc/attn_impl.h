@@ -379,10 +379,12 @@ __device__ __forceinline__ void make_q(const AttnArgs& a, const QRaw<HD>& r, int
 
 // Combine the per-split partial softmax states of one query row with one wave: every
 // partial load goes out at once (split indices past nsplit repeat a valid split with
-// weight 0); the split statistics are read lane by lane into uniform registers
-// (v_readlane), so the weights need no cross-lane LDS traffic.
+// weight 0).  Lane s holds split s's statistics and normalized weight; each weight reaches
+// the other lanes by one v_readlane where it is used, so no per-split arrays of uniform
+// registers stay live (at 24 or 32 splits they spilled).
 template <int MAXS, bool COH>
 __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row, int lane) {
+  static_assert(MAXS <= 64, "one split per lane");
   const int hd = a.hd;
   const int grp = a.H / a.KV;
   const int hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
@@ -400,40 +402,37 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0) * 2));
   // out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s with w_s = exp(m_s - max)
-  float ms[MAXS], wv[MAXS];
-  float mmax = -INFINITY;
+  const bool mine = lane < ns;
+  float mmax = mine ? m_l : -INFINITY;
+  for (int o2 = 32; o2 > 0; o2 >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o2));
+  const float w = mine ? exp_hw(m_l - mmax) * l_l : 0.f;
+  const float lsum = wave_sum(w);
+  const float wn = w * (1.0f / lsum);  // lanes past nsplit: 0
+  // a trip count uniform across the wave: every lane is active at the v_readlane of each
+  // weight (a lane outside a divergent loop might not hold its weight there)
+  for (int db = 0; db < hd; db += 256) {
+    const int d = db + lane * 4;
+    if (db > 0) {  // head dims past 256
+      const int dc = min(d, hd - 4);
 #pragma unroll
-  for (int s = 0; s < MAXS; ++s) {
-    ms[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), s));
-    if (s < ns) mmax = fmaxf(mmax, ms[s]);
-  }
-  float lsum = 0.f;
-#pragma unroll
-  for (int s = 0; s < MAXS; ++s) {
-    const float ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), s));
-    wv[s] = s < ns ? exp_hw(ms[s] - mmax) * ls : 0.f;
-    lsum += wv[s];
-  }
-  const float inv = 1.0f / lsum;
-  for (int d = lane * 4; d < hd; d += 256) {
-    if (d != d0) {  // head dims past 256
-#pragma unroll
-      for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d) * 2));
+      for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + dc) * 2));
     }
     f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) {
-      const float ws = wv[s] * inv;
+      const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wn), s));
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] += ws * h2f(o[s][i]);
     }
     h4 o4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o4[i] = f2h(acc[i]);
-    const int col = h * hd + d;
-    const size_t oi = a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col;
-    if constexpr (COH) store_dev<h4>(dev_rsrc(a.out, 0x7FFFFFF0), (int)(oi * 2), o4);
-    else *reinterpret_cast<h4*>(a.out + oi) = o4;
+    if (d < hd) {
+      const int col = h * hd + d;
+      const size_t oi = a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col;
+      if constexpr (COH) store_dev<h4>(dev_rsrc(a.out, 0x7FFFFFF0), (int)(oi * 2), o4);
+      else *reinterpret_cast<h4*>(a.out + oi) = o4;
+    }
   }
 }
 
