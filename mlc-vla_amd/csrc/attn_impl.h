@@ -402,11 +402,17 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0) * 2));
   // out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s with w_s = exp(m_s - max)
+  // max and sum over the splits: butterflies within groups of P >= MAXS lanes (the first
+  // group holds every split; the other groups' results are never read)
+  constexpr int P = MAXS <= 8 ? 8 : MAXS <= 16 ? 16 : MAXS <= 32 ? 32 : 64;
   const bool mine = lane < ns;
   float mmax = mine ? m_l : -INFINITY;
-  for (int o2 = 32; o2 > 0; o2 >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o2));
+#pragma unroll
+  for (int o2 = P / 2; o2 > 0; o2 >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o2));
   const float w = mine ? exp_hw(m_l - mmax) * l_l : 0.f;
-  const float lsum = wave_sum(w);
+  float lsum = w;
+#pragma unroll
+  for (int o2 = P / 2; o2 > 0; o2 >>= 1) lsum += __shfl_xor(lsum, o2);
   const float wn = w * (1.0f / lsum);  // lanes past nsplit: 0
   // a trip count uniform across the wave: every lane is active at the v_readlane of each
   // weight (a lane outside a divergent loop might not hold its weight there)
