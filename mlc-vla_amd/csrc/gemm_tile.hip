@@ -146,15 +146,16 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(TgArgs a, int mtiles, in
 
 // ---- long-M GEMM: 256-row tiles, operands DMA'd straight into swizzled LDS ----------------
 //
-// Workgroup tile 256 (m) x BN (n) x 64 (k), 4 waves in 2 x 2: wave (wm, wn) owns m rows
-// [128 wm, +128) and n rows [BN/2 wn, +BN/2) as 4 x NBW blocks of 32 x 32 on
-// v_mfma_f32_32x32x16_f16 with the weights as the A operand, so D[n][m] leaves each lane
-// 4 consecutive n of one m row (8-byte stores).
-// LDS: per stage A 256 x 64 and B BN x 64 halfs.  One global_load_lds of 16 B per lane
-// moves 8 rows x 128 B (a row is 8 lanes, one whole line); row r's piece p (8 halfs) lands
-// in slot p ^ (r & 7) of the row, so the MFMA operand reads (8 consecutive lanes = 8 rows,
-// same piece) touch 8 distinct 16-byte slots of 8 different 128-byte rows: conflict-free.
-// Two stages: the DMA of k tile t + 1 runs while tile t is multiplied.
+// Workgroup tile 256 (m) x BN (n) x BK (k).  4 waves in 2 x 2: wave (wm, wn) owns m rows
+// [128 wm, +128) and n rows [BN/2 wn, +BN/2); 8 waves in 2 x 4: n rows [BN/4 wn, +BN/4).  A
+// wave's rows are 4 x NBW blocks of 32 x 32 on v_mfma_f32_32x32x16_f16 with the weights as
+// the A operand, so D[n][m] leaves each lane 4 consecutive n of one m row (8-byte stores).
+// LDS: per stage A 256 x BK and B BN x BK halfs.  One global_load_lds of 16 B per lane
+// moves 512 / BK rows (BK 64: 8 rows x 128 B, a row is 8 lanes, one whole line); row r's
+// piece p (8 halfs) lands in slot p ^ swz(r) of the row, so the MFMA operand reads
+// (consecutive lanes = consecutive rows, same piece) touch distinct 16-byte slots:
+// conflict-free.  NST stages: the DMA of k tiles t + 1 .. t + NST - 2 runs while tile t is
+// multiplied.
 // Split-K (SPLIT): the S workgroups of a tile run on one XCD (workgroups are dealt to the 8
 // XCDs round-robin by linear id); each writes its fp32 partial in the MFMA register order
 // (1 KB per store), they meet (group_meet_gen: the grid is launched only when it fits on
@@ -206,9 +207,14 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BN, int BK, int NST, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
-  constexpr int NBW = BN / 64;                  // n blocks of 32 per wave
+// NWV waves: 4 in 2 x 2 (a wave owns 128 m x BN/2 n), or 8 in 2 x 4 (128 m x BN/4 n; two
+// waves per SIMD, so one's LDS reads and barrier waits overlap the other's MFMAs)
+template <int BN, int BK, int NST, int EPI, bool SPLIT, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p) {
+  static_assert(NWV == 4 || (NWV == 8 && BN >= 128), "8 waves need n tiles of 128 or 256");
+  constexpr int WNN = NWV / 2;                  // waves along n
+  constexpr int TNW = BN / WNN;                 // n rows per wave
+  constexpr int NBW = TNW / 32;                 // n blocks of 32 per wave
   constexpr int ASZ = GBM * BK * 2, BSZ = BN * BK * 2;
   constexpr int STG = ASZ + BSZ;
   constexpr int RPI = 512 / BK, LPR = BK / 8;   // rows per DMA instruction, lanes per row
@@ -217,7 +223,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, lh = lane >> 5;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WNN, wn = w % WNN;
   // tile and K slice: XCD x (id % 8) owns the consecutive tiles [x per, (x + 1) per), all
   // M tiles of an N tile together, so each weight tile is fetched into one L2; the S
   // slices of a tile share the XCD
@@ -231,10 +237,11 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   const int m0 = tm * GBM;
   const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg + BK - 1) / BK;
 
-  // DMA of this wave's rows: A rows [64 w, +64), B rows [BN/4 w, +BN/4), 8 rows per
-  // instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in the
-  // scalar offset; rows past the operand read zeros (the buffer's size)
-  constexpr int NAI = GBM / RPI / 4, NBI = BN / RPI / 4, NI = NAI + NBI;
+  // DMA of this wave's rows: A rows [GBM/NWV w, +GBM/NWV), B rows [BN/NWV w, +BN/NWV), RPI
+  // rows per instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in
+  // the scalar offset; rows past the operand read zeros (the buffer's size)
+  constexpr int NAI = GBM / RPI / NWV, NBI = BN / RPI / NWV, NI = NAI + NBI;
+  static_assert(NAI * RPI * NWV == GBM && NBI * RPI * NWV == BN, "whole DMA instructions per wave");
   const int lr = lane / LPR, pc = (lane % LPR) ^ tile_swz<BK>(lr);  // row in the instruction, its piece
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<_Float16*>(a.a), 0, (int)min((size_t)a.M * a.lda * 2, (size_t)0x7fffffff), 0x00020000);
@@ -299,7 +306,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     const int pp = 2 * kb + lh;
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
-      wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz<BK>(wn * (BN / 2) + nb * 32 + l32, pp));
+      wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz<BK>(wn * TNW + nb * 32 + l32, pp));
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz<BK>(wm * 128 + mb * 32 + l32, pp));
   };
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     if (m >= a.M) return;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = tn * BN + wn2 * (BN / 2) + nb * 32 + 8 * q + 4 * lh;
+      const int n = tn * BN + wn2 * TNW + nb * 32 + 8 * q + 4 * lh;
       if (n >= a.N) continue;
       _Float16* cp = a.c + (size_t)m * a.ldc + n;
       h4 y;
@@ -376,7 +383,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
         if (m >= a.M) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int jo = tn * (BN / 2) + wn * (BN / 4) + hb * 32 + 8 * q + 4 * lh;
+          const int jo = tn * (BN / 2) + wn * (TNW / 2) + hb * 32 + 8 * q + 4 * lh;
           h4 y;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   } else {
     // partial of this split: [wave][nb][mb][q][lane] f4
     constexpr int BLK = NBW * 4;                // blocks per wave
-    constexpr size_t TILE_F4 = 4 * BLK * 4 * 64;  // f4 per split partial
+    constexpr size_t TILE_F4 = NWV * BLK * 4 * 64;  // f4 per split partial
     f4* part = reinterpret_cast<f4*>(p.ws) + ((size_t)tile * S + s) * TILE_F4;
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
@@ -407,7 +414,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
           const f4 v = {acc[nb][mb][4 * q], acc[nb][mb][4 * q + 1], acc[nb][mb][4 * q + 2], acc[nb][mb][4 * q + 3]};
           part[((w * BLK + nb * 4 + mb) * 4 + q) * 64 + lane] = v;
         }
-    __shared__ int met;
+    int& met = *reinterpret_cast<int*>(lds);  // the stages are free after the last tile
     wait_all_memory();
     __syncthreads();
     if (tid == 0) {
@@ -417,7 +424,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
     __syncthreads();
     // blocks u = (wave role, nb, mb) of the tile, u % S == s, one wave each
     const f4* base = reinterpret_cast<const f4*>(p.ws) + (size_t)tile * S * TILE_F4;
-    for (int u = s + S * w; u < 4 * BLK; u += 4 * S) {
+    for (int u = s + S * w; u < NWV * BLK; u += NWV * S) {
       const int w2 = u / BLK, b = u % BLK, nb = b / 4, mb = b % 4;
       f16v v;
 #pragma unroll
@@ -434,7 +441,7 @@ __global__ __launch_bounds__(256) void big_gemm_kernel(TgArgs a, GemmPlan p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) v[e] = __builtin_nanf("");
       }
-      store_block(v, w2 >> 1, w2 & 1, nb, mb);
+      store_block(v, w2 / WNN, w2 % WNN, nb, mb);
     }
   }
 }
@@ -466,11 +473,13 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
 int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   const int tiles = p.mtiles * p.ntiles;
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
-  // 256 x 256 tiles: 4 stages of 32 k (128 KB); 256 x 128: 3 stages of 64 k (144 KB)
-  if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false><<<blocks, 256, 0, st>>>(a, p);
+  // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
+  // 102 us, its split-K reduction spread over twice the waves; gate_up unchanged; 5 stages
+  // (160 KB) were slower); 256 x 128: 3 stages of 64 k (144 KB); 256 x 64: 3 stages of 64 k
+  if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false, 8><<<blocks, 512, 0, st>>>(a, p);
   else if (p.bn == 256) {
-    if (a.epi == TG_RESIDUAL) big_gemm_kernel<256, 32, 4, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
-    else big_gemm_kernel<256, 32, 4, TG_STORE, true><<<blocks, 256, 0, st>>>(a, p);
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<256, 32, 4, TG_RESIDUAL, true, 8><<<blocks, 512, 0, st>>>(a, p);
+    else big_gemm_kernel<256, 32, 4, TG_STORE, true, 8><<<blocks, 512, 0, st>>>(a, p);
   } else if (p.bn == 64) {
     if (p.splitk > 1) {
       if (a.epi == TG_RESIDUAL) big_gemm_kernel<64, 64, 3, TG_RESIDUAL, true><<<blocks, 256, 0, st>>>(a, p);
