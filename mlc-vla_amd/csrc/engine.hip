@@ -1156,17 +1156,19 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
 }
 
 int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void* stream) {
-  MLCV_REQUIRE(ctx && ptrs, "null argument");
+  MLCV_REQUIRE(ctx, "null argument");
   Ctx& c = ctx->c;
+  // unbound until this call has finished: any failure below (a rejected list included) leaves
+  // the context refusing every entry point ("parameters not bound") instead of pointing at
+  // freed copies or at a half-built set of layers
+  c.bound = false;
+  c.drop_graphs();
+  MLCV_REQUIRE(ptrs, "null argument");
   int32_t want = 0;
   MLCV_TRY(mlcv_param_count(&c.cfg, &want));
   MLCV_REQUIRE(count == want, "parameter count mismatch (expected " + std::to_string(want) + ")");
   for (int i = 0; i < count; ++i) MLCV_REQUIRE(ptrs[i] != nullptr, "null parameter pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // unbound until this call has finished: a failure below leaves the context refusing every
-  // entry point ("parameters not bound") instead of pointing at freed copies
-  c.bound = false;
-  c.drop_graphs();
   MLCV_HIP(hipStreamSynchronize(st));
   for (void* p : c.bind_owned) (void)hipFree(p);
   c.bind_owned.clear();

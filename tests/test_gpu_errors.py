@@ -6,6 +6,9 @@ again afterwards.
 - The tile GEMM's split-K meeting (csrc/gemm_tile.hip): through mlcv_tile_linear, which
   returns -4, and through the prefill of a context (MLCV_OPT_MEET_POLLS), reported by
   mlcv_sync when the keys are read.
+
+Also: a failed mlcv_bind_params leaves the context unbound, so a caller that still believes
+the old binding stands gets "parameters not bound" instead of a step over freed copies.
 """
 
 from __future__ import annotations
@@ -73,3 +76,22 @@ def test_prefill_meeting_give_up_is_reported_by_sync():
     k2, v2 = (t.numpy() for t in vm["prefill"](dv(prefix), pm, params))
     np.testing.assert_array_equal(k2, good_k)
     np.testing.assert_array_equal(v2, good_v)
+
+
+def test_failed_bind_leaves_the_context_unbound():
+    from stepcheck import Step
+
+    print("bind failure: tiny model", flush=True)
+    s = Step(TINY_KWARGS, persist=False)
+    vm = s.runner.vm
+    good = s.run()
+    ptrs = list(vm._bound)  # the device pointers of the current binding
+    ptrs[len(ptrs) // 2] = None
+    arr = (ctypes.c_void_p * len(ptrs))(*[ctypes.c_void_p(p) if p else None for p in ptrs])
+    with pytest.raises(N.MlcvError, match="null parameter pointer"):
+        N.call("mlcv_bind_params", vm._ctx, arr, len(ptrs), _st())
+    # the VM still believes in its old binding; the context refuses instead of stepping
+    with pytest.raises(N.MlcvError, match="parameters not bound"):
+        s.run()
+    vm._bound = None  # a caller that binds again gets the same results as before
+    np.testing.assert_array_equal(s.run(), good)
