@@ -183,10 +183,12 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, __attr
 // LDS image of a row-major operand tile of BK halfs per row: one 1 KB DMA instruction holds
 // RPI = 512 / BK rows, row r's 16-byte piece p sits in slot p ^ swz(r) of the row.  The
 // MFMA operand read (consecutive lanes = consecutive rows, one piece) then hits distinct
-// banks: BK 64 (128-byte rows) swizzles by r mod 8, BK 32 (64-byte rows, 4 per 256 bytes
-// of banks) by (r / 4) mod 4.
+// banks whether the LDS serves 128 or 256 bytes of a 16-byte read per clock (32 or 64 banks):
+// BK 32 (64-byte rows) swizzles by (r / 4) mod 4; BK 64 (128-byte rows) by (r mod 8) xor
+// bit 3 of r, which separates rows r and r + 8 (the same bank half at 64 banks; r mod 8
+// alone made them collide: a 2-way conflict on every operand read).
 template <int BK>
-__device__ __forceinline__ int tile_swz(int r) { return BK == 64 ? (r & 7) : ((r >> 2) & 3); }
+__device__ __forceinline__ int tile_swz(int r) { return BK == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : ((r >> 2) & 3); }
 template <int BK>
 __device__ __forceinline__ int lds_swz(int r, int p) {
   constexpr int RPI = 512 / BK;
@@ -242,14 +244,19 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   // the scalar offset; rows past the operand read zeros (the buffer's size)
   constexpr int NAI = GBM / RPI / NWV, NBI = BN / RPI / NWV, NI = NAI + NBI;
   static_assert(NAI * RPI * NWV == GBM && NBI * RPI * NWV == BN, "whole DMA instructions per wave");
-  const int lr = lane / LPR, pc = (lane % LPR) ^ tile_swz<BK>(lr);  // row in the instruction, its piece
+  // row in the instruction and LDS slot of this lane; the piece it loads depends on the tile row
+  const int lr = lane / LPR, ls = lane % LPR;
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<_Float16*>(a.a), 0, (int)min((size_t)a.M * a.lda * 2, (size_t)0x7fffffff), 0x00020000);
-  int aoff[NAI];
+  int aoff[NAI], apc[NAI];
 #pragma unroll
-  for (int i = 0; i < NAI; ++i) aoff[i] = ((m0 + (NAI * w + i) * RPI + lr) * a.lda + pc * 8) * 2;
+  for (int i = 0; i < NAI; ++i) {
+    const int r = (NAI * w + i) * RPI + lr;
+    apc[i] = ls ^ tile_swz<BK>(r);
+    aoff[i] = ((m0 + r) * a.lda + apc[i] * 8) * 2;
+  }
   const _Float16* bbase[NBI];  // per instruction (wave-uniform): segment base and bytes
-  int bbytes[NBI], boff[NBI];
+  int bbytes[NBI], boff[NBI], bpc[NBI];
 #pragma unroll
   for (int i = 0; i < NBI; ++i) {
     const int r0 = (NBI * w + i) * RPI;  // first B tile row of the instruction (uniform)
@@ -271,7 +278,8 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     }
     bbase[i] = base;
     bbytes[i] = (int)min((size_t)rows * a.ldb * 2, (size_t)0x7fffffff);
-    boff[i] = (row * a.ldb + pc * 8) * 2;
+    bpc[i] = ls ^ tile_swz<BK>(r0 + lr);
+    boff[i] = (row * a.ldb + bpc[i] * 8) * 2;
   }
   // DMA instruction i (A rows for i < NAI, then B rows) of k tile kt into a stage
   // K past the last multiple of BK: this lane's 8-half piece at k >= K gets an offset past the
@@ -280,7 +288,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   auto dma1 = [&](int i, int kt, int stage) __attribute__((always_inline)) {
     char* sb = lds + stage * STG;
     const int ko = (kbeg + kt * BK) * 2;
-    const bool kin = kbeg + kt * BK + pc * 8 < a.K;
+    const bool kin = kbeg + kt * BK + (i < NAI ? apc[i] : bpc[i - NAI]) * 8 < a.K;
     if (i < NAI)
       buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), kin ? aoff[i] : OOB, ko);
     else
