@@ -203,11 +203,13 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
                          int32_t k_f32, const void* vp, int32_t Sp, const float* mask, const void* ks,
                          const void* vs, int32_t Ts, void* out, void* stream);
 
-/* The prefill's attention kernel as prefill runs it (attn_prefill_e0, gemma_dual.py:236-253,
+/* The prefill's attention as prefill runs it (attn_prefill_e0, gemma_dual.py:236-253,
  * 334-341; testing): q [P][q_ld] f16 as the q/k/v projection leaves it (heads of hd columns
  * from column 0, not yet roped), roped with cos / sin [P][hd/2] f32 and scaled by 1/sqrt(hd)
- * in the kernel; keys [KV][P][hd] f32 roped and values [KV][P][hd] f16 (one layer of the
- * cache), mask [P] f32 additive -> out [P][H*hd] f16.  The same split plan as prefill. */
+ * (hd a multiple of 64: by a kernel that writes q split hi/lo in the attention's fragment
+ * order, then the 8-wave attention; otherwise in the attention's loader); keys [KV][P][hd]
+ * f32 roped and values [KV][P][hd] f16 (one layer of the cache), mask [P] f32 additive ->
+ * out [P][H*hd] f16.  The same split plan and launches as prefill. */
 int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const float* sin, int32_t P, int32_t H,
                            int32_t KV, int32_t hd, const float* keys, const void* values, const float* mask, void* out,
                            void* stream);

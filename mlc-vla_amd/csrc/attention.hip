@@ -100,6 +100,55 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   combine_row<MAXS, false>(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
+// q fragments of the prefill: one thread per (kv head, 16-row tile, k step of the first half
+// of the head dims, lane): lane 16 g + r of k step ks takes row 16 tile + r, dims
+// d = 32 ks + 8 g .. +7 and their RoPE partners d + hd/2, and writes their hi and lo halves,
+// so every wave store is one whole 1 KB fragment block (attn_qf_index).  RoPE and the scale
+// in fp32 as the attention's own q loader (make_q) computes them.
+__device__ __forceinline__ void q_frag_item(const _Float16* __restrict__ q, int ld, const float* __restrict__ cosb,
+                                            const float* __restrict__ sinb, int P, int grp, int hd, float q_scale,
+                                            int KV, int ntiles, _Float16* __restrict__ qf, long idx) {
+  const int half = hd / 2, nks = hd / 32, nk2 = nks / 2;
+  if (idx >= (long)KV * ntiles * nk2 * 64) return;
+  const int lane = (int)(idx & 63);
+  const long rest = idx >> 6;
+  const int ks = (int)(rest % nk2), tile = (int)((rest / nk2) % ntiles), kvh = (int)(rest / nk2 / ntiles);
+  const int row = 16 * tile + (lane & 15), d = 32 * ks + 8 * (lane >> 4);
+  h8 hi1, lo1, hi2, lo2;
+  if (row < P * grp) {
+    const int hl = row / P, t = row % P, h = kvh * grp + hl;
+    const _Float16* qr = q + (size_t)t * ld + (size_t)h * hd + d;
+    const h8 x1 = *reinterpret_cast<const h8*>(qr), x2 = *reinterpret_cast<const h8*>(qr + half);
+    const f4* cp = reinterpret_cast<const f4*>(cosb + (size_t)t * half + d);
+    const f4* sp = reinterpret_cast<const f4*>(sinb + (size_t)t * half + d);
+    const f4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = h2f(x1[e]), b = h2f(x2[e]);
+      const float c = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+      _Float16 hv, lv;
+      split_f32((a * c - b * sn) * q_scale, hv, lv);
+      hi1[e] = hv;
+      lo1[e] = lv;
+      split_f32((b * c + a * sn) * q_scale, hv, lv);
+      hi2[e] = hv;
+      lo2[e] = lv;
+    }
+  } else {
+    hi1 = lo1 = hi2 = lo2 = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  *reinterpret_cast<h8*>(qf + attn_qf_index(kvh, ntiles, nks, row, d, 0)) = hi1;
+  *reinterpret_cast<h8*>(qf + attn_qf_index(kvh, ntiles, nks, row, d, 1)) = lo1;
+  *reinterpret_cast<h8*>(qf + attn_qf_index(kvh, ntiles, nks, row, d + half, 0)) = hi2;
+  *reinterpret_cast<h8*>(qf + attn_qf_index(kvh, ntiles, nks, row, d + half, 1)) = lo2;
+}
+__global__ __launch_bounds__(256) void q_frag_kernel(const _Float16* __restrict__ q, int ld,
+                                                     const float* __restrict__ cosb, const float* __restrict__ sinb,
+                                                     int P, int grp, int hd, float q_scale, int KV, int ntiles,
+                                                     _Float16* __restrict__ qf) {
+  q_frag_item(q, ld, cosb, sinb, P, grp, hd, q_scale, KV, ntiles, qf, (long)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
 // post-RoPE K (fp32) and V (fp16) of one prefill layer into the [KV][P][hd] cache slices
 __global__ void kv_writer_kernel(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
                                  const float* __restrict__ cosb, const float* __restrict__ sinb, int P, int KV,
@@ -124,11 +173,11 @@ __global__ void kv_writer_kernel(const _Float16* __restrict__ qkv, int ld, int k
 }
 
 // the same with 4 consecutive dims per thread (hd % 8 == 0, ld, koff, voff multiples of 4)
-__global__ void kv_writer4_kernel(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
-                                  const float* __restrict__ cosb, const float* __restrict__ sinb, int P, int KV, int hd,
-                                  float* __restrict__ keys, _Float16* __restrict__ values) {
+__device__ __forceinline__ void kv_writer4_item(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
+                                                const float* __restrict__ cosb, const float* __restrict__ sinb, int P,
+                                                int KV, int hd, float* __restrict__ keys,
+                                                _Float16* __restrict__ values, long idx) {
   const int half = hd / 2, q4 = half / 4;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long total = (long)P * KV * q4;
   if (idx >= total) return;
   const int i = (int)(idx % q4) * 4;
@@ -152,6 +201,25 @@ __global__ void kv_writer4_kernel(const _Float16* __restrict__ qkv, int ld, int 
   *reinterpret_cast<f4*>(ko + i + half) = o2;
   *reinterpret_cast<h4*>(vo + i) = *reinterpret_cast<const h4*>(vr + i);
   *reinterpret_cast<h4*>(vo + i + half) = *reinterpret_cast<const h4*>(vr + i + half);
+}
+__global__ void kv_writer4_kernel(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
+                                  const float* __restrict__ cosb, const float* __restrict__ sinb, int P, int KV, int hd,
+                                  float* __restrict__ keys, _Float16* __restrict__ values) {
+  kv_writer4_item(qkv, ld, koff, voff, cosb, sinb, P, KV, hd, keys, values,
+                  (long)blockIdx.x * blockDim.x + threadIdx.x);
+}
+// one launch for both: the first kvb blocks write the K/V cache slices, the rest q's fragments
+__global__ __launch_bounds__(256) void kvq_writer_kernel(const _Float16* __restrict__ qkv, int ld, int koff, int voff,
+                                                         const float* __restrict__ cosb, const float* __restrict__ sinb,
+                                                         int P, int H, int KV, int hd, float* __restrict__ keys,
+                                                         _Float16* __restrict__ values, float q_scale, int ntiles,
+                                                         _Float16* __restrict__ qf, int kvb) {
+  if ((int)blockIdx.x < kvb)
+    kv_writer4_item(qkv, ld, koff, voff, cosb, sinb, P, KV, hd, keys, values,
+                    (long)blockIdx.x * blockDim.x + threadIdx.x);
+  else
+    q_frag_item(qkv, ld, cosb, sinb, P, H / KV, hd, q_scale, KV, ntiles, qf,
+                (long)(blockIdx.x - kvb) * blockDim.x + threadIdx.x);
 }
 
 // plain Gemma RMSNorm: out = fp16(x / sqrt(mean(x^2) + eps) * (1 + w)), one block per row.
@@ -372,6 +440,39 @@ int kv_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const floa
     kv_writer_kernel<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(qkv, ld, koff, voff, cos, sin, P, KV, hd, keys,
                                                                        values);
   }
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int kvq_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin, int P,
+                      int H, int KV, int hd, float* keys, _Float16* values, float q_scale, int rpad, _Float16* qf,
+                      hipStream_t st) {
+  const bool vec = hd % 8 == 0 && ld % 4 == 0 && koff % 4 == 0 && voff % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(keys) |
+                     reinterpret_cast<uintptr_t>(values) | reinterpret_cast<uintptr_t>(cos) |
+                     reinterpret_cast<uintptr_t>(sin) | reinterpret_cast<uintptr_t>(qf)) & 15) == 0;
+  if (!vec || !qf || hd % 64 != 0 || ld % 8 != 0) {  // two launches
+    MLCV_TRY(kv_writer_launch(qkv, ld, koff, voff, cos, sin, P, KV, hd, keys, values, st));
+    return qf ? q_frag_launch(qkv, ld, cos, sin, P, H, KV, hd, q_scale, rpad, qf, st) : 0;
+  }
+  MLCV_REQUIRE(P > 0 && KV > 0 && H % KV == 0 && rpad % 64 == 0 && rpad >= P * (H / KV), "q fragment shape");
+  const long kvt = (long)P * KV * (hd / 8), qt = (long)KV * (rpad / 16) * (hd / 64) * 64;
+  const int kvb = (int)((kvt + 255) / 256);
+  kvq_writer_kernel<<<(unsigned)(kvb + (qt + 255) / 256), 256, 0, st>>>(qkv, ld, koff, voff, cos, sin, P, H, KV, hd,
+                                                                          keys, values, q_scale, rpad / 16, qf, kvb);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int q_frag_launch(const _Float16* q, int ld, const float* cos, const float* sin, int P, int H, int KV, int hd,
+                  float q_scale, int rpad, _Float16* qf, hipStream_t st) {
+  MLCV_REQUIRE(q && cos && sin && qf && P > 0 && KV > 0 && H % KV == 0, "q fragment arguments");
+  MLCV_REQUIRE(hd % 64 == 0 && ld % 8 == 0 && rpad % 64 == 0 && rpad >= P * (H / KV), "q fragment shape");
+  MLCV_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(cos) | reinterpret_cast<uintptr_t>(sin) |
+                 reinterpret_cast<uintptr_t>(qf)) & 15) == 0, "q fragment buffers must be 16-byte aligned");
+  const long total = (long)KV * (rpad / 16) * (hd / 64) * 64;
+  q_frag_kernel<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(q, ld, cos, sin, P, H / KV, hd, q_scale, KV, rpad / 16,
+                                                                   qf);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

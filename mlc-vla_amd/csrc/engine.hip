@@ -162,6 +162,9 @@ struct Ctx {
   // prefill path
   _Float16 *px, *pxn, *pqkv, *pctx, *ph, *pvalues;
   float *pcos, *psin, *pkeys;
+  // the prefill attention's q in fragment order (q_frag_launch; head dims a multiple of 64,
+  // else null and the attention ropes the raw q in its loader)
+  _Float16* pqf = nullptr;
   // the joint forward (denoise_step): suffix RoPE tables at positions P..P+T-1, all-valid mask
   float *m0cos = nullptr, *m0sin = nullptr, *m0mask = nullptr;
   // workspaces
@@ -628,11 +631,16 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     g.epi = TG_STORE;
     gemm_ws_args(c, g);
     MLCV_TRY(tg_launch(g, st));
-    MLCV_TRY(kv_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.KV, HD, kL, vL, st));
-    if (L == c.D - 1) break;  // the last layer's attention / MLP feed no output
-    MLCV_TRY(attn_launch(prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
-                                           c.pf_nsplit, c.pf_kps, c.attn_ws),
-                         st));
+    // the cache slices of this layer, and (but for the last layer, whose attention feeds no
+    // output) q roped, scaled and split into the attention's fragment order, in one launch
+    const bool last = L == c.D - 1;
+    AttnArgs pa = prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
+                                    c.pf_nsplit, c.pf_kps, c.attn_ws);
+    MLCV_TRY(kvq_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, pa.q_scale,
+                               pa.rpad, last ? nullptr : c.pqf, st));
+    if (last) break;
+    pa.qf = c.pqf;  // null: the attention ropes the raw q in its loader
+    MLCV_TRY(attn_launch(pa, st));
     TgArgs o{};
     o.a = c.pctx;
     o.lda = nq;
@@ -913,6 +921,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.pxn, P * c.W0);
   ALLOC(c.pqkv, P * (nq + 2 * nkv));
   ALLOC(c.pctx, P * nq);
+  if (hd % 64 == 0) ALLOC(c.pqf, q_frag_halfs(c.KV, (int)((P * (c.H / c.KV) + 63) / 64 * 64), hd));
   ALLOC(c.ph, P * c.F0);
   ALLOC(c.pcos, P * hd / 2);
   ALLOC(c.psin, P * hd / 2);
@@ -1705,11 +1714,23 @@ int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const 
   int nsplit = 1, kps = 32;
   attn_plan(rows, P, 0, prefill_attn_target(rows), &nsplit, &kps);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
-  MLCV_TRY(scratch_reserve(attn_ws_floats(KV, rows, hd, nsplit) + 4, 1));
-  return attn_launch(prefill_attn_args(reinterpret_cast<const _Float16*>(q), q_ld, cos, sin, P, H, KV, hd, keys,
-                                       reinterpret_cast<const _Float16*>(values), mask,
-                                       reinterpret_cast<_Float16*>(out), nsplit, kps, g_scratch.ws),
-                     reinterpret_cast<hipStream_t>(stream));
+  // the attention's split partials, then (head dims a multiple of 64) q in fragment order,
+  // 16-byte aligned -- the prefill's own sequence of launches
+  const size_t ws_n = (attn_ws_floats(KV, rows, hd, nsplit) + 4 + 3) / 4 * 4;
+  const int rpad = (rows + 63) / 64 * 64;
+  const bool frag = hd % 64 == 0;
+  MLCV_TRY(scratch_reserve(ws_n + (frag ? q_frag_halfs(KV, rpad, hd) / 2 : 0), 1));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  AttnArgs a = prefill_attn_args(reinterpret_cast<const _Float16*>(q), q_ld, cos, sin, P, H, KV, hd, keys,
+                                 reinterpret_cast<const _Float16*>(values), mask, reinterpret_cast<_Float16*>(out),
+                                 nsplit, kps, g_scratch.ws);
+  if (frag) {
+    _Float16* qf = reinterpret_cast<_Float16*>(g_scratch.ws + ws_n);
+    MLCV_TRY(q_frag_launch(reinterpret_cast<const _Float16*>(q), q_ld, cos, sin, P, H, KV, hd, a.q_scale, a.rpad, qf,
+                           st));
+    a.qf = qf;
+  }
+  return attn_launch(a, st);
 }
 
 int mlcv_q4_quantize(const void* w, uint32_t* q_weight, void* q_scale, int32_t N, int32_t K, void* stream) {

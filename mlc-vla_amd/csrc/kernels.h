@@ -222,6 +222,17 @@ int rmsnorm_launch(const _Float16* x, const _Float16* w, _Float16* out, int rows
                    hipStream_t st);
 int kv_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin,
                      int P, int KV, int hd, float* keys, _Float16* values, hipStream_t st);
+// q of the prefill [P][ld] (heads of hd columns from column 0) roped with cos / sin [P][hd/2],
+// scaled by q_scale and split fp16 hi + lo into the attention's fragment order (attn_qf_index,
+// rows = P * H/KV padded to rpad, the padding rows zero); hd % 64 == 0.  The attention then
+// reads q as the step's attention does (AttnArgs::qf).
+int q_frag_launch(const _Float16* q, int ld, const float* cos, const float* sin, int P, int H, int KV, int hd,
+                  float q_scale, int rpad, _Float16* qf, hipStream_t st);
+inline size_t q_frag_halfs(int KV, int rpad, int hd) { return (size_t)KV * rpad * hd * 2; }
+// kv_writer_launch and q_frag_launch in one launch (where both apply; qf null: K/V only)
+int kvq_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin, int P,
+                      int H, int KV, int hd, float* keys, _Float16* values, float q_scale, int rpad, _Float16* qf,
+                      hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // tiled GEMM for prefill: C[M,N] = A[M,K] . B[N,K]^T, MFMA 32x32x16
