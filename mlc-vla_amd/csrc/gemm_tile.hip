@@ -285,10 +285,13 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   // K past the last multiple of BK: this lane's 8-half piece at k >= K gets an offset past the
   // buffer, which reads zeros (K % 8 == 0, so a piece is wholly inside or outside)
   constexpr int OOB = 0x7ffffff0;
-  auto dma1 = [&](int i, int kt, int stage) __attribute__((always_inline)) {
+  // live = false: the same instruction reads zeros (an offset past the buffer) into a free
+  // stage, so the k loop issues its DMA unconditionally: a branch around it made the compiler
+  // wait for every outstanding LDS read at the join, before the first MFMA of the tile
+  auto dma1 = [&](int i, int kt, int stage, bool live = true) __attribute__((always_inline)) {
     char* sb = lds + stage * STG;
     const int ko = (kbeg + kt * BK) * 2;
-    const bool kin = kbeg + kt * BK + (i < NAI ? apc[i] : bpc[i - NAI]) * 8 < a.K;
+    const bool kin = live && kbeg + kt * BK + (i < NAI ? apc[i] : bpc[i - NAI]) * 8 < a.K;
     if (i < NAI)
       buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), kin ? aoff[i] : OOB, ko);
     else
@@ -296,9 +299,9 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
           __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i - NAI]), 0, bbytes[i - NAI], 0x00020000),
           (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), kin ? boff[i - NAI] : OOB, ko);
   };
-  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+  auto dma = [&](int kt, int stage, bool live) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) dma1(i, kt, stage);
+    for (int i = 0; i < NI; ++i) dma1(i, kt, stage, live);
   };
 
   f16v acc[NBW][4];
@@ -320,44 +323,65 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   };
 
   // NST-stage ring: the DMA of tiles kt+1 .. kt+NST-2 stays in flight while tile kt
-  // multiplies; tile kt+NST-1 goes into the stage tile kt-1 used
+  // multiplies; tile kt+NST-1 goes into the stage tile kt-1 used.  Every tile issues its NI
+  // instructions (zeros past the K range), so the vmcnt counts below hold at the tail too.
+  // Pipelined across tiles: before the last MFMA group of tile kt (whose fragments are in
+  // registers) the wave waits for tile kt+1, crosses the barrier and reads tile kt+1's first
+  // fragments, so that LDS latency hides under that group.
+  static_assert(NST >= 3, "the ring keeps one tile in flight beyond the next");
+  constexpr int KB = BK / 16;          // k steps per tile
+  constexpr int NP = KB * NBW;         // MFMA groups of 4 per tile
+  static_assert(KB % 2 == 0, "fragment buffers alternate by k step parity");
+  // DMA instructions issued before the last group (tile kt+NST-1's part in flight at the wait)
+  constexpr int ISSUED = [] {
+    int n = 0;
+    for (int i = 0; i < NI; ++i) n += (i * NP) / NI < NP - 1;
+    return n;
+  }();
+  // late: the next k step's fragments are read after the first group of this one (NBW >= 2;
+  // read before the group, the compiler waited for all of them at its first MFMA)
+  constexpr bool LATE = NBW >= 2;
 #pragma unroll
-  for (int t = 0; t < NST - 1; ++t)
-    if (t < nkt) dma(t, t);
+  for (int t = 0; t < NST - 1; ++t) dma(t, t, t < nkt);
+  h8 wf[2][NBW], xf[2][4];
+  vm_wait<(NST - 2) * NI>();  // this wave's DMA of tile 0 (loads complete in issue order)
+  lds_barrier();
+  ldfrag(lds, 0, wf[0], xf[0]);
   for (int kt = 0; kt < nkt; ++kt) {
-    // this wave's DMA of tile kt has landed (loads complete in issue order); at the end of
-    // the K range fewer later tiles are in flight, so wait for all
-    if (kt + NST - 2 < nkt) vm_wait<(NST - 2) * NI>();
-    else vm_wait<0>();
-    lds_barrier();  // every wave's has, and nobody reads tile kt-1's stage any more
-    const bool more = kt + NST - 1 < nkt;
+    const bool more = kt + NST - 1 < nkt, next = kt + 1 < nkt;
     const int knext = kt + NST - 1, snext = (kt + NST - 1) % NST;
     const char* sa = lds + (kt % NST) * STG;
-    // the fragments of k step kb + 1 are read while step kb multiplies; the DMA
-    // instructions of tile kt+NST-1 are spread between the MFMA groups (issued in one
-    // burst, a busy memory pipeline holds the wave at issue while its MFMA unit idles)
-    constexpr int NP = (BK / 16) * NBW;  // MFMA groups of 4 per tile
-    h8 wf[2][NBW], xf[2][4];
-    ldfrag(sa, 0, wf[0], xf[0]);
 #pragma unroll
-    for (int kb = 0; kb < BK / 16; ++kb) {
-      if (kb + 1 < BK / 16) ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
+    for (int kb = 0; kb < KB; ++kb) {
+      if (!LATE && kb + 1 < KB) ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
         const int piece = kb * NBW + nb;
-        if (more) {
-#pragma unroll
-          for (int i = 0; i < NI; ++i)
-            if ((i * NP) / NI == piece) dma1(i, knext, snext);
+        if (piece == NP - 1 && next) {
+          // every fragment of tile kt is in registers once this wave's reads are back; after
+          // the barrier no wave reads tile kt's stage, and tile kt+1 is in LDS
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+          vm_wait<(NST - 3) * NI + ISSUED>();
+          lds_barrier();
+          ldfrag(lds + ((kt + 1) % NST) * STG, 0, wf[0], xf[0]);
+          __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if ((i * NP) / NI == piece) dma1(i, knext, snext, more);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[kb & 1][nb], xf[kb & 1][mb], acc[nb][mb]);
         __builtin_amdgcn_sched_barrier(0);
+        if (LATE && nb == 0 && kb + 1 < KB) {
+          ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   }
+  vm_wait<0>();  // the zero-filling DMA past the K range, before the epilogue
 
   // epilogue of one 32 x 32 block (wave role wm2 / wn2, blocks nb / mb): lane column
   // m = l32, rows n = 8 (e / 4) + 4 lh + (e % 4)
