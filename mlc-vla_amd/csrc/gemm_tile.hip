@@ -1,3 +1,4 @@
+#include <cstdlib>
 // Tiled MFMA GEMM for prefill (M = prefix length, ~1k rows): C[M,N] = A[M,K] . B[N,K]^T,
 // fp16 operands, fp32 accumulation on v_mfma_f32_32x32x16_f16.
 //
@@ -211,13 +212,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 // NWV waves: 4 in 2 x 2 (a wave owns 128 m x BN/2 n), or 8 in 2 x 4 (128 m x BN/4 n; two
 // waves per SIMD, so one's LDS reads and barrier waits overlap the other's MFMAs)
-template <int BN, int BK, int NST, int EPI, bool SPLIT, int NWV = 4>
+// BM: m rows of the tile (256, or 128: 64 m rows per wave)
+template <int BN, int BK, int NST, int EPI, bool SPLIT, int NWV = 4, int BM = GBM>
 __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p) {
   static_assert(NWV == 4 || (NWV == 8 && BN >= 128), "8 waves need n tiles of 128 or 256");
+  static_assert(BM == 256 || BM == 128, "m tiles of 256 or 128 rows");
   constexpr int WNN = NWV / 2;                  // waves along n
   constexpr int TNW = BN / WNN;                 // n rows per wave
   constexpr int NBW = TNW / 32;                 // n blocks of 32 per wave
-  constexpr int ASZ = GBM * BK * 2, BSZ = BN * BK * 2;
+  constexpr int TMW = BM / 2;                   // m rows per wave
+  constexpr int MB = TMW / 32;                  // m blocks of 32 per wave
+  constexpr int ASZ = BM * BK * 2, BSZ = BN * BK * 2;
   constexpr int STG = ASZ + BSZ;
   constexpr int RPI = 512 / BK, LPR = BK / 8;   // rows per DMA instruction, lanes per row
   __shared__ __attribute__((aligned(16))) char lds[NST * STG];
@@ -236,14 +241,14 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   const int tile = xcd * per + tl;
   if (tile >= ntile_all) return;
   const int tm = tile % p.mtiles, tn = tile / p.mtiles;
-  const int m0 = tm * GBM;
+  const int m0 = tm * BM;
   const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg + BK - 1) / BK;
 
   // DMA of this wave's rows: A rows [GBM/NWV w, +GBM/NWV), B rows [BN/NWV w, +BN/NWV), RPI
   // rows per instruction, as buffer loads to LDS: a 32-bit row offset per lane, the k tile in
   // the scalar offset; rows past the operand read zeros (the buffer's size)
-  constexpr int NAI = GBM / RPI / NWV, NBI = BN / RPI / NWV, NI = NAI + NBI;
-  static_assert(NAI * RPI * NWV == GBM && NBI * RPI * NWV == BN, "whole DMA instructions per wave");
+  constexpr int NAI = BM / RPI / NWV, NBI = BN / RPI / NWV, NI = NAI + NBI;
+  static_assert(NAI * RPI * NWV == BM && NBI * RPI * NWV == BN, "whole DMA instructions per wave");
   // row in the instruction and LDS slot of this lane; the piece it loads depends on the tile row
   const int lr = lane / LPR, ls = lane % LPR;
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
@@ -304,11 +309,11 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     for (int i = 0; i < NI; ++i) dma1(i, kt, stage, live);
   };
 
-  f16v acc[NBW][4];
+  f16v acc[NBW][MB];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[nb][mb][e] = 0.f;
 
@@ -319,7 +324,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     for (int nb = 0; nb < NBW; ++nb)
       wf[nb] = *reinterpret_cast<const h8*>(sa + ASZ + lds_swz<BK>(wn * TNW + nb * 32 + l32, pp));
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz<BK>(wm * 128 + mb * 32 + l32, pp));
+    for (int mb = 0; mb < MB; ++mb) xf[mb] = *reinterpret_cast<const h8*>(sa + lds_swz<BK>(wm * TMW + mb * 32 + l32, pp));
   };
 
   // NST-stage ring: the DMA of tiles kt+1 .. kt+NST-2 stays in flight while tile kt
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   constexpr bool LATE = NBW >= 2;
 #pragma unroll
   for (int t = 0; t < NST - 1; ++t) dma(t, t, t < nkt);
-  h8 wf[2][NBW], xf[2][4];
+  h8 wf[2][NBW], xf[2][MB];
   vm_wait<(NST - 2) * NI>();  // this wave's DMA of tile 0 (loads complete in issue order)
   lds_barrier();
   ldfrag(lds, 0, wf[0], xf[0]);
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
           if ((i * NP) / NI == piece) dma1(i, knext, snext, more);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32x32x16(wf[kb & 1][nb], xf[kb & 1][mb], acc[nb][mb]);
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma32x32x16(wf[kb & 1][nb], xf[kb & 1][mb], acc[nb][mb]);
         __builtin_amdgcn_sched_barrier(0);
         if (LATE && nb == 0 && kb + 1 < KB) {
           ldfrag(sa, kb + 1, wf[(kb + 1) & 1], xf[(kb + 1) & 1]);
@@ -386,7 +391,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   // epilogue of one 32 x 32 block (wave role wm2 / wn2, blocks nb / mb): lane column
   // m = l32, rows n = 8 (e / 4) + 4 lh + (e % 4)
   auto store_block = [&](const f16v& v, int wm2, int wn2, int nb, int mb) __attribute__((always_inline)) {
-    const int m = m0 + wm2 * 128 + mb * 32 + l32;
+    const int m = m0 + wm2 * TMW + mb * 32 + l32;
     if (m >= a.M) return;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -410,8 +415,8 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
 #pragma unroll
     for (int hb = 0; hb < NBW / 2; ++hb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int m = m0 + wm * 128 + mb * 32 + l32;
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = m0 + wm * TMW + mb * 32 + l32;
         if (m >= a.M) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -430,21 +435,21 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) store_block(acc[nb][mb], wm, wn, nb, mb);
+      for (int mb = 0; mb < MB; ++mb) store_block(acc[nb][mb], wm, wn, nb, mb);
     return;
   } else {
     // partial of this split: [wave][nb][mb][q][lane] f4
-    constexpr int BLK = NBW * 4;                // blocks per wave
+    constexpr int BLK = NBW * MB;               // blocks per wave
     constexpr size_t TILE_F4 = NWV * BLK * 4 * 64;  // f4 per split partial
     f4* part = reinterpret_cast<f4*>(p.ws) + ((size_t)tile * S + s) * TILE_F4;
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f4 v = {acc[nb][mb][4 * q], acc[nb][mb][4 * q + 1], acc[nb][mb][4 * q + 2], acc[nb][mb][4 * q + 3]};
-          part[((w * BLK + nb * 4 + mb) * 4 + q) * 64 + lane] = v;
+          part[((w * BLK + nb * MB + mb) * 4 + q) * 64 + lane] = v;
         }
     int& met = *reinterpret_cast<int*>(lds);  // the stages are free after the last tile
     wait_all_memory();
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     // blocks u = (wave role, nb, mb) of the tile, u % S == s, one wave each
     const f4* base = reinterpret_cast<const f4*>(p.ws) + (size_t)tile * S * TILE_F4;
     for (int u = s + S * w; u < NWV * BLK; u += NWV * S) {
-      const int w2 = u / BLK, b = u % BLK, nb = b / 4, mb = b % 4;
+      const int w2 = u / BLK, b = u % BLK, nb = b / MB, mb = b % MB;
       f16v v;
 #pragma unroll
       for (int e = 0; e < 16; ++e) v[e] = 0.f;
@@ -496,6 +501,8 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
   in.ws_floats = a.ws_floats;
   in.sync_tiles = a.sync_tiles;
   in.cus = device_cus();
+  static const bool m128 = !std::getenv("MLCV_TG_M128") || std::atoi(std::getenv("MLCV_TG_M128")) != 0;
+  in.m128 = m128;  // tuning switch
   if (!tile_plan(in, p)) return false;
   p.ws = a.ws;
   p.sync = a.sync;
@@ -508,7 +515,13 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
   // 102 us, its split-K reduction spread over twice the waves; gate_up unchanged; 5 stages
   // (160 KB) were slower); 256 x 128: 3 stages of 64 k (144 KB); 256 x 64: 3 stages of 64 k
-  if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false, 8><<<blocks, 512, 0, st>>>(a, p);
+  if (p.bm == 128) {
+    // 128 x 128 over the whole K: 4 stages of 64 k (128 KB), 8 waves of 64 x 32 (the prefill's
+    // q/k/v 21.2 and o_proj 23.2 us against 256 x 64 tiles' 27 and 29 us; 8 waves against 4:
+    // prefill -12 us)
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<128, 64, 4, TG_RESIDUAL, false, 8, 128><<<blocks, 512, 0, st>>>(a, p);
+    else big_gemm_kernel<128, 64, 4, TG_STORE, false, 8, 128><<<blocks, 512, 0, st>>>(a, p);
+  } else if (a.epi == TG_GEGLU) big_gemm_kernel<256, 32, 4, TG_GEGLU, false, 8><<<blocks, 512, 0, st>>>(a, p);
   else if (p.bn == 256) {
     if (a.epi == TG_RESIDUAL) big_gemm_kernel<256, 32, 4, TG_RESIDUAL, true, 8><<<blocks, 512, 0, st>>>(a, p);
     else big_gemm_kernel<256, 32, 4, TG_STORE, true, 8><<<blocks, 512, 0, st>>>(a, p);

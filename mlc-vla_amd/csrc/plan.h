@@ -80,11 +80,12 @@ struct TilePlanIn {
   size_t ws_floats;
   int sync_tiles;  // tiles with meeting counters
   int cus;         // compute units of the device
+  bool m128 = true;  // 128 x 128 tiles allowed (tuning switch)
 };
 
 struct TilePlan {
-  int bn, splitk, kt_per;  // n tile, K slices, k tiles (of TG_BK) per slice
-  int mtiles, ntiles;      // ntiles: n tiles of bn (GeGLU: of bn / 2 outputs)
+  int bm, bn, splitk, kt_per;  // m tile, n tile, K slices, k tiles (of TG_BK) per slice
+  int mtiles, ntiles;          // ntiles: n tiles of bn (GeGLU: of bn / 2 outputs)
 };
 
 // fp32 partials of one split of a tile: [4 waves][bn / 64 blocks][4][4][64] f4
@@ -98,6 +99,7 @@ inline int tile_slots(int tiles) { return ((tiles + TG_NXCD - 1) / TG_NXCD) * TG
 // a tile meet through a bounded wait, and its partials within the workspace.
 inline bool tile_plan(const TilePlanIn& a, TilePlan& p) {
   if (a.small_tiles || a.K % 8 != 0 || a.M < 1 || a.lda % 8 != 0 || a.ldb % 8 != 0 || a.ldc % 4 != 0) return false;
+  p.bm = TG_BM;
   if (a.geglu) {
     if (a.F % 128 != 0) return false;
     p.bn = 256;
@@ -106,23 +108,27 @@ inline bool tile_plan(const TilePlanIn& a, TilePlan& p) {
     if (a.N % 4 != 0) return false;
     if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
     // long K (down_proj): 256 x 256 tiles over up to 8 K slices load a third less through
-    // L2 than 256 x 128 tiles over 4.  Shorter K: 256 x 64 tiles over the whole K when they
-    // give at least half a workgroup per CU (the prefill's q/k/v and o_proj at P = 968: 6.11
-    // vs 6.25 ms per prefill against 256 x 128 tiles over 3 / 4 K slices), else 256 x 128.
-    const int mt = (a.M + TG_BM - 1) / TG_BM;
-    if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N))
+    // L2 than 256 x 128 tiles over 4.  Shorter K, over the whole K, when the tiles give at
+    // least half a workgroup per CU: 128 x 128 (the prefill's q/k/v and o_proj at P = 968),
+    // else 256 x 64; else 256 x 128.
+    const int mt = (a.M + TG_BM - 1) / TG_BM, mt2 = (a.M + 127) / 128;
+    if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N)) {
       p.bn = 256;
-    else if (a.K < 8192 && 2 * mt * ((a.N + 63) / 64) >= a.cus && a.cus > 0)
-      p.bn = 64;
-    else
+    } else if (a.K < 8192 && a.m128 && 2 * mt2 * ((a.N + 127) / 128) >= a.cus && a.cus > 0) {
+      p.bm = 128;
       p.bn = 128;
+    } else if (a.K < 8192 && 2 * mt * ((a.N + 63) / 64) >= a.cus && a.cus > 0) {
+      p.bn = 64;
+    } else {
+      p.bn = 128;
+    }
     p.ntiles = (a.N + p.bn - 1) / p.bn;
   }
-  p.mtiles = (a.M + TG_BM - 1) / TG_BM;
+  p.mtiles = (a.M + p.bm - 1) / p.bm;
   const int tiles = p.mtiles * p.ntiles, kts = (a.K + TG_BK - 1) / TG_BK;
   const int slots = tile_slots(tiles);
   int S = 1;
-  if (!a.geglu && p.bn != 64 && a.split_ws && tiles <= a.sync_tiles && a.cus > 0) {
+  if (!a.geglu && p.bn != 64 && p.bm == TG_BM && a.split_ws && tiles <= a.sync_tiles && a.cus > 0) {
     // at least 4 k tiles per slice
     S = std::min({8, a.cus / slots, kts / 4});
     const size_t part = tile_part_floats(p.bn);
