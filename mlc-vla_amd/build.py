@@ -29,7 +29,7 @@ FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
-    # no packed-fp32 VALU instructions on this target
+    # no packed-fp32 VALU instructions on this target: some of their forms gave wrong results
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"),
 ]

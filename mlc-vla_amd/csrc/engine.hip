@@ -38,6 +38,7 @@ struct Layer {
 struct OpDesc {
   int seg_off = 0, nseg = 0, ntiles = 0, K = 0, epi = 0, seg_tiles = 0;
   int tr = 64, splits = 0;  // weight rows per tile, K slices (0: planner's choice)
+  int mg = 1;               // m groups per weight slab (fragment-major 16-row tiles)
   bool q4 = false;
   bool frag = false;  // fragment-major X and weights (16-row tiles)
   bool xrow = false;  // row-major X with M <= 16, fragment-major weights (16-row tiles)
@@ -46,13 +47,16 @@ struct OpDesc {
 // Tiling of the step's layer GEMMs.  With fragment-major operands (M < 64): 16-row tiles
 // whose waves load their operand fragments straight into registers; q/k/v, o_proj and
 // gate_up take the whole K per workgroup (no split-K exchange), down splits K in 4.
+// o_proj (64 weight slabs) shares each slab out over 4 workgroups of one m tile each, so
+// that it runs on 256 workgroups with a quarter of X each.
 // Otherwise (M >= 64) the row-major kernels stage X through LDS with 16/32-row tiles.
 // Everything else uses 64-row tiles and the planner's split.
 struct Tiling {
   int tr, splits;
+  int mg = 1;  // m groups: workgroups sharing a weight slab, each with 4 / mg m tiles
 };
 struct LayerTilings {
-  Tiling qkv = {16, 1}, o = {16, 1}, gu = {16, 1}, down = {16, 4};
+  Tiling qkv = {16, 1}, o = {16, 1, 4}, gu = {16, 1}, down = {16, 4};
   Tiling head = {16, 1}, tmlp = {16, 1};  // action_out and the time MLP (16-row tiles)
 };
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
@@ -73,10 +77,10 @@ enum : unsigned {
 };
 constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 
-// MLCV_TILING="qkv=16:S,o=TR:S,gu=TR:S,down=TR:S,head=16:S,tmlp=16:S" overrides the tile
-// rows (16, or 32 for o / gate_up / down) and K slices of the fragment-major GEMMs (the
-// time MLP's K slices apply to its small-M tiles) for tuning (read at context creation;
-// 0 = planner).
+// MLCV_TILING="qkv=16:S[:G],o=TR:S[:G],gu=TR:S[:G],down=TR:S[:G],head=16:S[:G],tmlp=16:S"
+// overrides the tile rows (16, or 32 for o / gate_up / down), K slices and, for 16-row
+// tiles, the m groups (1, 2 or 4) of the fragment-major GEMMs (the time MLP's K slices apply
+// to its small-M tiles) for tuning (read at context creation; 0 = planner).
 LayerTilings read_tilings() {
   LayerTilings lt;
   const char* e = std::getenv("MLCV_TILING");
@@ -92,8 +96,11 @@ LayerTilings read_tilings() {
       const std::string name = item.substr(0, eq);
       const int tr = std::atoi(item.substr(eq + 1, colon - eq - 1).c_str());
       const int sp = std::atoi(item.substr(colon + 1).c_str());
+      const size_t colon2 = item.find(':', colon + 1);
+      int mg = colon2 == std::string::npos ? 1 : std::atoi(item.substr(colon2 + 1).c_str());
+      if (!(mg == 2 || mg == 4) || tr != 16 || name == "tmlp") mg = 1;
       if (tr == 16 || (tr == 32 && (name == "o" || name == "gu" || name == "down"))) {
-        Tiling t{tr, sp};
+        Tiling t{tr, sp, mg};
         if (name == "qkv") lt.qkv = t;
         else if (name == "head") lt.head = t;
         else if (name == "tmlp") lt.tmlp = t;
@@ -286,6 +293,7 @@ SkOp make_op(const Ctx& c, const OpDesc& d, const _Float16* x, int ldx, int M) {
   for (int i = 0; i < d.nseg && i < 3; ++i) op.inl[i] = c.h_segs[d.seg_off + i];
   op.ntiles = d.ntiles;
   op.tr = d.tr;
+  op.mg = d.frag ? d.mg : 1;
   const SkPlan p = sk_plan(d.ntiles, d.K, (M + 63) / 64, d.splits);
   op.splitk = p.splitk;
   op.kper = p.kper;
@@ -1063,20 +1071,21 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
   const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
   struct Shape {
-    int ntiles, K, mb, tr, splits;
+    int ntiles, K, mb, tr, splits;  // mb: m blocks times m groups
   };
   auto tiles = [](int n, int cols) { return (n + cols - 1) / cols; };
   std::vector<Shape> shapes = {
-      {tiles(nq, tile_qkv(c).tr) + 2 * tiles(nkv, tile_qkv(c).tr), W1, mb_t, tile_qkv(c).tr, tile_qkv(c).splits},
-      {tiles(W1, tile_o(c).tr), nq, mb_t, tile_o(c).tr, tile_o(c).splits},
-      {tiles(c.F1, tile_gu(c).tr / 2), W1, mb_t, tile_gu(c).tr, tile_gu(c).splits},
-      {tiles(W1, tile_down(c).tr), c.F1, mb_t, tile_down(c).tr, tile_down(c).splits},
+      {tiles(nq, tile_qkv(c).tr) + 2 * tiles(nkv, tile_qkv(c).tr), W1, mb_t * tile_qkv(c).mg, tile_qkv(c).tr,
+       tile_qkv(c).splits},
+      {tiles(W1, tile_o(c).tr), nq, mb_t * tile_o(c).mg, tile_o(c).tr, tile_o(c).splits},
+      {tiles(c.F1, tile_gu(c).tr / 2), W1, mb_t * tile_gu(c).mg, tile_gu(c).tr, tile_gu(c).splits},
+      {tiles(W1, tile_down(c).tr), c.F1, mb_t * tile_down(c).mg, tile_down(c).tr, tile_down(c).splits},
       {tiles(W1, 16), W1, mb_s, 16, c.tilings.tmlp.splits},                      // time mlp
       {tiles(W1, 64), W1, mb_s, 64, 0},
       {std::max(2, c.NM - 2) * tiles(3 * W1, 64), W1, mb_s, 64, 0},              // modulation pieces
       {std::max(2, c.NM) * tiles(3 * W1, 16), W1, mb_s, 16, MOD_SPLITS},
       {tiles(W1, TR_AIN), c.A, mb_t, TR_AIN, SPLIT_AIN},                         // action_in
-      {tiles(c.A, tile_head(c).tr), W1, mb_t, tile_head(c).tr, tile_head(c).splits},  // action_out
+      {tiles(c.A, tile_head(c).tr), W1, mb_t * tile_head(c).mg, tile_head(c).tr, tile_head(c).splits},  // action_out
   };
   for (const Shape& s : shapes) {
     const SkPlan p = sk_plan(s.ntiles, s.K, s.mb, s.splits);
@@ -1289,6 +1298,10 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     seg_ops(c, ops[2], {seg_of(fgu, c.h, c.F1, c.F1)}, W1, EPI_GEGLU, c.q4, tile_gu(c).tr, tile_gu(c).splits);
     seg_ops(c, ops[3], {seg_of(fdn, c.x16, W1, W1)}, c.F1, EPI_GATED_RES, c.q4, tile_down(c).tr, tile_down(c).splits);
     for (int i = 0; i < 4; ++i) ops[i].frag = c.frag;
+    ops[0].mg = c.frag ? tile_qkv(c).mg : 1;
+    ops[1].mg = c.frag ? tile_o(c).mg : 1;
+    ops[2].mg = c.frag ? tile_gu(c).mg : 1;
+    ops[3].mg = c.frag ? tile_down(c).mg : 1;
   }
   {
     // small-M GEMVs: 16-row register-direct tiles on shuffled weights, or 64-row tiles
@@ -1332,6 +1345,7 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     MLCV_REQUIRE(fa.N >= 0, get_error());
     seg_ops(c, c.op_aout, {seg_of(fa, c.vout, c.A, c.A)}, W1, EPI_VOUT, c.q4, tile_head(c).tr, tile_head(c).splits);
     c.op_aout.frag = c.frag;
+    c.op_aout.mg = c.frag ? tile_head(c).mg : 1;
     c.pk.aout = pkl(fa);
   }
   if (c.pk_ok) {

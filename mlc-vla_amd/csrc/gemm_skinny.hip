@@ -114,8 +114,16 @@ __device__ __forceinline__ void sum_splits(const float* base, size_t split_strid
 // XM: 0 X row-major, staged through LDS; 1 fragment-major X and weights, loaded straight
 // into registers (16-row tiles); 2 row-major X with M <= 16 (one m tile, lanes of rows
 // past M contribute zeros) and fragment-major weights, loaded straight into registers.
-template <bool Q4, int NORM, int EPI, int NC, bool TABLE, int TR, int XM>
+// MG (fragment-major 16-row tiles): the 4 m tiles of a 64-row block are shared out over
+// MG workgroups per weight slab (grid z = m block * MG + m group), each multiplying 4 / MG
+// m tiles: MG times the weight reads (one XCD's L2 serves them, the groups of a slab share
+// its XCD when the tile count is a multiple of 8), a 1 / MG share of X per workgroup and
+// MG times the workgroups, with no exchange between them.  With the pre-scaled adaRMS
+// input every group also multiplies the m tile that holds the shift row M.
+template <bool Q4, int NORM, int EPI, int NC, bool TABLE, int TR, int XM, int MG = 1>
 __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
+  static_assert(MG == 1 || ((MG == 2 || MG == 4) && XM == 1 && TR == 16 && NORM != 1),
+                "m groups: fragment-major 16-row tiles");
   constexpr int SLABS = TR / 16;
   constexpr int KG = 4 / SLABS;      // waves per slab
   constexpr int CPW = NC / KG;       // chunks per wave per round
@@ -131,7 +139,11 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   // its MFMA B fragments are loaded straight from X into registers (no LDS staging, no
   // barrier between loads and MFMAs: each MFMA waits only for its own operands)
   constexpr bool DIRECT = XM != 0;
-  constexpr int XMT = XM == 2 ? 1 : 4;  // m tiles loaded and multiplied by the direct path
+  constexpr int XMT = XM == 2 ? 1 : 4 / MG;  // this workgroup's m tiles (direct path)
+  constexpr int EXT = MG > 1 && NORM == 2 ? 1 : 0;  // + the shift row's m tile (local XMT)
+  constexpr int PMT = XMT + EXT;              // m tiles loaded and multiplied by the direct path
+  constexpr int RMT = MG > 1 ? PMT : 4;       // m tiles held in the k-group sums
+  constexpr int MROWS = MG > 1 ? 16 * XMT : MB;  // rows of X this workgroup covers
   // fragment-major tiles of several slabs: the 4 waves split K as in a 16-row tile and
   // every wave multiplies its X fragments by all the slabs' weights (X is loaded once per
   // workgroup); the 4 k-group partials of each slab are summed before the epilogue, which
@@ -157,11 +169,12 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     if (blockIdx.z == 0) prefetch_run(op.pf, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * op.splitk);
     return;
   }
-  const int tile_id = blockIdx.x, s = blockIdx.y, mb = blockIdx.z;
+  const int tile_id = blockIdx.x, s = blockIdx.y, mb = blockIdx.z / MG;
+  const int mgi = MG > 1 ? (int)blockIdx.z % MG : 0;  // m group: m tiles XMT*mgi .. +XMT-1
   const int S = op.splitk;
-  const int m0 = mb * MB;
+  const int m0 = mb * MB + 16 * XMT * mgi;
   const int mlast = op.M - 1;
-  const int mrows = min(MB, op.M - m0);
+  const int mrows = min(MROWS, op.M - m0);
   const int xlast = NORM == 2 ? op.M : mlast;  // pre-scaled X carries the shift as row M
 
   // the segment: up to 3 from the kernel arguments, picked by selects (no branch on an
@@ -272,7 +285,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     // side instead of filling this XCD's L2 with lines the next launch cannot reuse
     __amdgpu_buffer_rsrc_t xr;
     if constexpr (XM == 1) xr = dev_rsrc(op.x, MB * K * 2);
-    h8 xf[LCPW][4][XMT];
+    h8 xf[LCPW][4][PMT];
 #pragma unroll
     for (int c = 0; c < LCPW; ++c)
 #pragma unroll
@@ -282,8 +295,10 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
           const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
           const int piece = Q4 ? 16 * j + r16 : lane;
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
-            xf[c][j][mt] = load_dev<h8>(xr, ((ks * 4 + mt) * 64 + piece) * 16);
+          for (int mt = 0; mt < PMT; ++mt) {
+            const int gmt = mt < XMT ? XMT * mgi + mt : op.M >> 4;  // 64-row block's m tile
+            xf[c][j][mt] = load_dev<h8>(xr, ((ks * 4 + gmt) * 64 + piece) * 16);
+          }
         } else {
           const int kx = min(kcs + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g), K - 8);
           xf[c][j][0] = load_global(reinterpret_cast<const h8*>(op.x + (size_t)min(r16, mlast) * op.ldx + kx));
@@ -325,7 +340,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
           for (int e = 0; e < 8; ++e) a[sl][e] = kok ? a[sl][e] : (_Float16)0.0f;
         }
 #pragma unroll
-        for (int mt = 0; mt < XMT; ++mt) {
+        for (int mt = 0; mt < PMT; ++mt) {
           h8 b = xf[c][j][mt];
           if constexpr (XM == 2) {
 #pragma unroll
@@ -439,12 +454,14 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
     for (int sl = 0; sl < SW; ++sl)
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < RMT; ++mt)
         red[((lkg * SLABS + (MSD ? sl : slab)) * 4 + mt) * 64 + lane] = acc[sl][mt];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NOWN; ++i) {
-      const int mt = kg + i * KG;
+      // with m groups, waves kg >= XMT own no m tile of the output (rows past MROWS: nothing
+      // is stored); wave XMT holds the shift row's tile (pre-scaled input)
+      const int mt = min(kg + i * KG, RMT - 1);
       f4 sum = red[((0 * SLABS + slab) * 4 + mt) * 64 + lane];
 #pragma unroll
       for (int q = 1; q < LKG; ++q) sum += red[((q * SLABS + slab) * 4 + mt) * 64 + lane];
@@ -458,7 +475,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
   for (int i = 0; i < NOWN; ++i) own_off[i] = ((slab * 4 + kg + i * KG) * 64 + lane) * 4;
   if (S > 1) {
-    const int cidx = tile_id * gridDim.z + mb;
+    const int cidx = tile_id * gridDim.z + blockIdx.z;
     float* wsp = op.ws + ((size_t)cidx * S + s) * TILE_F;
     if ((gridDim.x & 7) == 0) {
 #pragma unroll
@@ -495,7 +512,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     const int mtM = op.M >> 4, cM = op.M & 15;  // the shift row (M < 64: one m block)
 #pragma unroll
     for (int i = 0; i < NOWN; ++i)
-      if (kg + i * KG == mtM && r16 == cM) shiftacc[slab * 4 + g] = own[i];
+      if (kg + i * KG == (MG > 1 ? XMT : mtM) && r16 == cM) shiftacc[slab * 4 + g] = own[i];
     __syncthreads();
     const f4 sv = shiftacc[slab * 4 + g];
     const float nsc = op.nsc ? *op.nsc : 1.0f;
@@ -555,7 +572,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       const float o1a = x1a * rcs[0] - x2a * rcs[2], o1b = x1b * rcs[1] - x2b * rcs[3];
       const float o2a = x2a * rcs[0] + x1a * rcs[2], o2b = x2b * rcs[1] + x1b * rcs[3];
       const int m = m0 + 16 * kg + r16;
-      if (m < op.M) {
+      if (16 * kg + r16 < mrows) {  // m < M, and a row of this m group
         if (seg.rope == 1) {
           const int kvh = hh / op.rope_grp, row = (hh % op.rope_grp) * op.M + m;
           const int ntiles = op.rope_rpad / 16, nks = (HD + 31) / 32;
@@ -639,7 +656,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   }
   if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
     // the shift row of the pre-scaled copy: one lane per 4 columns
-    if (op.xu_out && kg == 0 && r16 == 0 && nok)
+    if (op.xu_out && kg == 0 && r16 == 0 && nok && mgi == 0)
       *reinterpret_cast<h4*>(op.xu_out + (op.frag_out ? xf_index(op.M, n0) : (size_t)op.M * ldo + n0)) = xush;
   }
   if constexpr (EPI == EPI_GATED_RES || EPI == EPI_STORE) {
@@ -761,24 +778,39 @@ constexpr bool sk_combo() {
   return TR == 64 && NORM != 2 && EPI != EPI_GATED_RES && EPI != EPI_GEGLU;
 }
 
+template <bool Q4, int NORM, int EPI, bool TABLE, int TR, int XM, int MG>
+int launch_nc_mg(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
+  constexpr bool MSD = XM == 1 && TR > 16;  // multi-slab fragment-major tiles: 4 k groups
+  constexpr int KG = MSD ? 4 : 4 / (TR / 16);
+  if (nc < KG) nc = KG;
+  switch (nc) {
+    case 1:
+      if constexpr (KG <= 1) skinny_kernel<Q4, NORM, EPI, 1, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op);
+      break;
+    case 2:
+      if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op);
+      break;
+    case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op); break;
+    default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op); break;
+  }
+  return 0;
+}
+
 template <bool Q4, int NORM, int EPI, bool TABLE, int TR, int XM>
 int launch_nc(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
   if constexpr (!sk_combo<NORM, EPI, TABLE, TR, XM>()) {
     MLCV_REQUIRE(false, "skinny GEMM: tile rows / prologue / epilogue combination not built");
   } else {
-    constexpr bool MSD = XM == 1 && TR > 16;  // multi-slab fragment-major tiles: 4 k groups
-    constexpr int KG = MSD ? 4 : 4 / (TR / 16);
-    if (nc < KG) nc = KG;
-    switch (nc) {
-      case 1:
-        if constexpr (KG <= 1) skinny_kernel<Q4, NORM, EPI, 1, TABLE, TR, XM><<<grid, 256, 0, st>>>(op);
-        break;
-      case 2:
-        if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR, XM><<<grid, 256, 0, st>>>(op);
-        break;
-      case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR, XM><<<grid, 256, 0, st>>>(op); break;
-      default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR, XM><<<grid, 256, 0, st>>>(op); break;
+    if (op.mg > 1) {
+      // m groups: built for the fragment-major 16-row tiles
+      if constexpr (XM == 1 && TR == 16 && !TABLE) {
+        if (op.mg == 2) return launch_nc_mg<Q4, NORM, EPI, TABLE, TR, XM, 2>(op, nc, grid, st);
+        return launch_nc_mg<Q4, NORM, EPI, TABLE, TR, XM, 4>(op, nc, grid, st);
+      } else {
+        MLCV_REQUIRE(false, "skinny GEMM m groups need fragment-major 16-row tiles");
+      }
     }
+    return launch_nc_mg<Q4, NORM, EPI, TABLE, TR, XM, 1>(op, nc, grid, st);
   }
   return 0;
 }
@@ -848,7 +880,8 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
     MLCV_REQUIRE(op.inl[i].n % 4 == 0 && op.inl[i].ldo % 4 == 0, "skinny GEMM outputs need n % 4 == 0");
   }
   const int mblocks = (op.M + MB - 1) / MB;
-  dim3 grid(op.ntiles, op.splitk, mblocks);
+  const int mg = op.mg > 1 ? op.mg : 1;
+  dim3 grid(op.ntiles, op.splitk, mblocks * mg);
   MLCV_REQUIRE(!op.prescaled || (op.rowss_in && op.M < MB && op.rowss_tiles >= 4 && op.rowss_tiles % 4 == 0 &&
                                   op.rowss_ld % 4 == 0),
                "pre-scaled adaRMS needs M < 64 (row M carries the shift) and the row statistics");
@@ -872,6 +905,8 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
                                          op.rope_sin && op.rope_hd >= 16 && op.rope_hd % 16 == 0 &&
                                          op.rope_grp >= 1 && op.rope_rpad % 64 == 0),
                  "RoPE epilogue needs fragment-major 16-row store tiles and its tables");
+  MLCV_REQUIRE(mg == 1 || ((mg == 2 || mg == 4) && op.frag && op.tr == 16 && norm != 1 && op.nseg <= 3),
+               "skinny GEMM m groups (2 or 4) need fragment-major 16-row tiles");
   if (!direct && nc > 4 && (long)grid.x * grid.y * grid.z > 256) nc = 4;  // keep 2 workgroups per CU (LDS)
   MLCV_REQUIRE(op.pf.nreg >= 0 && op.pf.nreg <= PF_MAX_REGIONS, "prefetch regions");
   for (int i = 0; i < op.pf.nreg; ++i)

@@ -144,6 +144,10 @@ struct SkOp {
   int nseg, ntiles;
   int seg_tiles;         // > 0: every segment has this many tiles (direct table index)
   int tr;                // weight rows per tile: 16, 32 or 64 (GeGLU: half gate, half up)
+  int mg;                // m groups per 64-row block (0 or 1: none; 2 or 4: fragment-major
+                         // 16-row tiles, 4 / mg m tiles per workgroup, plus the shift row's
+                         // tile with pre-scaled input); the split-K workspace and counters
+                         // then cover ntiles * mblocks * mg
   int splitk, kper;
   float* ws;             // split-K partials
   const float* zero;     // >= 64*64 zero floats, never written (absent bias)

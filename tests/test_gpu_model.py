@@ -347,6 +347,31 @@ def test_multi_slab_tiles_bit_identical(kw, monkeypatch):
     np.testing.assert_array_equal(outs[1][1], outs[0][1])
 
 
+@pytest.mark.parametrize("kw", [dict(TINY_KWARGS, action_horizon=50), DUMMY_KWARGS], ids=["tiny_h50", "dummy"])
+def test_m_group_tiles_bit_identical(kw, monkeypatch):
+    """o_proj and down with their 16-row weight slabs shared out over 1, 2 or 4 workgroups
+    (each multiplying 4, 2 or 1 of the 64-row block's m tiles over the same K slices and k
+    groups): the step and the graph loop are bit-identical whatever the m groups."""
+    outs = []
+    for til in ("o=16:1:1,down=16:4:1", "o=16:1:2,down=16:4:2", "o=16:1:4,down=16:4:4", None):
+        if til:
+            monkeypatch.setenv("MLCV_TILING", til)
+        m = Model(kw)
+        if til:
+            monkeypatch.delenv("MLCV_TILING")
+        pm = make_prefix_mask_np(m.cfg.prefix_len)
+        cos, sin = make_rope_np(m.cfg.suffix_len, m.cfg.vlm.head_dim, m.cfg.rope_theta, offset=m.cfg.prefix_len)
+        te = make_time_embs(m.cfg.num_denoise_steps, m.cfg.action_expert.width)[2].astype(np.float16)
+        k, v = _prefill(m, pm)
+        step = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                              m.params).numpy()
+        outs.append((step, m.runner.sample_graph(m.params, m.prefix, noise=m.noise)))
+    assert np.all(np.isfinite(outs[0][0])) and np.all(np.isfinite(outs[0][1]))
+    for step, chunk in outs[1:]:
+        np.testing.assert_array_equal(step, outs[0][0])
+        np.testing.assert_array_equal(chunk, outs[0][1])
+
+
 def test_side_stream_modulations_bit_identical(tiny, monkeypatch):
     """The modulations as one launch over all 2 D + 1 norms (default) and as two pieces on
     a second stream (MLCV_FORK_MOD=1, layer 0 first) run the same tiles: the step and the
