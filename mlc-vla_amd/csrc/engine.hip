@@ -48,7 +48,9 @@ struct OpDesc {
 // whose waves load their operand fragments straight into registers; q/k/v, o_proj and
 // gate_up take the whole K per workgroup (no split-K exchange), down splits K in 4.
 // o_proj (64 weight slabs) shares each slab out over 4 workgroups of one m tile each, so
-// that it runs on 256 workgroups with a quarter of X each.
+// that it runs on 256 workgroups with a quarter of X each.  fp16 gate_up runs on 32-row tiles
+// (256 workgroups, X loaded once for both slabs: -11 us per step, bit-identical); q4f16_1
+// gate_up stays on 16-row tiles (32-row: +5 us).
 // Otherwise (M >= 64) the row-major kernels stage X through LDS with 16/32-row tiles.
 // Everything else uses 64-row tiles and the planner's split.
 struct Tiling {
@@ -81,8 +83,9 @@ constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 // overrides the tile rows (16, or 32 for o / gate_up / down), K slices and, for 16-row
 // tiles, the m groups (1, 2 or 4) of the fragment-major GEMMs (the time MLP's K slices apply
 // to its small-M tiles) for tuning (read at context creation; 0 = planner).
-LayerTilings read_tilings() {
+LayerTilings read_tilings(bool q4) {
   LayerTilings lt;
+  if (!q4) lt.gu = {32, 1};
   const char* e = std::getenv("MLCV_TILING");
   if (!e) return lt;
   std::string spec(e);
@@ -858,7 +861,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
     return -1;
   }
   Ctx& c = h->c;
-  c.tilings = read_tilings();
+  c.tilings = read_tilings(cfg->quant == MLCV_QUANT_Q4F16_1);
   c.cfg = *cfg;
   c.q4 = cfg->quant == MLCV_QUANT_Q4F16_1;
   c.W0 = cfg->vlm_width;

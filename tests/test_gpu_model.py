@@ -327,9 +327,10 @@ def test_q4_path_vs_oracle_and_vs_fp(tiny):
 def test_multi_slab_tiles_bit_identical(kw, monkeypatch):
     """32-row fragment-major tiles (every wave multiplies its X fragments by both 16-row
     weight slabs) split K over the same 4 waves and sum the k groups in the same order as
-    16-row tiles: with equal K slices the step and the graph loop are bit-identical."""
+    16-row tiles: with equal K slices the step and the graph loop are bit-identical (gate_up
+    defaults to 32-row tiles for fp16, so the variant runs it on 16)."""
     ref = Model(kw)
-    monkeypatch.setenv("MLCV_TILING", "o=32:2,gu=32:1,down=32:4")
+    monkeypatch.setenv("MLCV_TILING", "o=32:2,gu=16:1,down=32:4")
     alt = Model(kw)
     monkeypatch.delenv("MLCV_TILING")
     pm = make_prefix_mask_np(ref.cfg.prefix_len)
