@@ -503,6 +503,8 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
   in.cus = device_cus();
   static const bool m128 = !std::getenv("MLCV_TG_M128") || std::atoi(std::getenv("MLCV_TG_M128")) != 0;
   in.m128 = m128;  // tuning switch
+  static const bool n64m128 = !std::getenv("MLCV_TG_N64M128") || std::atoi(std::getenv("MLCV_TG_N64M128")) != 0;
+  in.n64m128 = n64m128;
   if (!tile_plan(in, p)) return false;
   p.ws = a.ws;
   p.sync = a.sync;
@@ -515,7 +517,13 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
   // 102 us, its split-K reduction spread over twice the waves; gate_up unchanged; 5 stages
   // (160 KB) were slower); 256 x 128: 3 stages of 64 k (144 KB); 256 x 64: 3 stages of 64 k
-  if (p.bm == 128) {
+  if (p.bm == 128 && p.bn == 64) {
+    // 128 x 64 over the whole K, 4 waves of 64 x 32, 4 stages (96 KB): the prefill's o_proj on
+    // 256 workgroups instead of 128 (prefill 5.25 vs 5.33 ms, results identical); q/k/v on
+    // 3-stage 128 x 64 tiles (two workgroups per CU for its 320 tiles) was slower than 128 x 128
+    if (a.epi == TG_RESIDUAL) big_gemm_kernel<64, 64, 4, TG_RESIDUAL, false, 4, 128><<<blocks, 256, 0, st>>>(a, p);
+    else big_gemm_kernel<64, 64, 4, TG_STORE, false, 4, 128><<<blocks, 256, 0, st>>>(a, p);
+  } else if (p.bm == 128) {
     // 128 x 128 over the whole K: 4 stages of 64 k (128 KB), 8 waves of 64 x 32 (the prefill's
     // q/k/v 21.2 and o_proj 23.2 us against 256 x 64 tiles' 27 and 29 us; 8 waves against 4:
     // prefill -12 us)

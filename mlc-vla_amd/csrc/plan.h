@@ -81,6 +81,7 @@ struct TilePlanIn {
   int sync_tiles;  // tiles with meeting counters
   int cus;         // compute units of the device
   bool m128 = true;  // 128 x 128 tiles allowed (tuning switch)
+  bool n64m128 = true;  // 128 x 64 tiles where 128 x 128 ones fill at most half the CUs (tuning switch)
 };
 
 struct TilePlan {
@@ -109,14 +110,15 @@ inline bool tile_plan(const TilePlanIn& a, TilePlan& p) {
     if ((a.n1 % 8 != 0 && a.n1 != a.N) || (a.n2 % 8 != 0 && a.n2 != a.N)) return false;
     // long K (down_proj): 256 x 256 tiles over up to 8 K slices load a third less through
     // L2 than 256 x 128 tiles over 4.  Shorter K, over the whole K, when the tiles give at
-    // least half a workgroup per CU: 128 x 128 (the prefill's q/k/v and o_proj at P = 968),
-    // else 256 x 64; else 256 x 128.
+    // least half a workgroup per CU: 128 x 128 (the prefill's q/k/v at P = 968), or 128 x 64
+    // where 128 x 128 would leave half the CUs idle (o_proj: 256 tiles instead of 128); else
+    // 256 x 64; else 256 x 128.
     const int mt = (a.M + TG_BM - 1) / TG_BM, mt2 = (a.M + 127) / 128;
     if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N)) {
       p.bn = 256;
     } else if (a.K < 8192 && a.m128 && 2 * mt2 * ((a.N + 127) / 128) >= a.cus && a.cus > 0) {
       p.bm = 128;
-      p.bn = 128;
+      p.bn = a.n64m128 && mt2 * ((a.N + 127) / 128) <= a.cus / 2 ? 64 : 128;
     } else if (a.K < 8192 && 2 * mt * ((a.N + 63) / 64) >= a.cus && a.cus > 0) {
       p.bn = 64;
     } else {

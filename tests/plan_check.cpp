@@ -111,7 +111,7 @@ static void check_tile() {
               }
               ++checked;
               const int tiles = p.mtiles * p.ntiles, kts = (K + TG_BK - 1) / TG_BK;
-              CHECK(p.bm == TG_BM || (p.bm == 128 && p.bn == 128 && p.splitk == 1 && !geglu), "m tile %d", p.bm);
+              CHECK(p.bm == TG_BM || (p.bm == 128 && (p.bn == 128 || p.bn == 64) && p.splitk == 1 && !geglu), "m tile %d", p.bm);
               CHECK((long)p.mtiles * p.bm >= M && (long)(p.mtiles - 1) * p.bm < M, "m tiles %d for M %d", p.mtiles, M);
               const long ncover = geglu ? (long)p.ntiles * (p.bn / 2) : (long)p.ntiles * p.bn;
               CHECK(ncover >= N, "n tiles %d x %d for N %d", p.ntiles, p.bn, N);

@@ -82,7 +82,9 @@ TILE_SHAPES = [(968, 2048, 2560, 0), (968, 2048, 2048, 1), (968, 2048, 16384, 2)
                # K not a multiple of 64 (SigLIP fc2 and patch embedding, a ragged case)
                (256, 4304, 1152, 1), (256, 592, 1152, 0), (77, 200, 260, 1), (300, 136, 256, 2),
                # enough 256 x 64 tiles for the whole-K narrow plan, with N and K tails
-               (4096, 1024, 1156, 0), (2000, 200, 1028, 1)]
+               (4096, 1024, 1156, 0), (2000, 200, 1028, 1),
+               # 128 x 64 tiles (128 x 128 ones would fill half the CUs), with N and K tails
+               (1000, 1000, 2040, 0)]
 
 
 @pytest.mark.parametrize("m,k,n,epi", TILE_SHAPES)
