@@ -96,11 +96,12 @@ __device__ __forceinline__ void store_dev(__amdgpu_buffer_rsrc_t r, int byte_off
   else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, byte_off, 0, AUX);
 }
 // cache policy of the streamed operands (measured on the step at P=968, T=50):
-// prefix / suffix keys and values: device scope, 4 us per step faster than plain loads;
+// prefix keys and values (written by an earlier launch): plain loads, 9 us per step and
+// 40 us per prefill faster than device-scope ones on the current kernels;
 // weights (layer GEMMs, and the row-major time-MLP / modulation GEMVs): non-temporal (2),
-// 15 us per step faster with a cold memory-side cache, 9-25 us with a warm one
+// 54 us per step faster than plain loads on the current kernels
 #ifndef MLCV_KV_AUX
-#define MLCV_KV_AUX 16
+#define MLCV_KV_AUX 0
 #endif
 #ifndef MLCV_W_AUX
 #define MLCV_W_AUX 2
@@ -108,7 +109,12 @@ __device__ __forceinline__ void store_dev(__amdgpu_buffer_rsrc_t r, int byte_off
 #ifndef MLCV_WROW_AUX
 #define MLCV_WROW_AUX 2
 #endif
-constexpr int KV_AUX = MLCV_KV_AUX, W_AUX = MLCV_W_AUX, WROW_AUX = MLCV_WROW_AUX;
+// the fragment-major activations of the layer GEMMs (the previous launch's output): device
+// scope; plain loads measure the same on the current kernels (812.0 vs 812.1 us per step)
+#ifndef MLCV_X_AUX
+#define MLCV_X_AUX 16
+#endif
+constexpr int KV_AUX = MLCV_KV_AUX, W_AUX = MLCV_W_AUX, WROW_AUX = MLCV_WROW_AUX, X_AUX = MLCV_X_AUX;
 
 // fp16 <-> fp32 with IEEE round-to-nearest-even (v_cvt_f16_f32 / v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }

@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
           for (int mt = 0; mt < PMT; ++mt) {
             const int gmt = mt < XMT ? XMT * mgi + mt : op.M >> 4;  // 64-row block's m tile
-            xf[c][j][mt] = load_dev<h8>(xr, ((ks * 4 + gmt) * 64 + piece) * 16);
+            xf[c][j][mt] = load_dev<h8, X_AUX>(xr, ((ks * 4 + gmt) * 64 + piece) * 16);
           }
         } else {
           const int kx = min(kcs + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g), K - 8);
