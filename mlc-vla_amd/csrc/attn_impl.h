@@ -37,6 +37,13 @@
 #define MLCV_ATTN_Q_AUX 16
 #endif
 constexpr int ATTN_Q_AUX = MLCV_ATTN_Q_AUX;
+// cache policy of the split combine's partial loads when the attention wrote them in an
+// earlier launch (the persistent step's combine, in the same launch, reads at device scope):
+// device scope; plain loads measure the same on the current kernels (813.0 vs 813.1 us)
+#ifndef MLCV_COMB_AUX
+#define MLCV_COMB_AUX 16
+#endif
+constexpr int COMB_AUX = MLCV_COMB_AUX;
 
 // timeline stamps of the trace build of the persistent step (empty otherwise)
 #ifndef ATTN_STAMP
@@ -398,13 +405,13 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
   // the partials were written by the attention kernel just before: device-scope loads
   const uint32_t nrow = (uint32_t)a.KV * ns * a.rpad;
   const __amdgpu_buffer_rsrc_t rml = dev_rsrc(a.part_ml, nrow * 8), ro = dev_rsrc(a.part_o, nrow * hd * 2);
-  const float m_l = load_dev<float>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8));
-  const float l_l = load_dev<float>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8 + 4));
+  const float m_l = load_dev<float, COH ? 16 : COMB_AUX>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8));
+  const float l_l = load_dev<float, COH ? 16 : COMB_AUX>(rml, (int)((pr0 + (size_t)sl * a.rpad) * 8 + 4));
   // the O loads of the first 256 dims go out with the m / l loads (partials: fp16 O_s / l_s)
   const int d0 = min(lane * 4, hd - 4);
   h4 o[MAXS];
 #pragma unroll
-  for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0) * 2));
+  for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4, COH ? 16 : COMB_AUX>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + d0) * 2));
   // out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s with w_s = exp(m_s - max)
   // max and sum over the splits: butterflies within groups of P >= MAXS lanes (the first
   // group holds every split; the other groups' results are never read)
@@ -425,7 +432,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
     if (db > 0) {  // head dims past 256
       const int dc = min(d, hd - 4);
 #pragma unroll
-      for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + dc) * 2));
+      for (int s = 0; s < MAXS; ++s) o[s] = load_dev<h4, COH ? 16 : COMB_AUX>(ro, (int)(((pr0 + (size_t)min(s, ns - 1) * a.rpad) * hd + dc) * 2));
     }
     f4 acc = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
