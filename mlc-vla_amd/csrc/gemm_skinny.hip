@@ -268,6 +268,16 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[sl][i] = (f4){0.f, 0.f, 0.f, 0.f};
   const int lkg = MSD ? w : kg;  // this wave's k group in the product
+  // chunk of a round taken by k group q as its c-th: rounds of up to 8 chunks give each k group
+  // a run of LCPW; a 16-chunk round is two 8-chunk rounds in one, so that every wave sums the
+  // same k ranges in the same order as with NC = 8 (bit-identical results)
+  auto chunk_of = [&](int q, int c) __attribute__((always_inline)) -> int {
+    if constexpr (NC <= 8) return q * LCPW + c;
+    else {
+      constexpr int CPV = 8 / LKG;  // chunks per k group in each 8-chunk half
+      return (c / CPV) * 8 + q * CPV + c % CPV;
+    }
+  };
 
   // one round: rounds after the first run in a loop, the first is peeled so that the
   // prefetched loads above stay in flight (a loop header would wait for all of them)
@@ -290,7 +300,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int c = 0; c < LCPW; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int kcs = kr + (lkg * LCPW + c) * KC;
+        const int kcs = kr + chunk_of(lkg, c) * KC;
         if constexpr (XM == 1) {
           const int ks = min((kcs >> 5) + (Q4 ? g : j), KS - 1);
           const int piece = Q4 ? 16 * j + r16 : lane;
@@ -309,7 +319,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int sl = 0; sl < SW; ++sl)
 #pragma unroll
       for (int c = 0; c < LCPW; ++c) {
-        const int kcs = kr + (lkg * LCPW + c) * KC;
+        const int kcs = kr + chunk_of(lkg, c) * KC;
         const size_t wsl = (size_t)SLABS * lt + sl;  // 16-row slab of the shuffled weights
         if constexpr (!Q4) {
           const __amdgpu_buffer_rsrc_t rw = dev_rsrc(seg.w + wsl * KS * 512, (uint32_t)KS * 1024);
@@ -331,7 +341,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
       for (int j = 0; j < 4; ++j) {
         // k past the slice: the weight fragment is zeroed (X there is finite data of the
         // same rows, so the products vanish)
-        const bool kok = kr + (lkg * LCPW + c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g) < kend;
+        const bool kok = kr + chunk_of(lkg, c) * KC + (Q4 ? 32 * g + 8 * j : 32 * j + 8 * g) < kend;
         h8 a[SW];
 #pragma unroll
         for (int sl = 0; sl < SW; ++sl) {
@@ -791,6 +801,10 @@ int launch_nc_mg(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
       if constexpr (KG <= 2) skinny_kernel<Q4, NORM, EPI, 2, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op);
       break;
     case 4: skinny_kernel<Q4, NORM, EPI, 4, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op); break;
+    case 16:  // one m tile per wave (4 m groups): a K slice of 2048 in one round of loads
+      if constexpr (MG == 4 && NORM == 0) skinny_kernel<Q4, NORM, EPI, 16, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op);
+      else skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op);
+      break;
     default: skinny_kernel<Q4, NORM, EPI, 8, TABLE, TR, XM, MG><<<grid, 256, 0, st>>>(op); break;
   }
   return 0;
@@ -891,6 +905,8 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   const int norm = op.prescaled ? 2 : (op.scale != nullptr ? 1 : 0);
   const int cps = op.kper / KC;
   int nc = cps >= 5 ? 8 : cps >= 3 ? 4 : cps;
+  static const bool nc16 = !std::getenv("MLCV_SK_NC16") || std::atoi(std::getenv("MLCV_SK_NC16")) != 0;
+  if (nc16 && cps >= 16 && op.mg == 4 && op.frag && norm == 0) nc = 16;
   const bool direct = op.frag || op.xrow;  // operands straight into registers, little LDS
   MLCV_REQUIRE(!(op.frag && op.xrow), "fragment-major and row-major X at once");
   MLCV_REQUIRE(!direct || op.tr == 16 || (op.frag && op.tr == 32),

@@ -18,6 +18,7 @@ from conftest import DUMMY_KWARGS, TINY_KWARGS, cosine, max_abs
 from mlc_vla import runtime
 from mlc_vla.compile_quant import compile_model_quant, quantize_params
 from mlc_vla.model.pi0 import Pi0Config
+from mlc_vla.model.pi0.pi0_config import GemmaExpertConfig
 from mlc_vla.sample import PiZeroRunner, make_prefix_mask_np, make_rope_np, make_time_embs
 from oracle import m0_torch
 from oracle import pi0_oracle as O
@@ -348,11 +349,19 @@ def test_multi_slab_tiles_bit_identical(kw, monkeypatch):
     np.testing.assert_array_equal(outs[1][1], outs[0][1])
 
 
-@pytest.mark.parametrize("kw", [dict(TINY_KWARGS, action_horizon=50), DUMMY_KWARGS], ids=["tiny_h50", "dummy"])
+# one layer with 8 heads of 256: o_proj has K = 2048, which 4 m groups take in one round of
+# 16 chunks (two rounds of 8 otherwise)
+_WIDE = GemmaExpertConfig(width=256, depth=1, mlp_dim=512, num_heads=8, num_kv_heads=1, head_dim=256)
+WIDE_HEADS_KWARGS = dict(TINY_KWARGS, paligemma_variant=_WIDE, action_expert_variant=_WIDE, action_horizon=50)
+
+
+@pytest.mark.parametrize("kw", [dict(TINY_KWARGS, action_horizon=50), DUMMY_KWARGS, WIDE_HEADS_KWARGS],
+                         ids=["tiny_h50", "dummy", "wide_heads"])
 def test_m_group_tiles_bit_identical(kw, monkeypatch):
     """o_proj and down with their 16-row weight slabs shared out over 1, 2 or 4 workgroups
     (each multiplying 4, 2 or 1 of the 64-row block's m tiles over the same K slices and k
-    groups): the step and the graph loop are bit-identical whatever the m groups."""
+    groups; with 4 groups a K of 2048 runs as one 16-chunk round laid out as two 8-chunk ones):
+    the step and the graph loop are bit-identical whatever the m groups."""
     outs = []
     for til in ("o=16:1:1,down=16:4:1", "o=16:1:2,down=16:4:2", "o=16:1:4,down=16:4:4", None):
         if til:
