@@ -21,6 +21,16 @@ namespace {
 template <int HD, bool KF32, bool ROPE, bool IMG, bool QF, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds_raw[2 * attn_buf_bytes<HD, IMG>()];
+  if (a.xgroup) {  // XCD-grouped order: column x of the grid runs on XCD x
+    const int x = blockIdx.x, j = blockIdx.y, rbs = (a.rows + ROWS - 1) / ROWS;
+    const int nt = (a.nsplit - x + 7) / 8 * rbs;  // tasks of splits x, x + 8, ...
+    if (j < nt) {
+      attn_block<HD, KF32, ROPE, IMG, QF, false, NW>(a, j % rbs, x + 8 * (j / rbs), blockIdx.z, lds_raw, threadIdx.x);
+    } else if (j < nt + a.pf.nblocks / 8 && blockIdx.z == 0) {
+      prefetch_ranked(a.pf, x, j - nt, a.pf.nblocks / 8);
+    }
+    return;
+  }
   if (blockIdx.y >= a.nsplit) {  // prefetch workgroups (grid rows past the key splits)
     if (blockIdx.z == 0) prefetch_run(a.pf, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * a.nsplit);
     return;
@@ -349,6 +359,12 @@ int attn_launch(const AttnArgs& a, hipStream_t st) {
   const int pf_rows = a.pf.nreg > 0 && a.pf.nblocks > 0 ? (a.pf.nblocks + rb - 1) / rb : 0;
   ka.pf.nblocks = pf_rows * rb;
   dim3 grid(rb, a.nsplit + pf_rows, a.KV);
+  if (a.xgroup) {
+    MLCV_REQUIRE(a.qf && !a.kimg, "XCD-grouped order: the 8-wave q-fragment form");
+    const int pfx = a.pf.nreg > 0 && a.pf.nblocks > 0 ? (a.pf.nblocks + 7) / 8 : 0;  // per XCD
+    ka.pf.nblocks = 8 * pfx;
+    grid = dim3(8, (a.nsplit + 7) / 8 * rb + pfx, a.KV);
+  }
 // the step's form (q fragments, converted chunks) runs on 8 waves (attn_block): 868 vs 871 us
 // per step; the others on 4 (the prefill's form spills at 8 waves: +20 us per prefill)
 #define MLCV_ATTN_CASE(HDV)                                                                        \

@@ -206,6 +206,10 @@ struct Ctx {
   bool loop_img = false;
   size_t attn_ws_floats_n = 0;
   int st_nsplit = 1, st_kps = 32, pf_nsplit = 1, pf_kps = 32;
+  // the step attention in the XCD-grouped order: with plain K/V loads the 7 row blocks of a key
+  // split share its K/V in one XCD's L2 (step 808 vs 821 us); MLCV_ATTN_XG=0 deals the tasks
+  // over the XCDs in grid order instead
+  bool attn_xg = true;
 
   SkSeg* d_segs = nullptr;
   std::vector<SkSeg> h_segs;
@@ -487,6 +491,7 @@ int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipSt
   pf_weights(c, a.pf, c.layer_ops[4 * L + 3], PF_ATTN_DOWN);
   if (L + 1 < c.D) pf_weights(c, a.pf, c.layer_ops[4 * (L + 1)], PF_ATTN_QKV);
   if (L + 1 < c.D) pf_kv(c, a.pf, L + 1, keys, values, PF_ATTN_KV, 0);
+  a.xgroup = c.attn_xg && a.qf && !a.kimg ? 1 : 0;
   return attn_launch(a, st);
 }
 
@@ -1114,6 +1119,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // off unless MLCV_FORK_MOD=1 (tuning)
   c.fork_mod = std::getenv("MLCV_FORK_MOD") != nullptr && std::atoi(std::getenv("MLCV_FORK_MOD")) != 0;
   if (const char* e = std::getenv("MLCV_LOOP_IMG")) c.loop_img = std::atoi(e) != 0;
+  if (const char* e = std::getenv("MLCV_ATTN_XG")) c.attn_xg = std::atoi(e) != 0;
   if (const char* e = std::getenv("MLCV_PREFILL_SMALL_TILES")) c.gemm_small = std::atoi(e) != 0;
   if (const char* e = std::getenv("MLCV_PREFETCH")) c.prefetch = (unsigned)std::strtoul(e, nullptr, 0);
   if (const char* e = std::getenv("MLCV_PF_BLOCKS")) c.pf_blocks = std::max(8, std::atoi(e));

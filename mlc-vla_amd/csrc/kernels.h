@@ -33,12 +33,9 @@ struct Prefetch {
 // In a prefetch workgroup: `lin` = its linear workgroup id, `lin0` = the linear id of the
 // launch's first prefetch workgroup.  The lines of the slabs this XCD reads are spread
 // over the XCD's prefetch workgroups, 16 loads in flight per lane (any workgroup size).
-__device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
-  const int xcd = lin & 7;
-  const int p = lin - lin0;
-  const int p0 = (xcd - lin0) & 7;  // the first prefetch workgroup on this XCD
-  const int rank = (p - p0) >> 3;
-  const int nrank = (pf.nblocks - p0 + 7) >> 3;
+// prefetch_ranked: the workgroup of rank `rank` among the `nrank` prefetch workgroups of XCD
+// `xcd`.
+__device__ inline void prefetch_ranked(const Prefetch& pf, int xcd, int rank, int nrank) {
   const int tid = threadIdx.x, nt = blockDim.x;
   unsigned acc = 0;
   for (int ri = 0; ri < pf.nreg; ++ri) {
@@ -63,6 +60,12 @@ __device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
     }
   }
   if (pf.sink) pf.sink[tid] = acc;
+}
+__device__ inline void prefetch_run(const Prefetch& pf, int lin, int lin0) {
+  const int xcd = lin & 7;
+  const int p = lin - lin0;
+  const int p0 = (xcd - lin0) & 7;  // the first prefetch workgroup on this XCD
+  prefetch_ranked(pf, xcd, (p - p0) >> 3, (pf.nblocks - p0 + 7) >> 3);
 }
 
 // ---------------------------------------------------------------------------
@@ -212,6 +215,10 @@ struct AttnArgs {
   int nsplit, kps;       // splits (the last one is the suffix block when Ts > 0), prefix keys per split
   int rows, rpad;        // rows per kv head (Tq*H/KV) and padded
   Prefetch pf;           // prefetch workgroups appended as grid rows y >= nsplit
+  // XCD-grouped order (8-wave q-fragment form): grid (8, Y, KV), column x runs on XCD x and
+  // takes every row block of the splits x, x + 8, ..., then pf.nblocks / 8 prefetch
+  // workgroups, so a split's K/V is read into one XCD's L2 for all its row blocks
+  int xgroup;
 };
 // nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
 // prefix K (split hi/lo), V (transposed) and mask of `layers` consecutive layers (keys /

@@ -382,6 +382,29 @@ def test_m_group_tiles_bit_identical(kw, monkeypatch):
         np.testing.assert_array_equal(chunk, outs[0][1])
 
 
+@pytest.mark.parametrize("kw", [dict(TINY_KWARGS, action_horizon=50), WIDE_HEADS_KWARGS], ids=["tiny_h50", "wide_heads"])
+def test_attention_task_order_bit_identical(kw, monkeypatch):
+    """The step attention's workgroups in the XCD-grouped order (every row block of a key split
+    on one XCD) and in grid order run the same tasks: bit-identical steps and chunks."""
+    outs = []
+    for xg in ("0", None):
+        if xg:
+            monkeypatch.setenv("MLCV_ATTN_XG", xg)
+        m = Model(kw)
+        if xg:
+            monkeypatch.delenv("MLCV_ATTN_XG")
+        pm = make_prefix_mask_np(m.cfg.prefix_len)
+        cos, sin = make_rope_np(m.cfg.suffix_len, m.cfg.vlm.head_dim, m.cfg.rope_theta, offset=m.cfg.prefix_len)
+        te = make_time_embs(m.cfg.num_denoise_steps, m.cfg.action_expert.width)[4].astype(np.float16)
+        k, v = _prefill(m, pm)
+        step = m.runner.vm["denoise_step_kv"](k, v, m.dev(m.x_t), m.dev(te), m.dev(cos), m.dev(sin), m.dev(pm),
+                                              m.params).numpy()
+        outs.append((step, m.runner.sample_graph(m.params, m.prefix, noise=m.noise)))
+    assert np.all(np.isfinite(outs[0][0])) and np.all(np.isfinite(outs[0][1]))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1], outs[0][1])
+
+
 def test_side_stream_modulations_bit_identical(tiny, monkeypatch):
     """The modulations as one launch over all 2 D + 1 norms (default) and as two pieces on
     a second stream (MLCV_FORK_MOD=1, layer 0 first) run the same tiles: the step and the
