@@ -94,6 +94,19 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * before a waiting workgroup gives up; the outputs of that call are then invalid and the next
  * mlcv_sync on the context returns -4. */
 #define MLCV_OPT_MEET_POLLS 5
+/* MLCV_OPT_XTP (default 1 where it applies; env MLCV_XTP=0 turns it off): run the decoder
+ * layers of each step tensor-parallel over the GPU's 8 XCDs, two launches per layer (built for
+ * width 1024, MLP 4096, 8 query heads / 1 kv head of 256, T < 64, prefix + T <= 1024, fp16, on
+ * a part of 8 XCDs x 32 CUs; setting it elsewhere returns an error).  Its barrier waits are
+ * bounded by MLCV_OPT_PERSIST_SPIN polls; a wait that gives up makes the next mlcv_sync
+ * return -4.  MLCV_OPT_PERSIST = 1 turns it off, MLCV_OPT_XTP = 1 turns the persistent step off.
+ * Value 2 runs it without skipping the key chunks whose keys are all masked (testing: the skip
+ * is exact, the results are bit-identical). */
+#define MLCV_OPT_XTP 6
+/* MLCV_OPT_XTP_KEEP (default 0): the XCD step keeps every layer's intermediates for
+ * mlcv_step_probe (1) or reuses one set of buffers for all layers (0, faster; probes then
+ * return an error). */
+#define MLCV_OPT_XTP_KEEP 7
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 
 /* Synchronize `stream` and report a persistent step that ended early (a wait between its
@@ -115,7 +128,10 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream);
  *   MLCV_PROBE_X_MID  residual stream after the attention's gated residual [T][W1] f16
  *   MLCV_PROBE_H      GeGLU output [T][ae_mlp] f16
  *   MLCV_PROBE_MOD    adaRMS modulations [2 depth + 1][3 W1] f16 (layer 0)
- *   MLCV_PROBE_VOUT   the velocity of the last head [T][A] f32 (layer 0) */
+ *   MLCV_PROBE_VOUT   the velocity of the last head [T][A] f32 (layer 0)
+ *   MLCV_PROBE_XCD_X  the XCD step's copy of the residual stream on XCD `layer % 8` entering
+ *                     layer `layer / 8` [T][W1] f16 (every XCD keeps its own copy)
+ * The XCD step keeps every layer's intermediates too (XCD 0's copy of the residual stream). */
 #define MLCV_PROBE_X 0
 #define MLCV_PROBE_Q 1
 #define MLCV_PROBE_K 2
@@ -125,6 +141,7 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream);
 #define MLCV_PROBE_H 6
 #define MLCV_PROBE_MOD 7
 #define MLCV_PROBE_VOUT 8
+#define MLCV_PROBE_XCD_X 9
 int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream);
 
 /* prefill -- Pi0Model.prefill (pi0_model.py:128-140).

@@ -243,6 +243,12 @@ struct Ctx {
   bool pk_on = false;   // ... and it is enabled
   PkArgs pk{};          // buffers, dims and plan; weights filled at bind
   PkLin* d_pklin = nullptr;
+  // XCD tensor-parallel step (step_xtp.hip): two launches per layer for the pi0.5 action
+  // expert's shape on a part of 8 XCDs x 32 CUs; on by default where it applies (MLCV_XTP=0 or
+  // MLCV_OPT_XTP = 0 turns it off); activations are per layer and XCD
+  bool xt_ok = false;  // the shapes and the device allow it (decided at create)
+  bool xt_on = false;  // ... and it is enabled
+  XtArgs xt{};         // buffers and dims; weights filled at bind
   float* nscale = nullptr;  // [steps][2D+1] prescale of each norm's pre-scaled input
   _Float16* ain16 = nullptr;  // action_in weights in fp16 (q4 models: dequantized at bind)
 
@@ -322,7 +328,7 @@ int run_op(const Ctx& c, const OpDesc& d, SkOp op, hipStream_t st) { return sk_l
 int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool fork) {
   MLCV_TRY(run_op(c, c.op_tin, make_op(c, c.op_tin, te, c.W1, M), st));
   MLCV_TRY(run_op(c, c.op_tout, make_op(c, c.op_tout, c.tmp, c.W1, M), st));
-  if (c.pk_on) fork = false;  // the persistent step starts after every modulation
+  if (c.pk_on || c.xt_on) fork = false;  // the one-launch / XCD steps start after every modulation
   hipStream_t ms = st;
   if (fork) {
     MLCV_HIP(hipEventRecord(c.cond_ev, st));
@@ -331,7 +337,7 @@ int enqueue_time_mod(Ctx& c, const _Float16* te, int M, hipStream_t st, bool for
   }
   // with each piece of modulations, the power-of-two prescale of its norms' pre-scaled inputs
   // (piece 0: layer 0's two norms; piece 1: the others)
-  const bool nsc = c.prescaled || c.pk_on;
+  const bool nsc = c.prescaled || c.pk_on || c.xt_on;
   if (!fork && c.mod_all.nseg > 0) {
     MLCV_TRY(run_op(c, c.mod_all, make_op(c, c.mod_all, c.cond, c.W1, M), st));
     if (nsc) MLCV_TRY(nscale_launch(c.mod, c.W1, c.NM, M, 0, c.NM, c.nscale, st));
@@ -546,6 +552,26 @@ int enqueue_action_in(Ctx& c, const _Float16* modp, hipStream_t st) {  // action
 // forked: the modulation pieces run on the side stream (enqueue_time_mod with fork)
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
                  hipStream_t st, bool forked = false) {
+  if (c.xt_on) {
+    // the XCD tensor-parallel layers, then the launch chain's head on the residual stream
+    XtArgs a = c.xt;
+    const size_t mi = (size_t)(modp - c.mod) / ((size_t)3 * c.W1);  // first norm of this step
+    a.modp = modp;
+    a.nscale = c.nscale + mi;
+    a.keys = keys;
+    a.values = values;
+    a.mask = c.mask;
+    a.cos = c.cos;
+    a.sin = c.sin;
+    a.xin = c.xin16;
+    for (int L = 0; L < c.D; ++L) {
+      a.L = L;
+      MLCV_TRY(xt_attn_launch(a, st));
+      MLCV_TRY(xt_mlp_launch(a, st));
+    }
+    MLCV_TRY(xt_final_launch(a, st));
+    return enqueue_head(c, modp, euler, st);
+  }
   if (c.pk_on) {
     PkArgs p = c.pk;
     const size_t mi = (size_t)(modp - c.mod) / ((size_t)3 * c.W1);  // first norm of this step
@@ -1076,6 +1102,54 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
     }
   }
 
+  // XCD tensor-parallel step: the shape it is built for, on a part of 8 XCDs x 32 CUs
+  {
+    const char* e = std::getenv("MLCV_XTP");
+    c.xt_ok = !c.q4 && c.frag && xt_shape_ok(W1, c.F1, c.H, c.KV, hd, T, (int)P, c.A) && device_cus() == 256;
+    c.xt_on = c.xt_ok && !(e && std::atoi(e) == 0) && !c.pk_on;
+    if (c.xt_ok) {
+      XtArgs& x = c.xt;
+      x.D = c.D;
+      x.T = T;
+      x.P = (int)P;
+      x.A = c.A;
+      x.eps = cfg->rms_norm_eps;
+      x.spin = 1u << 22;
+      x.pf_next = 0;
+      if (const char* pe = std::getenv("MLCV_XT_PF")) x.pf_next = std::atoi(pe);
+      const size_t D8 = (size_t)c.D * 8, TW = (size_t)T * W1;
+      ALLOC(x.x, D8 * TW);
+      ALLOC(x.xm, D8 * TW);
+      ALLOC(x.qf, D8 * XT_QF);
+      ALLOC(x.k32, D8 * T * hd);
+      ALLOC(x.v, D8 * T * hd);
+      ALLOC(x.attn, D8 * 64 * hd);
+      ALLOC(x.h, D8 * 64 * (c.F1 / 8));
+      ALLOC(x.u, (size_t)8 * 64 * W1);
+      ALLOC(x.rss, (size_t)8 * T * (W1 / 16));
+      ALLOC(x.ap, (size_t)8 * 32 * 64 * hd);
+      ALLOC(x.aml, (size_t)8 * 32 * 64 * 2);
+      ALLOC(x.opart, (size_t)8 * 32 * T * 32);
+      ALLOC(x.dpart, (size_t)8 * 32 * T * 32);
+      ALLOC(x.flags, (size_t)8 * 32);
+      ALLOC(x.err, 1);
+      x.x16 = c.x16;
+      x.xu = c.xu;
+      x.rowss = c.rowss;
+      const std::pair<void*, size_t> zero_fill[] = {
+          {x.x, D8 * TW * 2}, {x.xm, D8 * TW * 2}, {x.qf, D8 * XT_QF * 2}, {x.k32, D8 * T * hd * 4},
+          {x.v, D8 * T * hd * 2}, {x.attn, D8 * 64 * hd * 2}, {x.h, D8 * 64 * (c.F1 / 8) * 2},
+          {x.u, (size_t)8 * 64 * W1 * 2}, {x.rss, (size_t)8 * T * (W1 / 16) * 4}, {x.ap, (size_t)8 * 32 * 64 * hd * 2},
+          {x.aml, (size_t)8 * 32 * 64 * 2 * 4}, {x.opart, (size_t)8 * 32 * T * 32 * 4},
+          {x.dpart, (size_t)8 * 32 * T * 32 * 4}, {x.flags, (size_t)8 * 32 * 4}, {x.err, 4}};
+      for (const auto& z : zero_fill)
+        if (hipMemset(z.first, 0, z.second) != hipSuccess) {
+          set_error("XCD step buffers: memset failed");
+          return fail(-1);
+        }
+    }
+  }
+
   // skinny-GEMM op descriptions (segments are filled at bind time; shapes now)
   const int mb_t = (T + 63) / 64, mb_s = (c.NS + 63) / 64;
   struct Shape {
@@ -1171,9 +1245,19 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
   else if (key == MLCV_OPT_PERSIST) {
     MLCV_REQUIRE(value == 0 || c.pk_ok, "the persistent step is not built for this configuration");
     c.pk_on = value != 0;
+    if (c.pk_on) c.xt_on = false;
+  } else if (key == MLCV_OPT_XTP) {
+    MLCV_REQUIRE(value == 0 || c.xt_ok, "the XCD tensor-parallel step is not built for this configuration");
+    MLCV_REQUIRE(value >= 0 && value <= 2, "XCD step option: 0, 1 or 2");
+    c.xt_on = value != 0;
+    c.xt.noskip = value == 2 ? 1 : 0;
+    if (c.xt_on) c.pk_on = false;
+  } else if (key == MLCV_OPT_XTP_KEEP) {
+    c.xt.ls = value != 0 ? 1 : 0;
   } else if (key == MLCV_OPT_PERSIST_SPIN) {
     MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "spin limit");
     c.pk.spin = (unsigned)value;
+    c.xt.spin = (unsigned)value;
   } else if (key == MLCV_OPT_MEET_POLLS) {
     MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "meeting poll limit");
     c.meet_polls = (unsigned)value;
@@ -1357,7 +1441,7 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     c.op_aout.mg = c.frag ? tile_head(c).mg : 1;
     c.pk.aout = pkl(fa);
   }
-  if (c.pk_ok) {
+  if (c.pk_ok || c.xt_ok) {
     // action_in as fp16 rows (a q4 model's copy is dequantized once here)
     c.ain16 = const_cast<_Float16*>(c.ain.w);
     if (c.q4) {
@@ -1369,6 +1453,9 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     if (!c.d_pklin) MLCV_HIP(hipMalloc(&c.d_pklin, (size_t)c.D * PK_NLIN * sizeof(PkLin)));
     MLCV_HIP(hipMemcpy(c.d_pklin, pklin.data(), pklin.size() * sizeof(PkLin), hipMemcpyHostToDevice));
     c.pk.lw = c.d_pklin;
+    c.xt.lw = c.d_pklin;
+    c.xt.ain_w = c.ain16;
+    c.xt.ain_b = c.ain.b;
   }
 
   if (c.d_segs) {
@@ -1509,6 +1596,19 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
               "successful sync are invalid");
     return -4;
   }
+  if (c.xt_ok) {
+    unsigned xerr = 0;
+    MLCV_HIP(hipMemcpy(&xerr, c.xt.err, 4, hipMemcpyDeviceToHost));
+    if (xerr != 0) {
+      // the barrier words are no longer equal after an abandoned launch: start over
+      MLCV_HIP(hipMemset(c.xt.flags, 0, (size_t)8 * 32 * 4));
+      MLCV_HIP(hipMemset(c.xt.err, 0, 4));
+      MLCV_HIP(hipDeviceSynchronize());
+      set_error("XCD step: a barrier wait gave up (error word " + std::to_string(xerr) +
+                "); the outputs of the calls since the last successful sync are invalid");
+      return -4;
+    }
+  }
   if (!c.pk_ok) return 0;
   unsigned err = 0;
   MLCV_HIP(hipMemcpy(&err, c.pk.err, 4, hipMemcpyDeviceToHost));
@@ -1529,14 +1629,19 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
 int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream) {
   MLCV_REQUIRE(ctx && out, "null argument");
   Ctx& c = ctx->c;
-  // the persistent step keeps every layer's intermediates; the launch chain reuses one set of
-  // buffers, which hold the outputs of the last operation run (layer 0 names them)
-  const bool chain = !c.pk_on;
+  // the persistent and XCD steps keep every layer's intermediates; the launch chain reuses one
+  // set of buffers, which hold the outputs of the last operation run (layer 0 names them)
+  const bool xt = c.xt_on;
+  const bool chain = !c.pk_on && !xt;
   MLCV_REQUIRE(!chain || c.frag, "probes of the launch chain need its fragment-major form (T < 64)");
   const PkArgs& p = c.pk;
   const int T = c.T, W1 = c.W1, nq = c.H * c.HD, nkv = c.KV * c.HD;
-  const int last = chain ? 0 : what == MLCV_PROBE_X ? c.D : c.D - 1;
+  const int last = what == MLCV_PROBE_XCD_X ? 8 * c.D - 1 : chain ? 0 : what == MLCV_PROBE_X ? c.D : c.D - 1;
   MLCV_REQUIRE(layer >= 0 && layer <= last, "probe layer out of range");
+  MLCV_REQUIRE(what != MLCV_PROBE_XCD_X || xt, "the per-XCD copies exist only in the XCD step");
+  MLCV_REQUIRE(!xt || c.xt.ls == 1 || what == MLCV_PROBE_VOUT || what == MLCV_PROBE_MOD ||
+                   (what == MLCV_PROBE_X && layer == c.D),
+               "the XCD step keeps per-layer intermediates only with MLCV_OPT_XTP_KEEP = 1");
   MLCV_TRY(mlcv_sync(ctx, stream));
   auto fetch = [&](const void* src, size_t n, std::vector<char>& h) -> int {
     h.resize(n);
@@ -1555,10 +1660,59 @@ int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_
     return 0;
   };
   const size_t qf_halfs = (size_t)c.KV * c.attn_rpad * ((c.HD + 31) / 32) * 64;
+  if (xt && what != MLCV_PROBE_VOUT && what != MLCV_PROBE_MOD && !(what == MLCV_PROBE_X && layer == c.D)) {
+    // XCD 0's copy of the residual stream; head / MLP-column blocks gathered from the 8 XCDs
+    const XtArgs& x = c.xt;
+    const size_t TW = (size_t)T * W1, hd = (size_t)c.HD, FX = (size_t)c.F1 / 8;
+    auto gather_frag = [&](const _Float16* base, size_t per, int K, int ld) -> int {  // 8 x [64][K] -> [T][8K]
+      MLCV_REQUIRE(bytes == (size_t)T * ld * 2, "probe output size");
+      MLCV_TRY(fetch(base, 8 * per * 2, raw));
+      const _Float16* f = reinterpret_cast<const _Float16*>(raw.data());
+      _Float16* o = static_cast<_Float16*>(out);
+      for (int xc = 0; xc < 8; ++xc)
+        for (int m = 0; m < T; ++m)
+          for (int k = 0; k < K; ++k) o[(size_t)m * ld + xc * K + k] = f[xc * per + xf_index(m, k)];
+      return 0;
+    };
+    switch (what) {
+      case MLCV_PROBE_X:
+      case MLCV_PROBE_X_MID:
+        MLCV_REQUIRE(bytes == TW * 2, "probe output size");
+        MLCV_HIP(hipMemcpy(out, (what == MLCV_PROBE_X ? x.x : x.xm) + L * 8 * TW, bytes, hipMemcpyDeviceToHost));
+        return 0;
+      case MLCV_PROBE_XCD_X:  // layer = 8 L + XCD
+        MLCV_REQUIRE(bytes == TW * 2, "probe output size");
+        MLCV_HIP(hipMemcpy(out, x.x + L * TW, bytes, hipMemcpyDeviceToHost));
+        return 0;
+      case MLCV_PROBE_K:
+        MLCV_REQUIRE(bytes == (size_t)T * nkv * 4, "probe output size");
+        MLCV_HIP(hipMemcpy(out, x.k32 + L * 8 * T * hd, bytes, hipMemcpyDeviceToHost));
+        return 0;
+      case MLCV_PROBE_V:
+        MLCV_REQUIRE(bytes == (size_t)T * nkv * 2, "probe output size");
+        MLCV_HIP(hipMemcpy(out, x.v + L * 8 * T * hd, bytes, hipMemcpyDeviceToHost));
+        return 0;
+      case MLCV_PROBE_ATTN: return gather_frag(x.attn + L * 8 * 64 * hd, 64 * hd, (int)hd, nq);
+      case MLCV_PROBE_H: return gather_frag(x.h + L * 8 * 64 * FX, 64 * FX, (int)FX, c.F1);
+      case MLCV_PROBE_Q: {  // hi + lo of each XCD's head -> [T][H*hd] f32
+        MLCV_REQUIRE(bytes == (size_t)T * nq * 4, "probe output size");
+        MLCV_TRY(fetch(x.qf + L * 8 * XT_QF, (size_t)8 * XT_QF * 2, raw));
+        const _Float16* f = reinterpret_cast<const _Float16*>(raw.data());
+        float* o = static_cast<float*>(out);
+        for (int hh = 0; hh < 8; ++hh)
+          for (int t = 0; t < T; ++t)
+            for (int d = 0; d < c.HD; ++d)
+              o[(size_t)t * nq + hh * c.HD + d] = (float)f[hh * XT_QF + attn_qf_index(0, 4, c.HD / 32, t, d, 0)] +
+                                                  (float)f[hh * XT_QF + attn_qf_index(0, 4, c.HD / 32, t, d, 1)];
+        return 0;
+      }
+      default: MLCV_REQUIRE(false, "unknown probe");
+    }
+  }
   switch (what) {
     case MLCV_PROBE_X:
       MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");
-      MLCV_HIP(hipMemcpy(out, chain ? c.x16 : p.xres + L * p.s_x, bytes, hipMemcpyDeviceToHost));
+      MLCV_HIP(hipMemcpy(out, chain || xt ? c.x16 : p.xres + L * p.s_x, bytes, hipMemcpyDeviceToHost));
       return 0;
     case MLCV_PROBE_X_MID:
       MLCV_REQUIRE(bytes == (size_t)T * W1 * 2, "probe output size");

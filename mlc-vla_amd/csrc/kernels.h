@@ -375,6 +375,69 @@ int pk_launch(const PkArgs& p, bool q4, hipStream_t st);
 // head dims the persistent step is built for
 bool pk_head_dim_ok(int hd);
 
+// ---------------------------------------------------------------------------
+// XCD tensor-parallel step (step_xtp.hip): the decoder layers of one denoise_step_kv as two
+// launches per layer of one workgroup per CU, tensor-parallel over the 8 XCDs.  XCD x owns
+// query head x (its q rows, its attention, its 256 columns of o_proj's K) and MLP columns
+// [512 x, 512 x + 512) (gate_up rows, down's K); each XCD computes the shared k / v itself.
+// Inside a launch the 32 workgroups of an XCD meet at barriers in that XCD's L2; the two
+// cross-XCD sums per layer (o_proj's and down's partials) happen at the launch boundaries,
+// where every XCD adds the 8 partials of its own 32-column slice of the residual stream.
+// Shape it is built for: width 1024, MLP 4096, 8 query heads / 1 kv head of 256 dims,
+// T < 64 tokens, P + T <= 1024 keys, fp16 weights, 8 XCDs x 32 CUs.
+// ---------------------------------------------------------------------------
+struct XtArgs {
+  const PkLin* lw;         // [D][PK_NLIN] fragment-major weights (wf_shuffle_launch copies)
+  const _Float16* ain_w;   // action_in, row-major [W1][A]
+  const _Float16* ain_b;   // [W1] or null
+  const _Float16* modp;    // [2D+1][3 W1] adaRMS (scale | shift | gate) of this step
+  const float* nscale;     // [2D+1] power-of-two prescale of each norm's pre-scaled input
+  const float* keys;       // prefix K [D][P][HD] f32 (roped)
+  const _Float16* values;  // prefix V [D][P][HD]
+  const float* mask;       // [P] additive
+  const float* cos;        // suffix RoPE [T][HD/2]
+  const float* sin;
+  const _Float16* xin;     // x_t [T][A] fp16
+  // per layer and XCD (XCD 0's copies are probed); with ls == 0 every layer reuses layer 0's set
+  // (its pages and lines stay warm: 0.7 us per launch faster), with ls == 1 each keeps its own
+  _Float16* x;      // [D][8][T][W1]  residual stream entering layer L
+  _Float16* xm;     // [D][8][T][W1]  after the attention's gated residual
+  _Float16* qf;     // [D][8][XT_QF]  q roped, scaled, fp16 hi/lo in the attention's fragment order
+  float* k32;       // [D][8][T][HD]  suffix k roped
+  _Float16* v;      // [D][8][T][HD]  suffix v
+  _Float16* attn;   // [D][8][64][HD] attention output of head x, fragment-major
+  _Float16* h;      // [D][8][64][512] GeGLU output of the XCD's MLP columns, fragment-major
+  // reused by every launch
+  _Float16* u;      // [8][64][W1] fragment-major pre-scaled adaRMS input, shift in row T
+  float* rss;       // [8][T][W1/16] row sums of squares of the residual stream per 16 columns
+  _Float16* ap;     // [8][32][64][HD] attention split partials O_s / l_s
+  float* aml;       // [8][32][64][2]  their (m, l)
+  float* opart;     // [8][32][T][32]  o_proj partials: [XCD][residual column slice][row][column]
+  float* dpart;     // [8][32][T][32]  down partials
+  unsigned* flags;  // [8][32] monotonic barrier words (all equal between launches)
+  unsigned* err;    // non-zero: a barrier wait gave up
+  unsigned spin;    // polls before a wait gives up
+  int D, T, P, A, L;
+  int ls;           // layer stride of the per-layer buffers (0 or 1)
+  int pf_next;      // the MLP launch prefetches the next layer's attention inputs: 0 no (default:
+                    // every placement measured slowed the stage it overlapped more than it saved),
+                    // 1 during down, 2 with the down weights
+  int noskip;       // 1: compute key chunks whose keys are all masked too (testing the skip)
+  float eps;
+  // the final reduce's outputs in the launch chain's layout (the head reads them)
+  _Float16* x16;    // [T][W1]
+  _Float16* xu;     // [64][W1] fragment-major, shift in row T
+  float* rowss;     // [T][W1/16]
+};
+constexpr int XT_QF = 4 * 8 * 2 * 512;  // halfs of one head's q fragments (64 rows, 256 dims)
+// the shape the XCD tensor-parallel step is built for
+bool xt_shape_ok(int W1, int F1, int H, int KV, int HD, int T, int P, int A);
+// layer L's attention half (reduce or action_in, q/k/v, attention, combine, o_proj) and MLP
+// half (reduce, gate_up, down); the final reduce into x16 / xu / rowss
+int xt_attn_launch(const XtArgs& a, hipStream_t st);
+int xt_mlp_launch(const XtArgs& a, hipStream_t st);
+int xt_final_launch(const XtArgs& a, hipStream_t st);
+
 // a batch of device-to-device copies in one launch (the entry points stage their inputs
 // into the context's buffers with one kernel instead of one copy launch per buffer)
 struct CopyJob {

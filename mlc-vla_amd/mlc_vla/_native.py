@@ -20,7 +20,9 @@ MLCV_OPT_HOIST_MODULATION = 2
 MLCV_OPT_PERSIST = 3
 MLCV_OPT_PERSIST_SPIN = 4
 MLCV_OPT_MEET_POLLS = 5
-PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7, "vout": 8}
+MLCV_OPT_XTP = 6
+MLCV_OPT_XTP_KEEP = 7
+PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7, "vout": 8, "xcd_x": 9}
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -194,7 +194,28 @@ class VirtualMachine:
         """Run each step as one persistent kernel (off by default; only for shapes it is built for)."""
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST, int(bool(on)))
 
+    def set_xtp(self, on: bool) -> None:
+        """Run the decoder layers tensor-parallel over the GPU's XCDs (on by default where the
+        shape and the device allow it; an error elsewhere)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_XTP, int(bool(on)))
+
+    def set_xtp_keep(self, on: bool) -> None:
+        """Keep every layer's intermediates of the XCD step for probes (testing; slower)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_XTP_KEEP, int(bool(on)))
+
+    def set_step_form(self, form: str) -> None:
+        """The execution of denoise_step_kv: "chain" (one launch per operation), "persistent"
+        (one launch per step) or "xtp" (two launches per layer over the XCDs)."""
+        if form not in ("chain", "persistent", "xtp"):
+            raise ValueError(f"unknown step form {form!r}")
+        if form == "xtp":
+            self.set_xtp(True)
+        else:
+            self.set_xtp(False)
+            self.set_persist(form == "persistent")
+
     def set_persist_spin(self, polls: int) -> None:
+        """Polls before a wait of the persistent or XCD step gives up."""
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST_SPIN, int(polls))
 
     def set_meet_polls(self, polls: int) -> None:

@@ -37,14 +37,18 @@ def is_ae(name: str) -> bool:
 
 
 class Step:
-    """One denoise_step_kv on the GPU with random-init weights and N(0,1) stand-in K/V (the
-    persistent step unless persist=False)."""
+    """One denoise_step_kv on the GPU with random-init weights and N(0,1) stand-in K/V, run in
+    the given form: "persistent" (one launch per step), "xtp" (two launches per layer over the
+    XCDs) or "chain" (one launch per operation)."""
 
-    def __init__(self, kw, seed=3, kv_seed=5, persist=True):
+    def __init__(self, kw, seed=3, kv_seed=5, form="persistent"):
         self.cfg = Pi0Config(**kw)
         self.d = O.dims_from_config(self.cfg)
         self.runner = PiZeroRunner(self.cfg, "rocm")
-        self.runner.vm.set_persist(persist)
+        self.form = form
+        self.runner.vm.set_step_form(form)
+        if form == "xtp":
+            self.runner.vm.set_xtp_keep(True)  # every layer's intermediates for the probes
         d = self.d
         g = torch.Generator(device="cuda").manual_seed(seed)
         specs = O.param_specs(d)

@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 def test_chain_ops_vs_oracle(which):
     kw = TINY_KWARGS if which == "tiny" else dict(dtype="float16", action_horizon=50)
     print(f"launch chain op by op: {which}", flush=True)
-    s = Step(kw, persist=False)
+    s = Step(kw, form="chain")
     v = s.run()
     r = ChainReplay(s)
     np.testing.assert_array_equal(r.probe("vout", 0).reshape(v.shape), v)

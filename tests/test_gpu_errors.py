@@ -82,7 +82,7 @@ def test_failed_bind_leaves_the_context_unbound():
     from stepcheck import Step
 
     print("bind failure: tiny model", flush=True)
-    s = Step(TINY_KWARGS, persist=False)
+    s = Step(TINY_KWARGS, form="chain")
     vm = s.runner.vm
     good = s.run()
     ptrs = list(vm._bound)  # the device pointers of the current binding

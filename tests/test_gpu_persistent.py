@@ -49,11 +49,11 @@ def test_persistent_step_matches_launch_chain(which, tiny_step, full_step):
     summation orders of the row statistics differ, so they agree to fp16 rounding)."""
     s = tiny_step if which == "tiny" else full_step
     a = s.run()
-    s.runner.vm.set_persist(False)
+    s.runner.vm.set_step_form("chain")
     try:
         b = s.run()
     finally:
-        s.runner.vm.set_persist(True)
+        s.runner.vm.set_step_form("persistent")
     assert np.all(np.isfinite(a)) and np.all(np.isfinite(b))
     assert cosine(a, b) >= 0.99999 and max_abs(a, b) <= 5e-3, (cosine(a, b), max_abs(a, b))
 
