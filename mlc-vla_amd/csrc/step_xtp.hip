@@ -274,6 +274,21 @@ __device__ __forceinline__ float xt_rinv(const char* den, int m, float eps, floa
 // o_proj / down), or (action_in) x = fp16(fp16(x_t W^T) + b); then the row sums of squares per
 // 16 columns and the next adaRMS's pre-scaled input fp16(x (1 + scale) c), its shift in row T.
 // Compute thread = (row m, 8 columns).
+// The cross-XCD partials of o_proj and down in fp16 (1) or fp32 (0).  The reference rounds these
+// projections to fp16 (their output dtype), so each XCD's share, a sum over a quarter or an eighth
+// of K, fits too; the 8 are added in fp32 before the one rounding of the sum.  fp16 halves the
+// 13 MB that the 256 workgroups read at the start of every launch: 40 us per step.
+#ifndef MLCV_XT_P16
+#define MLCV_XT_P16 1
+#endif
+constexpr bool XT_P16 = MLCV_XT_P16 != 0;
+// this lane's 4 columns (n .. n + 3) of row m of the partial block of (XCD h, slot s)
+__device__ __forceinline__ void xt_store_part(float* part, int h, int s, int T, int m, int n, f4 v) {
+  const size_t i = (((size_t)h * XT_NS + s) * T + m) * 32 + n;
+  if constexpr (XT_P16) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(part) + i) = (h4){f2h(v[0]), f2h(v[1]), f2h(v[2]), f2h(v[3])};
+  else *reinterpret_cast<f4*>(part + i) = v;
+}
+
 struct XtRed {
   const float* part;      // [8][32][T][32], or null: action_in
   const _Float16* xold;   // [T][W1]
@@ -294,13 +309,20 @@ __device__ __forceinline__ void xt_reduce(const XtArgs& a, const XtRed& r, int s
   const h8 sc = load_global(reinterpret_cast<const h8*>(r.mnext + n));
   h8 xn;
   if (r.part) {
-    const __amdgpu_buffer_rsrc_t rp = dev_rsrc(r.part, (uint32_t)(XT_NX * XT_NS * T * 32 * 4));
+    constexpr int EB = XT_P16 ? 2 : 4;  // bytes per partial element
+    const __amdgpu_buffer_rsrc_t rp = dev_rsrc(r.part, (uint32_t)(XT_NX * XT_NS * T * 32 * EB));
     f4 p[XT_NX][2];
 #pragma unroll
     for (int hx = 0; hx < XT_NX; ++hx) {
-      const int off = (((hx * XT_NS + s) * T + m) * 32 + 8 * c8) * 4;
-      p[hx][0] = load_dev<f4, 16>(rp, off);
-      p[hx][1] = load_dev<f4, 16>(rp, off + 16);
+      const int off = (((hx * XT_NS + s) * T + m) * 32 + 8 * c8) * EB;
+      if constexpr (XT_P16) {
+        const h8 q = load_dev<h8, 16>(rp, off);
+        p[hx][0] = (f4){h2f(q[0]), h2f(q[1]), h2f(q[2]), h2f(q[3])};
+        p[hx][1] = (f4){h2f(q[4]), h2f(q[5]), h2f(q[6]), h2f(q[7])};
+      } else {
+        p[hx][0] = load_dev<f4, 16>(rp, off);
+        p[hx][1] = load_dev<f4, 16>(rp, off + 16);
+      }
     }
     const h8 xo = load_dev<h8, 16>(dev_rsrc(r.xold, (uint32_t)(T * XT_W * 2)), (m * XT_W + n) * 2);
     const h8 g = load_global(reinterpret_cast<const h8*>(r.gate + n));
@@ -797,8 +819,7 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
     if (m < T) {
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl)
-        *reinterpret_cast<f4*>(a.opart + (((size_t)h * XT_NS + s) * T + m) * 32 + 16 * sl + 4 * g) =
-            xt_red_sum(lds + XA_RED, sl, w, lane);
+        xt_store_part(a.opart, h, s, T, m, 16 * sl + 4 * g, xt_red_sum(lds + XA_RED, sl, w, lane));
     }
   }
   XT_STAMP(2 * L, 10, 0);
@@ -917,6 +938,15 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
     if (comp) xt_vm_wait<0>();
     xt_sync();
     if (!comp && L + 1 < a.D) xt_prefetch_next(a, L, h, s, __builtin_amdgcn_readfirstlane((tid - XT_NC) >> 6), lane, pf);
+  } else if (a.pf_next == 3) {  // only the next layer's 32 prefix keys / values
+    if (comp) xt_vm_wait<0>();
+    xt_sync();
+    if (!comp && L + 1 < a.D) {
+      const int v = __builtin_amdgcn_readfirstlane((tid - XT_NC) >> 6);
+      const int kc = max(0, min(XT_KCH * s, a.P - XT_KCH));
+      xt_touch<1>(a.keys + ((size_t)(L + 1) * a.P + kc) * XT_HD, XT_KCH * XT_HD * 4, v, lane, pf);
+      if (v >= 2) pf[1] = load_dev<unsigned, 0>(dev_rsrc(a.values + ((size_t)(L + 1) * a.P + kc) * XT_HD + (size_t)(v - 2) * 64 * 64, 8 * 1024), lane * 128);
+    }
   }
   if (comp) {
     xt_mma<4>(acc, xd, lds + XB_DN, 16, 4 * w, 2, lane);
@@ -928,8 +958,7 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
     if (m < T) {
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl)
-        *reinterpret_cast<f4*>(a.dpart + (((size_t)h * XT_NS + s) * T + m) * 32 + 16 * sl + 4 * g) =
-            xt_red_sum(lds + XB_RED, sl, w, lane);
+        xt_store_part(a.dpart, h, s, T, m, 16 * sl + 4 * g, xt_red_sum(lds + XB_RED, sl, w, lane));
     }
   }
   XT_STAMP(2 * L + 1, 6, 0);
