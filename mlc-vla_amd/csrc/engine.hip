@@ -1115,8 +1115,6 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       x.A = c.A;
       x.eps = cfg->rms_norm_eps;
       x.spin = 1u << 22;
-      x.pf_next = 0;
-      if (const char* pe = std::getenv("MLCV_XT_PF")) x.pf_next = std::atoi(pe);
       const size_t D8 = (size_t)c.D * 8, TW = (size_t)T * W1;
       ALLOC(x.x, D8 * TW);
       ALLOC(x.xm, D8 * TW);

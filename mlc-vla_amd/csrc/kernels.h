@@ -412,16 +412,13 @@ struct XtArgs {
   float* rss;       // [8][T][W1/16] row sums of squares of the residual stream per 16 columns
   _Float16* ap;     // [8][32][64][HD] attention split partials O_s / l_s
   float* aml;       // [8][32][64][2]  their (m, l)
-  float* opart;     // [8][32][T][32]  o_proj partials: [XCD][residual column slice][row][column]
+  float* opart;     // [8][32][T][32]  o_proj partials (stored as fp16): [XCD][residual column slice][row][column]
   float* dpart;     // [8][32][T][32]  down partials
   unsigned* flags;  // [8][32] monotonic barrier words (all equal between launches)
   unsigned* err;    // non-zero: a barrier wait gave up
   unsigned spin;    // polls before a wait gives up
   int D, T, P, A, L;
   int ls;           // layer stride of the per-layer buffers (0 or 1)
-  int pf_next;      // the MLP launch prefetches the next layer's attention inputs: 0 no (default:
-                    // every placement measured slowed the stage it overlapped more than it saved),
-                    // 1 during down, 2 with the down weights
   int noskip;       // 1: compute key chunks whose keys are all masked too (testing the skip)
   float eps;
   // the final reduce's outputs in the launch chain's layout (the head reads them)

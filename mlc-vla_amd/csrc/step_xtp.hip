@@ -22,10 +22,17 @@
 //
 // A workgroup is 8 waves.  Waves 0-3 carry the critical path: the barrier polls, activation
 // loads, MFMA, epilogue stores.  Waves 4-7 stream: they move the weights of the coming stage into
-// LDS with buffer-to-LDS DMA and build the attention's key chunk (K split hi/lo, V transposed)
-// before the attention's inputs are ready.  The split matters: a wave's memory operations complete
-// in issue order against one counter, so a wave that polls a flag or waits for its own stores
-// would also wait for every weight load it issued before.
+// LDS with buffer-to-LDS DMA, and (launch A, waves 6-7) build the attention's key chunk (K split
+// hi/lo, V transposed) before the attention's inputs are ready.  The split matters: a wave's
+// memory operations complete in issue order against one counter, so a wave that polls a flag or
+// waits for its own stores would also wait for every weight load it issued before; and the
+// q/k/v weights (needed at barrier 1) and the key chunk (needed at barrier 2) are in different
+// waves, so barrier 1 waits for the first only.
+//
+// Each launch starts bound by the memory side (the weights of its first stage, 5-6 TB/s over all
+// CUs); the rest is a chain of L2 round trips and barriers.  Loads that pull the next launch's
+// weights into L2 during that chain delay the chain's own loads on the same CU (they share its
+// vector memory path) by about as much as they save the next launch, so there are none.
 //
 // Intra-XCD data is written with plain stores (L2) and read with device-scope loads (which miss
 // the CU's L1 and hit the XCD's L2); barrier words are plain stores polled with device-scope loads.
@@ -182,22 +189,6 @@ __device__ __forceinline__ void xt_dma(__amdgpu_buffer_rsrc_t r, int blk, char* 
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)dst, 16, blk * 1024 + lane * 16, 0, 0, 0);
 #endif
-}
-
-// One dword of every 128-byte line of the run [p, p + bytes) into this XCD's L2 for a later
-// launch: stream wave `v` of 4 takes every 4th group of 64 lines, NPL loads per lane (a
-// compile-time count, so that the waits on later DMA can count them); lines past the run read
-// nothing (the descriptor holds the run's size).  The values land in `out` (never stored).
-template <int NPL>
-__device__ __forceinline__ void xt_touch(const void* p, int bytes, int v, int lane, unsigned* out) {
-  const __amdgpu_buffer_rsrc_t r = dev_rsrc(p, (uint32_t)bytes);
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) out[i] = load_dev<unsigned, 0>(r, ((i * 4 + v) * 64 + lane) * 128);
-}
-// the prefetched values, used only here at the end of the launch: the loads stay in flight
-// across the barriers instead of being waited for where they were issued
-__device__ __forceinline__ void xt_keep(const unsigned (&pf)[4]) {
-  asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]));
 }
 
 // ---- compute waves: the skinny GEMM pieces ---------------------------------------------------
@@ -363,15 +354,95 @@ __device__ __forceinline__ void xt_reduce(const XtArgs& a, const XtRed& r, int s
   *reinterpret_cast<h8*>(r.u + xf_index(m, n)) = uu;
 }
 
+// The partial path of xt_reduce split at a workgroup barrier: every load issued before it, the
+// arithmetic and stores after.  Launch A's stream waves start their DMA at that barrier, so the
+// reduce's few loads are ahead of the 112 KB per CU of weights and keys in the memory system.
+struct XtRedLd {
+  h8 q[XT_NX];  // the 8 XCDs' partials (fp16) of this thread's 8 columns
+  h8 xo, g, sc, sh;
+};
+__device__ __forceinline__ void xt_red_issue(const XtArgs& a, const XtRed& r, int s, int tid, XtRedLd& l) {
+  static_assert(XT_P16, "the ordered reduce reads fp16 partials");
+  const int T = a.T, m = tid >> 2, c8 = tid & 3, n = 32 * s + 8 * c8;
+  const bool row = m < T;  // other rows read zeros without a fetch (offsets past the buffers)
+  const __amdgpu_buffer_rsrc_t rp = dev_rsrc(r.part, (uint32_t)(XT_NX * XT_NS * T * 32 * 2));
+#pragma unroll
+  for (int hx = 0; hx < XT_NX; ++hx)
+    l.q[hx] = load_dev<h8, 16>(rp, row ? (((hx * XT_NS + s) * T + m) * 32 + 8 * c8) * 2 : 0x7FFFFF00);
+  l.xo = load_dev<h8, 16>(dev_rsrc(r.xold, (uint32_t)(T * XT_W * 2)), row ? (m * XT_W + n) * 2 : 0x7FFFFF00);
+  l.g = load_global(reinterpret_cast<const h8*>(r.gate + n));
+  l.sc = load_global(reinterpret_cast<const h8*>(r.mnext + n));
+  l.sh = load_global(reinterpret_cast<const h8*>(r.mnext + XT_W + n));
+}
+// same arithmetic, order and stores as xt_reduce's partial path
+__device__ __forceinline__ void xt_red_finish(const XtArgs& a, const XtRed& r, int s, int tid, const XtRedLd& l) {
+  const int T = a.T, m = tid >> 2, c8 = tid & 3, n = 32 * s + 8 * c8;
+  if (m == T) *reinterpret_cast<h8*>(r.u + xf_index(T, n)) = l.sh;
+  if (m >= T) return;
+  h8 xn;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float acc = h2f(l.q[0][e]);
+#pragma unroll
+    for (int hx = 1; hx < XT_NX; ++hx) acc += h2f(l.q[hx][e]);
+    xn[e] = hadd(l.xo[e], hmul(f2h(acc), l.g[e]));
+  }
+  float s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s2 += h2f(xn[e]) * h2f(xn[e]);
+  s2 += __shfl_xor(s2, 1);
+  *reinterpret_cast<h8*>(r.x + (size_t)m * XT_W + n) = xn;
+  if ((c8 & 1) == 0) r.rss[m * XT_RSS + 2 * s + (c8 >> 1)] = s2;
+  h8 uu;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) uu[e] = f2h(h2f(xn[e]) * (1.0f + h2f(l.sc[e])) * r.nsc);
+  *reinterpret_cast<h8*>(r.u + xf_index(m, n)) = uu;
+}
+// s_barrier of all 8 waves with no wait on any counter (the loads before it stay in flight)
+__device__ __forceinline__ void xt_bar_raw() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ size_t xt_tw(const XtArgs& a, int L, int h) { return ((size_t)L * a.ls * XT_NX + h) * a.T * XT_W; }
 __device__ __forceinline__ const _Float16* xt_mod(const XtArgs& a, int norm) { return a.modp + (size_t)norm * 3 * XT_W; }
 
 // ---- attention key chunk ---------------------------------------------------------------------
-// keys [c0, c0 + 32) of [prefix ; suffix] into chunk registers (stream thread lt of 256): prefix
-// keys from the cache, suffix keys (when ready) from this XCD's k / v of the layer, keys past
-// P + T clamped to a valid key and masked with -inf.  Before the suffix is ready its keys hold
-// a prefix key as a placeholder (their mask is 0): the chunk is loaded again once it is.
-__device__ __forceinline__ void xt_load_chunk(ChunkRegs<XT_HD, 256>& R, const XtArgs& a, int L, int h, int c0,
+// The 32 key slots of workgroup s.  Slots [0, nh) hold prefix keys [nh s, nh s + nh); slots
+// [nh, nh + nt) hold keys [32 nh + nt s, + nt) of the tail [32 nh, P + T) (the last prefix keys,
+// then the suffix); later slots, and keys past P + T, are padding (masked with -inf).  nt is the
+// least count with 32 (nh + nt) >= P + T, nh = min(P / 32, 32 - nt), so the head keys are all
+// prefix keys and every workgroup holds at most nt of the suffix keys (2 at T = 50): the keys
+// computed in this launch reach each workgroup in one small load after barrier 2, instead of 50
+// of them reaching two workgroups.  Any partition of the keys gives the same attention; only the
+// order of the fp32 sums in the combine follows it.
+struct XtKeys {
+  int s, nh, nt;
+  __device__ __forceinline__ int key(int j) const {
+    return j < nh ? nh * s + j : (j < nh + nt ? 32 * nh + nt * s + (j - nh) : 0x3FFFFFFF);
+  }
+  __device__ __forceinline__ bool has_suffix(int P, int T) const {
+    const int t0 = 32 * nh + nt * s;
+    return t0 + nt > P && t0 < P + T;
+  }
+};
+__device__ __forceinline__ XtKeys xt_keys(int P, int T, int s) {
+  XtKeys k;
+  k.s = s;
+  for (k.nt = 1; k.nt < XT_KCH; ++k.nt) {  // ends: at nh + nt = 32, 32 (nh + nt) = 1024 >= P + T
+    k.nh = min(P / XT_KCH, XT_KCH - k.nt);
+    if (XT_KCH * (k.nh + k.nt) >= P + T) break;
+  }
+  return k;
+}
+
+// Key slots of `ck` into chunk registers (stream thread lt of NTH): prefix keys from the cache,
+// suffix keys (when ready) from this XCD's k / v of the layer, padding clamped to a valid key and
+// masked with -inf.  Before the suffix is ready its slots hold a prefix key as a placeholder
+// (mask 0): xt_store_suffix overwrites them once it is.
+template <int NTH>
+__device__ __forceinline__ void xt_load_chunk(ChunkRegs<XT_HD, NTH>& R, const XtArgs& a, int L, int h, const XtKeys& ck,
                                               bool suffix_ready, int lt) {
   constexpr int HALF = XT_HD / 2;
   const int P = a.P, T = a.T;
@@ -380,10 +451,10 @@ __device__ __forceinline__ void xt_load_chunk(ChunkRegs<XT_HD, 256>& R, const Xt
   const __amdgpu_buffer_rsrc_t sk = dev_rsrc(a.k32 + ((size_t)L * a.ls * XT_NX + h) * T * XT_HD, (uint32_t)(T * XT_HD * 4));
   const __amdgpu_buffer_rsrc_t sv = dev_rsrc(a.v + ((size_t)L * a.ls * XT_NX + h) * T * XT_HD, (uint32_t)(T * XT_HD * 2));
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<XT_HD, 256>::NK; ++i) {
+  for (int i = 0; i < ChunkRegs<XT_HD, NTH>::NK; ++i) {
     int j, dp;
-    kitem<XT_HD, 256>(i, lt, j, dp);
-    const int kj = c0 + j;
+    kitem<XT_HD, NTH>(i, lt, j, dp);
+    const int kj = ck.key(j);
     if (suffix_ready && kj >= P && kj < P + T) {
       const int off = (kj - P) * XT_HD + dp;
       ld8f<16>(sk, off * 4, R.k[i]);
@@ -395,27 +466,27 @@ __device__ __forceinline__ void xt_load_chunk(ChunkRegs<XT_HD, 256>& R, const Xt
     }
   }
 #pragma unroll
-  for (int i = 0; i < ChunkRegs<XT_HD, 256>::NV; ++i) {
+  for (int i = 0; i < ChunkRegs<XT_HD, NTH>::NV; ++i) {
     int jp, d0;
-    vitem<XT_HD, 256>(i, lt, jp, d0);
+    vitem<XT_HD, NTH>(i, lt, jp, d0);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int kj = c0 + 2 * jp + q;
+      const int kj = ck.key(2 * jp + q);
       if (suffix_ready && kj >= P && kj < P + T)
         R.v[i][q] = load_dev<h8, 16>(sv, ((kj - P) * XT_HD + d0) * 2);
       else
         R.v[i][q] = load_dev<h8, KV_AUX>(rv, (min(kj, P - 1) * XT_HD + d0) * 2);
     }
   }
-  const int km = c0 + (lt & (KCH - 1));
+  const int km = ck.key(lt & (KCH - 1));
   R.msk = km < P ? load_global(a.mask + km) : 0.f;
   R.mok = km < P + T;
 }
 
-// The suffix keys of a chunk that straddles [prefix ; suffix], once the layer's k / v are ready:
-// their K rows (split hi/lo) and their V^T key pairs over the placeholders the first load left
-// (stream thread lt of 256; a V pair holding one prefix and one suffix key is rewritten whole).
-__device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, int c0, AttnSmem<XT_HD>& sm, int lt) {
+// The suffix keys among this workgroup's slots, once the layer's k / v are ready: their K rows
+// (split hi/lo) and their V^T key pairs over the placeholders the first load left (stream thread
+// lt of 256; a V pair holding one prefix and one suffix key is rewritten whole).
+__device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, const XtKeys& ck, AttnSmem<XT_HD>& sm, int lt) {
   constexpr int HALF = XT_HD / 2, KLD = AttnSmem<XT_HD>::KLD;
   constexpr int NK = ChunkRegs<XT_HD, 256>::NK, NV = ChunkRegs<XT_HD, 256>::NV;
   const int P = a.P, T = a.T;
@@ -429,7 +500,7 @@ __device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, i
   for (int i = 0; i < NK; ++i) {
     int j, dp;
     kitem<XT_HD, 256>(i, lt, j, dp);
-    const int kj = c0 + j;
+    const int kj = ck.key(j);
     if (is_suf(kj)) {
       const int off = (kj - P) * XT_HD + dp;
       ld8f<LOC>(sk, off * 4, kr[i]);
@@ -440,11 +511,11 @@ __device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, i
   for (int i = 0; i < NV; ++i) {
     int jp, d0;
     vitem<XT_HD, 256>(i, lt, jp, d0);
-    const int k0 = c0 + 2 * jp;
-    if (is_suf(k0) || is_suf(k0 + 1)) {
+    const int k0 = ck.key(2 * jp), k1 = ck.key(2 * jp + 1);
+    if (is_suf(k0) || is_suf(k1)) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {  // one load per key: its source picked per lane
-        const int kj = k0 + q;
+        const int kj = q ? k1 : k0;
         const _Float16* src = is_suf(kj) ? sv + (size_t)(kj - P) * XT_HD + d0 : pv + (size_t)min(kj, P - 1) * XT_HD + d0;
         vr[i][q] = load_global(reinterpret_cast<const h8*>(src));
       }
@@ -454,7 +525,7 @@ __device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, i
   for (int i = 0; i < NK; ++i) {
     int j, dp;
     kitem<XT_HD, 256>(i, lt, j, dp);
-    if (!is_suf(c0 + j)) continue;
+    if (!is_suf(ck.key(j))) continue;
 #pragma unroll
     for (int hp = 0; hp < 2; ++hp) {
       h8 hi8, lo8;
@@ -473,35 +544,13 @@ __device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, i
   for (int i = 0; i < NV; ++i) {
     int jp, d0;
     vitem<XT_HD, 256>(i, lt, jp, d0);
-    const int k0 = c0 + 2 * jp;
-    if (!(is_suf(k0) || is_suf(k0 + 1))) continue;
+    if (!(is_suf(ck.key(2 * jp)) || is_suf(ck.key(2 * jp + 1)))) continue;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const h2 pair = {vr[i][0][e], vr[i][1][e]};
       *reinterpret_cast<h2*>(&sm.vt[(d0 + e) * VLD + 2 * jp]) = pair;
     }
   }
-}
-
-// The next layer's attention launch: this workgroup's q/k/v and o_proj weights and its 32 prefix
-// keys / values (4 loads per lane of stream wave v; the last layer touches its own)
-__device__ __forceinline__ void xt_prefetch_next(const XtArgs& a, int L, int h, int s, int v, int lane,
-                                                 unsigned (&pf)[4]) {
-  const int Ln = min(L + 1, a.D - 1);
-  const int j0 = s, j1 = s + XT_NS < 48 ? s + XT_NS : s;
-  auto qkv_slab = [&](int j) {
-    return j < 16 ? xt_weights(a, Ln, PK_Q) + (size_t)(16 * h + j) * 32 * 512
-           : j < 32 ? xt_weights(a, Ln, PK_K) + (size_t)(j - 16) * 32 * 512
-                    : xt_weights(a, Ln, PK_V) + (size_t)(j - 32) * 32 * 512;
-  };
-  xt_touch<1>(qkv_slab(j0), 32 * 1024, v, lane, pf);
-  xt_touch<1>(qkv_slab(j1), 32 * 1024, v, lane, pf + 1);
-  // 32 KB of K (all 4 waves), 16 KB of V (waves 2, 3), the o_proj slabs 2s, 2s + 1 (waves 0, 1)
-  const int kc = max(0, min(XT_KCH * s, a.P - XT_KCH));
-  xt_touch<1>(a.keys + ((size_t)Ln * a.P + kc) * XT_HD, XT_KCH * XT_HD * 4, v, lane, pf + 2);
-  const _Float16* run = v < 2 ? xt_weights(a, Ln, PK_O) + ((size_t)(2 * s + v) * 64 + 8 * h) * 512
-                              : a.values + ((size_t)Ln * a.P + kc) * XT_HD + (size_t)(v - 2) * 64 * 64;
-  pf[3] = load_dev<unsigned, 0>(dev_rsrc(run, 8 * 1024), lane * 128);
 }
 
 // ---- launch A: layer L's attention half -----------------------------------------------------
@@ -513,28 +562,34 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   const bool comp = tid < XT_NC;
   const int w = (tid >> 6) & 3, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int h = xt_xcd(), s = blockIdx.x >> 3, L = a.L, T = a.T, P = a.P;
-  const int c0 = XT_KCH * s;  // this workgroup's keys [c0, c0 + 32) of [prefix ; suffix]
-  const bool has_suffix = c0 + XT_KCH > P && c0 < P + T;
+  const int v = __builtin_amdgcn_readfirstlane(tid >> 6) - 4;  // stream wave 0-3 (negative: compute)
+  const XtKeys ck = xt_keys(P, T, s);  // this workgroup's keys of [prefix ; suffix]
+  const bool has_suffix = ck.has_suffix(P, T);
   const int nsl = s + XT_NS < 48 ? 2 : 1;  // q/k/v slabs: j = s, s + 32 of [q_h | k | v] (16 each)
   AttnSmem<XT_HD>& kv = *reinterpret_cast<AttnSmem<XT_HD>*>(lds + XA_KV);
   if (tid == 0) sh.base = xt_ld_agent(a.flags + h * XT_NS + s);
-  unsigned pf[4] = {0, 0, 0, 0};  // values of the stream waves' prefetch loads (never stored)
   XT_STAMP(2 * L, 0, 0);
 
-  // ---- 1. residual stream entering layer L | q/k/v weights, the prefix keys -----------------
+  // ---- 1. residual stream entering layer L | q/k/v weights (waves 4, 5), the key chunk (6, 7) --
+  XtRed r;
+  r.part = FIRST ? nullptr : a.dpart;
+  r.xold = FIRST ? nullptr : a.xm + xt_tw(a, L - 1, h);
+  r.gate = FIRST ? nullptr : xt_mod(a, 2 * L - 1) + 2 * XT_W;
+  r.mnext = xt_mod(a, 2 * L);
+  r.nsc = load_global(a.nscale + 2 * L);
+  r.x = a.x + xt_tw(a, L, h);
+  r.rss = a.rss + (size_t)h * T * XT_RSS;
+  r.u = a.u + (size_t)h * 64 * XT_W;
+  XtRedLd rl;
+  if (!FIRST) {  // the reduce's loads first, then the stream waves' 112 KB
+    if (comp) xt_red_issue(a, r, s, tid, rl);
+    xt_bar_raw();
+  }
+  ChunkRegs<XT_HD, 128> R;  // waves 6, 7: the key chunk, stored to LDS after barrier 1
   if (comp) {
-    XtRed r;
-    r.part = FIRST ? nullptr : a.dpart;
-    r.xold = FIRST ? nullptr : a.xm + xt_tw(a, L - 1, h);
-    r.gate = FIRST ? nullptr : xt_mod(a, 2 * L - 1) + 2 * XT_W;
-    r.mnext = xt_mod(a, 2 * L);
-    r.nsc = load_global(a.nscale + 2 * L);
-    r.x = a.x + xt_tw(a, L, h);
-    r.rss = a.rss + (size_t)h * T * XT_RSS;
-    r.u = a.u + (size_t)h * 64 * XT_W;
-    xt_reduce(a, r, s, tid);
-  } else {
-    const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
+    if (FIRST) xt_reduce(a, r, s, tid);
+    else xt_red_finish(a, r, s, tid, rl);
+  } else if (v < 2) {
     for (int sl = 0; sl < nsl; ++sl) {
       const int j = s + XT_NS * sl;
       const _Float16* base = j < 16 ? xt_weights(a, L, PK_Q) + (size_t)(16 * h + j) * 32 * 512
@@ -542,17 +597,17 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
                                       : xt_weights(a, L, PK_V) + (size_t)(j - 32) * 32 * 512;
       const __amdgpu_buffer_rsrc_t rw = dev_rsrc(base, 32 * 1024);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xt_dma(rw, v + 4 * i, lds + XA_W + (sl * 32 + v + 4 * i) * 1024, lane);
+      for (int i = 0; i < 16; ++i) xt_dma(rw, v + 2 * i, lds + XA_W + (sl * 32 + v + 2 * i) * 1024, lane);
     }
-    ChunkRegs<XT_HD, 256> R;
-    xt_load_chunk(R, a, L, h, c0, false, lt);
-    store_chunk<XT_HD, 256>(R, kv, lt);
+  } else {
+    xt_load_chunk<128>(R, a, L, h, ck, false, tid - XT_NC - 128);
   }
   XT_STAMP(2 * L, 1, 0);
   xt_arrive(a, h, s, comp, 1, sh);
-  if (!comp) xt_vm_wait<0>();
+  if (v == 0 || v == 1) xt_vm_wait<0>();  // the q/k/v blocks have landed (this wave issued only those)
   XT_STAMP(2 * L, 11, XT_NC);
   if (!xt_wait(a, h, 1, sh)) return;
+  if (v >= 2) store_chunk<XT_HD, 128>(R, kv, tid - XT_NC - 128);  // nothing reads the chunk before barrier 2
   XT_STAMP(2 * L, 2, 0);
 
   // ---- 2. adaRMS + q/k/v (RoPE, q hi/lo in the attention's fragment order) ------------------
@@ -627,29 +682,25 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   if (!xt_wait(a, h, 2, sh)) return;
   XT_STAMP(2 * L, 5, 0);
 
-  // ---- 3. attention of head h over keys [c0, c0 + 32): one split of 32 -----------------------
+  // ---- 3. attention of head h over this workgroup's 32 key slots: one split of 32 --------------
   h8 qh[8], ql[8];
   if (comp) {
     const __amdgpu_buffer_rsrc_t rq = dev_rsrc(a.qf + ((size_t)L * a.ls * XT_NX + h) * XT_QF, XT_QF * 2);
+    const bool qrow = 16 * w + r16 < T;  // rows past T: zeros without a fetch
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int qb = (((w * 8 + ks) * 2) * 512 + lane * 8) * 2;
-      qh[ks] = load_dev<h8, LOC>(rq, qb);
-      ql[ks] = load_dev<h8, LOC>(rq, qb + 1024);
+      qh[ks] = load_dev<h8, LOC>(rq, qrow ? qb : 0x7FFFFF00);
+      ql[ks] = load_dev<h8, LOC>(rq, qrow ? qb + 1024 : 0x7FFFFF00);
     }
   } else {
-    const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
     XT_STAMP(2 * L, 14, XT_NC);
-    if (has_suffix) xt_store_suffix(a, L, h, c0, kv, lt);  // this chunk holds suffix keys
+    if (has_suffix) xt_store_suffix(a, L, h, ck, kv, tid - XT_NC);  // this workgroup holds suffix keys
     XT_STAMP(2 * L, 15, XT_NC);
   }
   xt_sync();
   XT_STAMP(2 * L, 13, 0);
-  if (!comp) {
-    // o_proj weights (slabs 2s, 2s + 1, k steps [8h, 8h + 8)) into LDS; then, while the attention
-    // runs on LDS and registers, this workgroup's weights of the MLP launch and of the next
-    // layer's attention launch (and its next 32 prefix keys) into the memory-side cache / L2
-    const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
+  if (!comp) {  // o_proj weights (slabs 2s, 2s + 1, k steps [8h, 8h + 8)) into LDS, during the attention
     const _Float16* wo = xt_weights(a, L, PK_O);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -760,12 +811,6 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   }
   XT_STAMP(2 * L, 6, 0);
   xt_arrive(a, h, s, comp, 3, sh);
-  if (!comp) {  // this workgroup's gate_up and down weights of the MLP launch into the memory-side cache / L2
-    const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
-    xt_touch<2>(xt_weights(a, L, PK_GU) + (size_t)(XT_FX / 8 * h + 2 * s) * 32 * 512, 64 * 1024, v, lane, pf);
-    xt_touch<1>(xt_weights(a, L, PK_DN) + ((size_t)(2 * s) * 128 + 16 * h) * 512, 16 * 1024, v, lane, pf + 2);
-    xt_touch<1>(xt_weights(a, L, PK_DN) + ((size_t)(2 * s + 1) * 128 + 16 * h) * 512, 16 * 1024, v, lane, pf + 3);
-  }
   if (!xt_wait(a, h, 3, sh)) return;
   XT_STAMP(2 * L, 7, 0);
 
@@ -801,7 +846,7 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   }
   XT_STAMP(2 * L, 8, 0);
   xt_arrive(a, h, s, comp, 4, sh);
-  if (!comp) xt_vm_wait<4>();  // the o_proj blocks have landed (the 4 prefetch loads may not have)
+  if (!comp) xt_vm_wait<0>();  // the o_proj blocks have landed
   XT_STAMP(2 * L, 12, XT_NC);
   if (!xt_wait(a, h, 4, sh)) return;
   XT_STAMP(2 * L, 9, 0);
@@ -823,7 +868,6 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
     }
   }
   XT_STAMP(2 * L, 10, 0);
-  xt_keep(pf);
 }
 
 // ---- launch B: layer L's MLP half ----------------------------------------------------------
@@ -835,7 +879,6 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   const int w = (tid >> 6) & 3, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int h = xt_xcd(), s = blockIdx.x >> 3, L = a.L, T = a.T;
   if (tid == 0) sh.base = xt_ld_agent(a.flags + h * XT_NS + s);
-  unsigned pf[4] = {0, 0, 0, 0};  // values of the stream waves' prefetch loads (never stored)
   XT_STAMP(2 * L + 1, 0, 0);
 
   // ---- 1. residual stream after the attention | gate_up and down weights ---------------------
@@ -876,9 +919,7 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
     xt_vm_wait<0>();
   }
   xt_sync();
-  if (!comp) {
-    // down slabs 2 s, 2 s + 1, k steps [16 h, 16 h + 16); then the next layer's q/k/v and o_proj
-    // weights and prefix keys (those loads stay in flight to the end of the launch)
+  if (!comp) {  // down slabs 2 s, 2 s + 1, k steps [16 h, 16 h + 16)
     const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -886,7 +927,6 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
       xt_dma(dev_rsrc(xt_weights(a, L, PK_DN) + ((size_t)(2 * s + sl) * 128 + 16 * h) * 512, 16 * 1024), kk,
              lds + XB_DN + b * 1024, lane);
     }
-    if (a.pf_next == 2 && L + 1 < a.D) xt_prefetch_next(a, L, h, s, v, lane, pf);
   }
   if (comp) {
     xt_mma<8>(acc, xf, lds + XB_GU, 32, 8 * w, 2, lane);
@@ -921,10 +961,7 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   }
   XT_STAMP(2 * L + 1, 4, 0);
   xt_arrive(a, h, s, comp, 2, sh);
-  if (!comp) {  // the down blocks have landed (the 4 prefetch loads may not have)
-    if (a.pf_next == 2) xt_vm_wait<4>();
-    else xt_vm_wait<0>();
-  }
+  if (!comp) xt_vm_wait<0>();  // the down blocks have landed
   XT_STAMP(2 * L + 1, 12, XT_NC);
   if (!xt_wait(a, h, 2, sh)) return;
   XT_STAMP(2 * L + 1, 5, 0);
@@ -932,22 +969,6 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   // ---- 3. down, row-parallel: this XCD's 512 columns of K, outputs [32 s, 32 s + 32) ---------
   h8 xd[4][4];
   if (comp) xt_load_x<4>(xd, a.h + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_FX, XT_FX, 4 * w, T - 1, lane);
-  if (a.pf_next == 1) {
-    // once the activations have landed, the next layer's q/k/v and o_proj weights and prefix keys
-    // (those loads stay in flight to the end of the launch)
-    if (comp) xt_vm_wait<0>();
-    xt_sync();
-    if (!comp && L + 1 < a.D) xt_prefetch_next(a, L, h, s, __builtin_amdgcn_readfirstlane((tid - XT_NC) >> 6), lane, pf);
-  } else if (a.pf_next == 3) {  // only the next layer's 32 prefix keys / values
-    if (comp) xt_vm_wait<0>();
-    xt_sync();
-    if (!comp && L + 1 < a.D) {
-      const int v = __builtin_amdgcn_readfirstlane((tid - XT_NC) >> 6);
-      const int kc = max(0, min(XT_KCH * s, a.P - XT_KCH));
-      xt_touch<1>(a.keys + ((size_t)(L + 1) * a.P + kc) * XT_HD, XT_KCH * XT_HD * 4, v, lane, pf);
-      if (v >= 2) pf[1] = load_dev<unsigned, 0>(dev_rsrc(a.values + ((size_t)(L + 1) * a.P + kc) * XT_HD + (size_t)(v - 2) * 64 * 64, 8 * 1024), lane * 128);
-    }
-  }
   if (comp) {
     xt_mma<4>(acc, xd, lds + XB_DN, 16, 4 * w, 2, lane);
     xt_red_store(acc, lds + XB_RED, w, lane);
@@ -962,7 +983,6 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
     }
   }
   XT_STAMP(2 * L + 1, 6, 0);
-  xt_keep(pf);
 }
 
 // ---- the last layer's down partials -> the residual stream in the launch chain's layout --------
