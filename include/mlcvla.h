@@ -107,6 +107,11 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * mlcv_step_probe (1) or reuses one set of buffers for all layers (0, faster; probes then
  * return an error). */
 #define MLCV_OPT_XTP_KEEP 7
+/* MLCV_OPT_SYNC_WORDS (testing): set every progress word of the persistent step and every
+ * barrier word of the XCD step to `value` mod 2^32 (no step may be in flight).  The words only
+ * grow, wrapping at 2^32, and each launch compares them with wrapping arithmetic against its
+ * own start value; a value just below 2^32 makes the next launches wrap. */
+#define MLCV_OPT_SYNC_WORDS 8
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 
 /* Synchronize `stream` and report a persistent step that ended early (a wait between its

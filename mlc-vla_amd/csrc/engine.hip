@@ -1252,6 +1252,16 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
     if (c.xt_on) c.pk_on = false;
   } else if (key == MLCV_OPT_XTP_KEEP) {
     c.xt.ls = value != 0 ? 1 : 0;
+  } else if (key == MLCV_OPT_SYNC_WORDS) {
+    MLCV_HIP(hipDeviceSynchronize());
+    if (c.pk_ok) {
+      const std::vector<unsigned> w((size_t)c.pk.G, (unsigned)value);
+      MLCV_HIP(hipMemcpy(c.pk.prog, w.data(), w.size() * 4, hipMemcpyHostToDevice));
+    }
+    if (c.xt_ok) {
+      const std::vector<unsigned> w((size_t)8 * 32, (unsigned)value);
+      MLCV_HIP(hipMemcpy(c.xt.flags, w.data(), w.size() * 4, hipMemcpyHostToDevice));
+    }
   } else if (key == MLCV_OPT_PERSIST_SPIN) {
     MLCV_REQUIRE(value >= 0 && value <= 0x7FFFFFFF, "spin limit");
     c.pk.spin = (unsigned)value;
@@ -1587,12 +1597,13 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
   MLCV_REQUIRE(ctx, "null context");
   Ctx& c = ctx->c;
   MLCV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  // every error word is read and reset before returning, so that one cause does not leave
+  // another's words inconsistent for the calls after this sync
+  std::string why;
   if (const unsigned e = __atomic_load_n(c.status, __ATOMIC_ACQUIRE)) {
     __atomic_store_n(c.status, 0u, __ATOMIC_RELEASE);
-    set_error("a split-K meeting of the prefill GEMMs gave up (error word " + std::to_string(e) +
-              "; other work held the CUs the split workgroups need); the outputs of the calls since the last "
-              "successful sync are invalid");
-    return -4;
+    why += "a split-K meeting of the prefill GEMMs gave up (error word " + std::to_string(e) +
+           "; other work held the CUs the split workgroups need)";
   }
   if (c.xt_ok) {
     unsigned xerr = 0;
@@ -1601,26 +1612,28 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
       // the barrier words are no longer equal after an abandoned launch: start over
       MLCV_HIP(hipMemset(c.xt.flags, 0, (size_t)8 * 32 * 4));
       MLCV_HIP(hipMemset(c.xt.err, 0, 4));
-      MLCV_HIP(hipDeviceSynchronize());
-      set_error("XCD step: a barrier wait gave up (error word " + std::to_string(xerr) +
-                "); the outputs of the calls since the last successful sync are invalid");
-      return -4;
+      why += std::string(why.empty() ? "" : "; ") + "XCD step: a barrier wait gave up (error word " +
+             std::to_string(xerr) + ")";
     }
   }
-  if (!c.pk_ok) return 0;
-  unsigned err = 0;
-  MLCV_HIP(hipMemcpy(&err, c.pk.err, 4, hipMemcpyDeviceToHost));
-  if (err == 0) return 0;
-  // progress words and split-K counters are inconsistent after an abandoned launch: start over
-  const size_t Dn = (size_t)c.D, W16 = (size_t)c.W1 / 16;
-  MLCV_HIP(hipMemset(c.pk.prog, 0, (size_t)c.pk.G * 4));
-  MLCV_HIP(hipMemset(c.pk.cnto, 0, Dn * W16 * 4));
-  MLCV_HIP(hipMemset(c.pk.cntd, 0, Dn * W16 * 4));
-  MLCV_HIP(hipMemset(c.pk.cntm, 0, Dn * c.KV * (c.pk.rpad / 64) * 4));
-  MLCV_HIP(hipMemset(c.pk.err, 0, 4));
+  if (c.pk_ok) {
+    unsigned err = 0;
+    MLCV_HIP(hipMemcpy(&err, c.pk.err, 4, hipMemcpyDeviceToHost));
+    if (err != 0) {
+      // progress words and counters are inconsistent after an abandoned launch: start over
+      const size_t Dn = (size_t)c.D, W16 = (size_t)c.W1 / 16;
+      MLCV_HIP(hipMemset(c.pk.prog, 0, (size_t)c.pk.G * 4));
+      MLCV_HIP(hipMemset(c.pk.cnto, 0, Dn * W16 * 4));
+      MLCV_HIP(hipMemset(c.pk.cntd, 0, Dn * W16 * 4));
+      MLCV_HIP(hipMemset(c.pk.cntm, 0, Dn * c.KV * (c.pk.rpad / 64) * 4));
+      MLCV_HIP(hipMemset(c.pk.err, 0, 4));
+      why += std::string(why.empty() ? "" : "; ") + "persistent step: a wait between phases gave up (error word " +
+             std::to_string(err) + ")";
+    }
+  }
+  if (why.empty()) return 0;
   MLCV_HIP(hipDeviceSynchronize());
-  set_error("persistent step: a wait between phases gave up (error word " + std::to_string(err) +
-            "); the outputs of the calls since the last successful sync are invalid");
+  set_error(why + "; the outputs of the calls since the last successful sync are invalid");
   return -4;
 }
 

@@ -362,7 +362,6 @@ struct PkArgs {
   int nsplit, kps, rows, rpad;  // attention plan
   unsigned* prog;         // [G] progress words
   unsigned* err;          // device error word (non-zero: a wait gave up)
-  unsigned* err_host;     // pinned host copy of the error word, or null
   unsigned spin;          // polls before a wait gives up
   int merge_comb;         // the attention's key splits combine their row block after meeting
   unsigned* cntm;         // [D][KV][row blocks] arrival counters of those meetings (monotonic)

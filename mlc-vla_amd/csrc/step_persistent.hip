@@ -13,7 +13,7 @@
 // Data crossing workgroups is written with device-scope stores (through this XCD's L2 to the
 // memory side) and read with device-scope loads, and every buffer is written once per launch,
 // so no cache maintenance is needed.  Waits are bounded: a wait that gives up sets the error
-// word (and its pinned host copy) and every workgroup leaves the kernel.
+// word and every workgroup leaves the kernel (mlcv_sync reports it and resets the words).
 //
 // GEMM tasks are the fragment-major skinny tiles of gemm_skinny.hip in a fixed shape: SW
 // 16-row weight slabs, one K slice split over the 4 waves in equal k ranges, the 4 partial
@@ -130,7 +130,6 @@ __device__ __forceinline__ bool pk_wait(CPk& p, unsigned target, PkShared& sh) {
     if (lane == 0) {
       if (!ok && !failed) {  // this wait gave up: every workgroup leaves at its next wait
         __hip_atomic_fetch_or(p.err, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (p.err_host) __hip_atomic_fetch_or(p.err_host, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
       sh.flag = ok ? 1 : 0;
     }
@@ -162,7 +161,6 @@ __device__ __forceinline__ bool pk_wait_count(CPk& p, const unsigned* ctr, unsig
     if (pk_tid() == 0) {
       if (!ok && !failed) {
         __hip_atomic_fetch_or(p.err, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (p.err_host) __hip_atomic_fetch_or(p.err_host, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
       sh.flag = ok ? 1 : 0;
     }
@@ -625,11 +623,11 @@ __device__ __forceinline__ void pk_combine_row(const AttnArgs& a, int nsplit, in
 
 // Joint attention of layer L.  With merge_comb (every task on its own workgroup), the key
 // splits of a row block meet at the block's arrival counter once their partials are stored
-// (the counter advances by nsplit per launch: launch is this launch's index), and split s
-// then combines rows s * rps .. (s + 1) * rps - 1 of the block, one row per wave.
+// (each split adds 1; the counter is 0 at launch start: layer L's o_proj phase of the previous
+// launch reset it), and split s then combines rows s * rps .. (s + 1) * rps - 1 of the block, one
+// row per wave.
 template <int HD, bool Q4>
-__device__ __forceinline__ bool phase_attn(CPk& p, int L, unsigned target, unsigned launch, PkShared& sh,
-                                           char* smem) {
+__device__ __forceinline__ bool phase_attn(CPk& p, int L, unsigned target, PkShared& sh, char* smem) {
   if (!pk_wait(p, target, sh)) return false;
   const AttnArgs a = pk_attn_args(p, L);
   const int rb = p.rpad / 64, n = rb * p.nsplit * p.KV;
@@ -641,7 +639,7 @@ __device__ __forceinline__ bool phase_attn(CPk& p, int L, unsigned target, unsig
     if (p.merge_comb && p.nsplit > 1) {
       unsigned* ctr = p.cntm + ((size_t)L * p.KV + kvh) * rb + rbi;
       if (pk_tid() == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!pk_wait_count(p, ctr, (launch + 1u) * (unsigned)p.nsplit, sh)) return false;
+      if (!pk_wait_count(p, ctr, (unsigned)p.nsplit, sh)) return false;
       const int lane = pk_tid() & 63, w = pk_tid() >> 6;
       for (int r = split * rps + w; r < min(64, (split + 1) * rps); r += 4) {
         const int row = rbi * 64 + r;
@@ -709,6 +707,14 @@ __device__ __forceinline__ bool phase_res(CPk& p, int L, bool down, unsigned tar
   int t = pk_bid();
   if (t < n) pk_load_w<Q4, 1, KP>(wr, lin, t / S, K, (t % S) * kslice + w * kpw, kpw);
   if (!pk_wait(p, target, sh)) return false;
+  if (!down && p.merge_comb && p.nsplit > 1) {
+    // every workgroup has left layer L's attention phase (this wait): its row-block counters
+    // go back to 0 for the next launch, whose combiners wait for exactly nsplit arrivals
+    const int nc = p.KV * (p.rpad / 64);
+    if (pk_tid() == 0)
+      for (int c = pk_bid(); c < nc; c += p.G)
+        __hip_atomic_store(p.cntm + (size_t)L * nc + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   for (; t < n; t += p.G) {
     const int tile = t / S, s = t % S;
     const int kbase = s * kslice + w * kpw;
@@ -822,7 +828,6 @@ __global__ __launch_bounds__(PK_THREADS) void pstep_kernel(PkArgs args) {
   const unsigned base = ld_agent(ka->prog + pk_bid());
   const int ppl = ka->merge_comb ? 5 : 6;  // phases per layer
   const int nph = 2 + ppl * ka->D;
-  const unsigned launch = base / (unsigned)nph;  // every launch advances the progress words by nph
   for (int ph = 0; ph < nph; ++ph) {
     CPk& p = *launder(ka);
     const unsigned target = base + (unsigned)ph;  // every workgroup has published phase ph - 1
@@ -840,7 +845,7 @@ __global__ __launch_bounds__(PK_THREADS) void pstep_kernel(PkArgs args) {
       case PH_QKV:
         ok = k8 ? phase_qkv<HD, Q4, 8>(p, L, target, sh, smem) : phase_qkv<HD, Q4, 0>(p, L, target, sh, smem);
         break;
-      case PH_ATTN: ok = phase_attn<HD, Q4>(p, L, target, launch, sh, smem); break;
+      case PH_ATTN: ok = phase_attn<HD, Q4>(p, L, target, sh, smem); break;
       case PH_COMB: ok = phase_comb(p, L, target, sh); break;
       case PH_OPROJ:
         ok = p.nq / p.so == 1024  ? phase_res<Q4, 8>(p, L, false, target, sh, smem)

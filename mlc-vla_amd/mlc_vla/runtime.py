@@ -214,6 +214,11 @@ class VirtualMachine:
             self.set_xtp(False)
             self.set_persist(form == "persistent")
 
+    def set_sync_words(self, value: int) -> None:
+        """Set the persistent step's progress words and the XCD step's barrier words (testing:
+        a value just below 2**32 makes the next launches wrap them)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_SYNC_WORDS, int(value) & 0xFFFFFFFF)
+
     def set_persist_spin(self, polls: int) -> None:
         """Polls before a wait of the persistent or XCD step gives up."""
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST_SPIN, int(polls))

@@ -74,6 +74,19 @@ def test_persistent_graph_replays_and_repeats(tiny_step):
     np.testing.assert_array_equal(graph, host)
 
 
+def test_persistent_progress_words_wrap(full_step):
+    """Progress words started just below 2**32 wrap inside the next launches (92 phases each at
+    this shape): every launch compares them against its own start value, and the attention's
+    row-block counters start each launch at 0, so the steps equal those from words at 0 bit for
+    bit (a launch index derived from the words would jump at the wrap)."""
+    s = full_step
+    s.runner.vm.set_sync_words(0)
+    good = s.run()
+    s.runner.vm.set_sync_words(2**32 - 40)
+    for _ in range(4):
+        np.testing.assert_array_equal(s.run(), good)
+
+
 def test_persistent_wait_timeout_is_reported_and_recovered(tiny_step):
     """A wait between phases that gives up (forced from the host with a spin limit of zero
     polls, every kernel still exits) is reported by mlcv_sync / the output's .numpy(), and

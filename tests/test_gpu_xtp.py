@@ -3,7 +3,8 @@ workgroup per CU, tensor-parallel over the 8 XCDs, pi0_model.py:142-163 / gemma_
 at the full pi0.5 shape: against the oracle op by op and layer by layer (every layer's
 intermediates kept, MLCV_OPT_XTP_KEEP), the 8 XCDs' copies of the residual stream, against the
 launch chain, with the default reused buffers, across graph replays and the device loop, with
-the masked-chunk skip against the same step without it, and with a barrier wait that gives up."""
+the masked-chunk skip against the same step without it, with barrier words that wrap, and with
+a barrier wait that gives up."""
 
 from __future__ import annotations
 
@@ -104,6 +105,18 @@ def test_xtp_masked_chunk_skip_is_exact(xstep):
         vm.set_xtp_keep(True)
     assert np.all(np.isfinite(skipped))
     np.testing.assert_array_equal(skipped, full)
+
+
+def test_xtp_barrier_words_wrap(xstep):
+    """Barrier words started just below 2**32 wrap in the first layers' launches (4 barriers
+    per attention launch, 2 per MLP launch): the waits compare against each launch's start value
+    with wrapping arithmetic, so the steps equal those from words at 0 bit for bit."""
+    s = xstep
+    s.runner.vm.set_sync_words(0)
+    good = s.run()
+    s.runner.vm.set_sync_words(2**32 - 3)
+    for _ in range(3):
+        np.testing.assert_array_equal(s.run(), good)
 
 
 def test_xtp_wait_timeout_is_reported_and_recovered(xstep):
