@@ -52,8 +52,12 @@ def parse():
     ap.add_argument("--summarize-pmc", metavar="COUNTER_CSV",
                     help="print the mean of each counter per dispatch of a rocprofv3 --pmc CSV, by kernel and "
                          "launch shape, and exit")
-    ap.add_argument("--only-op", choices=sorted(list(OPS_PER_STEP) + ["attention_only", "prefill"]), default=None,
+    ap.add_argument("--only-op", choices=sorted(set(OPS_PER_STEP) | set(OPS_PER_STEP_CHAIN) | {"attention_only", "prefill"}),
+                    default=None,
                     help="after set-up, run --op-iters launches of one op of the step and exit (for --pmc runs)")
+    ap.add_argument("--xt-timeline", action="store_true",
+                    help="with MLCV_LIB naming the phase-stamp build (mlc-vla_amd/build.py --trace): run the "
+                         "step and print the XCD step's per-phase timeline as markdown, then exit")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run --op-iters device copies of this many MiB and exit (counter calibration)")
     return ap.parse_args()
@@ -91,6 +95,51 @@ def summarize_pmc(path):
         n = max(len(v) for v in cs.values())
         vals = [f"{sum(cs[c].values()) / len(cs[c]):.1f}" if c in cs else "" for c in counters]
         print(f"| {key[0][:48]} | {key[1]} | {key[2]} | {n} | " + " | ".join(vals) + " |")
+
+
+XT_PHASES_A = [(0, "start"), (1, "reduce stored (waves 0-3)"), (11, "q/k/v weights in LDS (waves 4-5)"),
+               (2, "barrier 1"), (3, "q/k/v MMA"), (4, "q/k/v epilogue stored"), (5, "barrier 2"),
+               (14, "suffix keys: load start (waves 4-7)"), (15, "suffix keys in LDS"), (13, "attention start"),
+               (6, "attention partials stored"), (7, "barrier 3"), (8, "combine stored"),
+               (12, "o_proj weights in LDS (waves 4-7)"), (9, "barrier 4"), (10, "o_proj partials stored")]
+XT_PHASES_B = [(0, "start"), (1, "reduce stored (waves 0-3)"), (11, "gate_up weights in LDS (waves 4-7)"),
+               (2, "barrier 1"), (3, "gate_up MMA"), (4, "GeGLU stored"), (12, "down weights in LDS (waves 4-7)"),
+               (5, "barrier 2"), (6, "down partials stored")]
+
+
+def xt_timeline_report(tr, depth):
+    """Markdown of the XCD step's phase stamps: tr[2 L + (MLP launch)][workgroup][stamp] in
+    s_memrealtime ticks (100 MHz).  Per phase: min / median / max over the 256 workgroups of the
+    time since the launch's first workgroup started, averaged over layers 1 .. depth - 1."""
+    import numpy as np
+
+    us = lambda t: t / 100.0  # noqa: E731
+    lines = []
+    ends = {0: 10, 1: 6}
+    for half, (name, phases) in enumerate((("attention launch (A)", XT_PHASES_A), ("MLP launch (B)", XT_PHASES_B))):
+        lines.append(f"\n{name}, layers 1-{depth - 1}: microseconds since the launch's first workgroup started\n")
+        lines.append("| stamp | phase | min | median | max |")
+        lines.append("|---|---|---|---|---|")
+        for k, label in phases:
+            mins, meds, maxs = [], [], []
+            for L in range(1, depth):
+                t = tr[2 * L + half]
+                v = us(t[:, k] - t[:, 0].min())
+                mins.append(v.min())
+                meds.append(np.median(v))
+                maxs.append(v.max())
+            lines.append(f"| {k} | {label} | {np.mean(mins):.2f} | {np.mean(meds):.2f} | {np.mean(maxs):.2f} |")
+    spans = {h: [us(tr[2 * L + h][:, ends[h]].max() - tr[2 * L + h][:, 0].min()) for L in range(depth)] for h in (0, 1)}
+    gaps = [us(tr[i + 1][:, 0].min() - tr[i][:, ends[i % 2]].max()) for i in range(2 * depth - 1)]
+    total = us(tr[2 * depth - 1][:, 6].max() - tr[0][:, 0].min())
+    lines.append("")
+    lines.append(f"- attention launch span (first workgroup start to last workgroup end): mean {np.mean(spans[0][1:]):.2f} us "
+                 f"(layer 0, with action_in: {spans[0][0]:.2f} us)")
+    lines.append(f"- MLP launch span: mean {np.mean(spans[1]):.2f} us")
+    lines.append(f"- between launches (last end to next first start): mean {np.mean(gaps):.2f} us, "
+                 f"A to B {np.mean(gaps[0::2]):.2f}, B to A {np.mean(gaps[1::2]):.2f}")
+    lines.append(f"- the {2 * depth} layer launches, first start to last end: {total:.1f} us")
+    return "\n".join(lines)
 
 
 def summarize_trace(path):
@@ -175,10 +224,23 @@ def op_bytes_flops(cfg, op):
         return W * F * 2 + T * F * 2 + 2 * T * W * 2 + W * 2, 2 * T * F * W
     if op == "head":
         return cfg.action_dim * W * 2 + T * W * 2 + T * cfg.action_dim * 4, 2 * T * W * cfg.action_dim
+    if op == "xt_attn":  # the XCD step's attention launch: q/k/v + attention + o_proj of one layer
+        b = (nq + 2 * nkv) * W * 2 + W * nq * 2  # q/k/v and o_proj weights
+        b += KV * P * hd * 6 + P * 4 + T * hd * 4  # prefix K (f32) / V (f16), mask, RoPE tables
+        b += 2 * T * W * 2 + 2 * 3 * W * 2  # residual stream in / out, two modulation rows
+        return b, 2 * T * W * (nq + 2 * nkv) + 4 * H * T * (P + T) * hd + 2 * T * nq * W
+    if op == "xt_mlp":  # the XCD step's MLP launch: gate_up + GeGLU + down of one layer
+        return 2 * F * W * 2 + W * F * 2 + 2 * T * W * 2 + 2 * 3 * W * 2, 2 * T * W * 2 * F + 2 * T * F * W
     raise KeyError(op)
 
 
-OPS_PER_STEP = {"modulation": 1, "qkv": 18, "attention": 18, "o_proj": 18, "gate_up": 18, "down": 18, "head": 1}
+# the default step (the XCD tensor-parallel form) and the launch chain (one launch per operation:
+# the form of the q4f16_1 step and of shapes the XCD step does not take)
+OPS_PER_STEP = {"modulation": 1, "xt_attn": 18, "xt_mlp": 18, "head": 1}
+OPS_PER_STEP_CHAIN = {"modulation": 1, "qkv": 18, "attention": 18, "o_proj": 18, "gate_up": 18, "down": 18, "head": 1}
+OP_LAYER = {"xt_attn": 1}  # layer 0's attention launch also computes action_in
+KERNEL_SYMBOLS = {"xt_attn": "xt_attn_kernel<false>", "xt_mlp": "xt_mlp_kernel",
+                  "attention": "attn_kernel<256, true, false, false, true, 8> + attn_combine_kernel<24>"}
 
 
 def _cpu_model():
@@ -318,6 +380,21 @@ def main():
     x0 = d(noise)
     keys, values = vm["prefill"](prefix, pm_all, params)
     torch.cuda.synchronize()
+    if args.xt_timeline:
+        lib = N.load()
+        if not hasattr(lib, "mlcv_xt_trace_ptr"):
+            sys.exit("--xt-timeline needs MLCV_LIB naming the phase-stamp build (mlc-vla_amd/build.py --trace)")
+        for _ in range(10):
+            vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)
+        torch.cuda.synchronize()
+        lib.mlcv_xt_trace_ptr.restype = ctypes.c_void_p
+        buf = np.zeros(64 * 256 * 16, np.uint64)
+        hip = ctypes.CDLL("libamdhip64.so")
+        if hip.hipMemcpy(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(lib.mlcv_xt_trace_ptr()),
+                         ctypes.c_size_t(buf.nbytes), 2) != 0:
+            sys.exit("hipMemcpy of the phase stamps failed")
+        print(xt_timeline_report(buf.reshape(64, 256, 16).astype(np.int64), cfg.vlm.depth))
+        return
 
     def timed(fn, iters, warmup):
         for _ in range(warmup):
@@ -371,7 +448,11 @@ def main():
     if args.only_op:
         op = N.OPS[args.only_op]
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        N.call("mlcv_bench_op", vm._ctx, op, 0, args.op_iters, runtime._ptr(keys), runtime._ptr(values), st)
+        if args.only_op.startswith("xt_"):  # the XCD launches read the inputs of a step
+            vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)
+            torch.cuda.synchronize()
+        N.call("mlcv_bench_op", vm._ctx, op, OP_LAYER.get(args.only_op, 0), args.op_iters, runtime._ptr(keys),
+               runtime._ptr(values), st)
         torch.cuda.synchronize()
         b, f = op_bytes_flops(cfg, args.only_op)
         print(json.dumps({"only_op": args.only_op, "launches": args.op_iters, "bytes_per_launch": int(b)}))
@@ -409,18 +490,38 @@ def main():
     copy_gbs = 2 * csrc.numel() * 4 / (copy_ms * 1e-3) / 1e9
     del csrc, cdst
 
-    # ---- per-op launch times (the step's kernels one op at a time) ------------
-    per_op = {}
-    for name, cnt in OPS_PER_STEP.items():
-        op = N.OPS[name]
-        run = lambda: N.call("mlcv_bench_op", vm._ctx, op, 0, args.op_iters, runtime._ptr(keys),  # noqa: E731
-                             runtime._ptr(values), stream())
-        ms, _ = timed(run, 1, 1)
-        us = ms * 1e3 / args.op_iters
-        b, f = op_bytes_flops(cfg, name)
-        per_op[name] = {"us": round(us, 2), "per_step": cnt, "us_per_step": round(us * cnt, 1),
-                        "GBps": round(b / (us * 1e-6) / 1e9, 1), "bytes": int(b), "flops": int(f)}
+    # ---- per-op launch times (the step's kernels one op at a time, back to back) ---
+    def op_table(ops):
+        tab = {}
+        for name, cnt in ops.items():
+            op, layer = N.OPS[name], OP_LAYER.get(name, 0)
+            run = lambda: N.call("mlcv_bench_op", vm._ctx, op, layer, args.op_iters,  # noqa: E731
+                                 runtime._ptr(keys), runtime._ptr(values), stream())
+            ms, _ = timed(run, 1, 1)
+            us = ms * 1e3 / args.op_iters
+            b, f = op_bytes_flops(cfg, name)
+            tab[name] = {"us": round(us, 2), "per_step": cnt, "us_per_step": round(us * cnt, 1),
+                         "GBps": round(b / (us * 1e-6) / 1e9, 1), "bytes": int(b), "flops": int(f)}
+        return tab
+
+    per_op = op_table(OPS_PER_STEP)
+    per_op_chain = op_table(OPS_PER_STEP_CHAIN)
     dom = max(per_op, key=lambda k: per_op[k]["us_per_step"])
+
+    # ---- the isolated attention of the fp16-cache configuration (prefix K/V fp16, 900 of 968
+    # prefix keys valid, 50 suffix keys, 8 heads, hd 256): mlcv_joint_attention, cold ---------
+    g1 = torch.Generator(device="cuda").manual_seed(11)
+    sc = 1.0 / 16.0  # N(0, 1) / sqrt(256)
+    a1 = {n: (torch.randn(shp, generator=g1, device="cuda") * sc).half() for n, shp in
+          (("q", (50, 8 * 256)), ("k", (1, 968, 256)), ("v", (1, 968, 256)), ("ks", (50, 256)), ("vs", (50, 256)))}
+    m1 = torch.where(torch.arange(968, device="cuda") < 900, 0.0, -1e9).float()
+    o1 = torch.empty((50, 8 * 256), dtype=torch.float16, device="cuda")
+    tp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    attn1 = lambda: N.call("mlcv_joint_attention", tp(a1["q"]), 50, 8, 1, 256, tp(a1["k"]), 0,  # noqa: E731
+                           tp(a1["v"]), 968, tp(m1), tp(a1["ks"]), tp(a1["vs"]), 50, tp(o1), stream())
+    c1_single = per_cold(attn1, 30)
+    c1_stack = per_cold(lambda: [attn1() for _ in range(18)], 10)
+    c1_bytes = 968 * 256 * 2 * 2 + 50 * 8 * 256 * 2 * 2 + 50 * 256 * 2 * 2  # K, V, q, out, suffix k / v
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):  # calibrated PMC bytes per launch (see profiles/traffic_per_op_pmc.md)
@@ -456,22 +557,34 @@ def main():
         "attention_isolated": {
             "workload": "joint attention of one layer, P=968 prefix keys (fp32) + 50 suffix keys, 8 q heads, hd 256",
             "instance": "the step's own attention (q as hi/lo fragments from the q/k/v epilogue, roped fp32 suffix "
-                        "keys, fp32 prefix K cache) + split combine, without prefetch workgroups; the prefix K is "
-                        "fp32 because prefill writes the roped cache in fp32 (a config naming fp16 K/V is timed "
-                        "on this fp32-K instance); its oracle check is the attention gate of "
-                        "tests/test_gpu_chain_ops.py at this shape",
+                        "keys, fp32 prefix K cache) + split combine, without prefetch workgroups (the launch chain's "
+                        "attention; the XCD step runs its attention inside its attention launch); the prefix K is "
+                        "fp32 because prefill writes the roped cache in fp32; its oracle check is the attention "
+                        "gate of tests/test_gpu_chain_ops.py at this shape",
             "single_cold_p50_us": round(_pct(a_single, 0.5), 2),
             "stacked18_cold_us_per_layer": round(_pct(a_stack, 0.5) / 18, 2),
             "bytes_per_launch": int(a_bytes),
             "single_GBps": round(a_bytes / (_pct(a_single, 0.5) * 1e-6) / 1e9, 1),
             "stacked18_GBps": round(a_bytes * 18 / (_pct(a_stack, 0.5) * 1e-6) / 1e9, 1)},
+        "attention_fp16_cache": {
+            "workload": "joint attention, q [50, 8 x 256] f16, prefix K/V [968, 256] f16 with 900 valid, "
+                        "suffix k/v [50, 256] f16, all N(0,1)/16 (mlcv_joint_attention; its oracle check is "
+                        "tests/test_gpu_kernels.py::test_joint_attention_vs_oracle at this shape)",
+            "single_cold_p50_us": round(_pct(c1_single, 0.5), 2),
+            "stacked18_cold_us_per_layer": round(_pct(c1_stack, 0.5) / 18, 2),
+            "bytes_per_launch": int(c1_bytes),
+            "single_GBps": round(c1_bytes / (_pct(c1_single, 0.5) * 1e-6) / 1e9, 1),
+            "stacked18_GBps": round(c1_bytes * 18 / (_pct(c1_stack, 0.5) * 1e-6) / 1e9, 1)},
         "prefill_ms": round(prefill_ms, 3),
         "loop_ms": round(loop_ms, 3),
         "step_roofline": {"bound": "hbm", "achieved": round(sbytes / (step_us * 1e-6) / 1e9, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(sbytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                           "bytes_per_step": int(sbytes), "flops_per_step": int(step_flops(cfg))},
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS,
+        "roofline": {"kernel": dom, "symbol": KERNEL_SYMBOLS.get(dom, dom), "bound": "hbm",
+                     "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS,
+                     "timing": "HIP events around --op-iters back-to-back launches on the step's stream (each "
+                               "interval also holds the launch gap between dependent kernels)",
                      "unit": "GB/s", "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": per_op[dom]["bytes"], "avg_launch_us": per_op[dom]["us"],
                      "measured_copy_GBps": round(copy_gbs, 1),
@@ -480,6 +593,7 @@ def main():
                          "protocol": "torch copy_ of 1 GiB fp32 device to device, 20 timed after 3 warm-ups; "
                                      "GB/s counts bytes read + written"},
         "per_op": per_op,
+        "per_op_chain": per_op_chain,
     }
     # executed prefill flops: q/k/v of all 18 layers (their K/V are the output); attention,
     # o_proj, gate_up and down of the first 17 (the last layer's feed nothing)

@@ -290,6 +290,12 @@ int mlcv_tile_linear(const void* x, int32_t M, int32_t K, const void* w, int32_t
 #define MLCV_OP_HEAD 7       /* final adaRMS + action_out_proj */
 #define MLCV_OP_ATTENTION_ONLY 8 /* MLCV_OP_ATTENTION without the workgroups that prefetch the next ops' weights */
 #define MLCV_OP_ACTION_IN 9  /* action_in_proj: the residual stream entering layer 0 */
+/* The XCD step's two launches of `layer` (MLCV_OPT_XTP on; they read the context's copies of the
+ * last denoise_step_kv call's inputs and the given keys / values): the attention launch (residual stream in,
+ * adaRMS, q/k/v, attention, combine, o_proj partials) and the MLP launch (residual stream,
+ * adaRMS, gate_up + GeGLU, down partials). */
+#define MLCV_OP_XT_ATTN 10
+#define MLCV_OP_XT_MLP 11
 int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
                   void* stream);
 

@@ -1,6 +1,7 @@
 """Build the gfx950 HIP library ``mlc_vla/libmlcvla_hip.so`` in-tree.
 
     python mlc-vla_amd/build.py          # compiles every csrc/*.hip and links
+    python mlc-vla_amd/build.py --trace  # also libmlcvla_hip_trace.so (XCD step phase stamps)
 
 Each translation unit is compiled for ``--offload-arch=gfx950`` only, in
 parallel, into ``mlc-vla_amd/_build/``; the shared library is written next to
@@ -69,5 +70,30 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+TRACE_LIB = os.path.join(HERE, "mlc_vla", "libmlcvla_hip_trace.so")
+
+
+def build_trace(verbose: bool = False) -> str:
+    """The library with the XCD step's phase stamps (step_xtp.hip with MLCV_XT_TRACE: every
+    workgroup of the last step's launches writes s_memrealtime at each phase boundary), for
+    ``bench.py --xt-timeline`` with ``MLCV_LIB`` naming it.  The other objects are the normal
+    build's."""
+    hipcc = _hipcc()
+    build(verbose=False)
+    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    objs = [os.path.join(BUILD, s[:-4] + ".o") for s in srcs if s != "step_xtp.hip"]
+    tobj = os.path.join(BUILD, "step_xtp_trace.o")
+    _run([hipcc, *FLAGS, "-DMLCV_XT_TRACE", "-c", os.path.join(CSRC, "step_xtp.hip"), "-o", tobj])
+    tmp = TRACE_LIB + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs, tobj, "-o", tmp])
+    os.replace(tmp, TRACE_LIB)
+    if verbose:
+        print(f"built {TRACE_LIB}")
+    return TRACE_LIB
+
+
 if __name__ == "__main__":
-    build(verbose="-q" not in sys.argv)
+    if "--trace" in sys.argv:
+        build_trace(verbose="-q" not in sys.argv)
+    else:
+        build(verbose="-q" not in sys.argv)

@@ -1805,6 +1805,24 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
       case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;
       case MLCV_OP_HEAD: MLCV_TRY(enqueue_head(c, c.mod, false, st)); break;
       case MLCV_OP_ACTION_IN: MLCV_TRY(enqueue_action_in(c, c.mod, st)); break;
+      case MLCV_OP_XT_ATTN:
+      case MLCV_OP_XT_MLP: {
+        MLCV_REQUIRE(c.xt_on, "the XCD step is off");
+        XtArgs x = c.xt;  // the inputs of a single step, as enqueue_step sets them
+        x.modp = c.mod;
+        x.nscale = c.nscale;
+        x.mask = c.mask;
+        x.cos = c.cos;
+        x.sin = c.sin;
+        x.xin = c.xin16;
+        x.L = layer;
+        MLCV_REQUIRE(keys && values, "the XCD launches need keys and values");
+        x.keys = keys;
+        x.values = vals;
+        if (op == MLCV_OP_XT_ATTN) MLCV_TRY(xt_attn_launch(x, st));
+        else MLCV_TRY(xt_mlp_launch(x, st));
+        break;
+      }
       default: MLCV_REQUIRE(false, "unknown op");
     }
   }

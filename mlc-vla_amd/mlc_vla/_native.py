@@ -10,7 +10,8 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlcvla_hip.so")
+# MLCV_LIB names another build of the library (the phase-stamp build for profiling)
+LIB_PATH = os.environ.get("MLCV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlcvla_hip.so")
 
 MLCV_DTYPE_F16 = 1
 MLCV_QUANT_NONE = 0
@@ -83,7 +84,7 @@ SIGNATURES = {
 }
 
 OPS = {"time_mod": 0, "modulation": 1, "qkv": 2, "attention": 3, "o_proj": 4, "gate_up": 5, "down": 6, "head": 7,
-       "attention_only": 8}
+       "attention_only": 8, "action_in": 9, "xt_attn": 10, "xt_mlp": 11}
 
 _lock = threading.Lock()
 _lib = None
