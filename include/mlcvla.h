@@ -112,6 +112,11 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * grow, wrapping at 2^32, and each launch compares them with wrapping arithmetic against its
  * own start value; a value just below 2^32 makes the next launches wrap. */
 #define MLCV_OPT_SYNC_WORDS 8
+/* MLCV_OPT_MASK_SKIP (default 1): the attentions of prefill and of every step form skip the
+ * 32-key chunks whose mask values are all <= -1e9.  For a row with at least one valid key their
+ * probabilities underflow to 0 in fp32, so the results are bit-identical; 0 computes them
+ * (testing). */
+#define MLCV_OPT_MASK_SKIP 9
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 
 /* Synchronize `stream` and report a persistent step that ended early (a wait between its

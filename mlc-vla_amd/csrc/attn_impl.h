@@ -506,8 +506,13 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
   for (int i = 0; i < NDT; ++i) oacc[i] = (f4){0.f, 0.f, 0.f, 0.f};
   float m_run = -1e30f, l_run = 0.f;
 
-  // logits, online softmax and O^T += V^T . P^T for one chunk resident in LDS
+  // logits, online softmax and O^T += V^T . P^T for one chunk resident in LDS.  A chunk whose
+  // 32 keys are all masked (<= -1e9, padding -inf) is skipped: for a row with any valid key its
+  // probabilities are exp(s - 1e9 - m) = 0 in fp32, so it changes neither l nor O (before the
+  // row's first valid chunk, its state is scaled by exp(-1e9 - m) = 0), and the results are
+  // bit-identical to computing it (GPU test at 800 of 968 prefix keys valid).
   auto chunk_math = [&](const AttnSmem<HD>& sk) __attribute__((always_inline)) {
+    if (!a.noskip && __all(sk.msk[lane & (KCH - 1)] <= -1e9f)) return;
     // ---- logits S^T for the 2 key tiles of 16: 6 independent accumulation chains --
     f4 acc3[2][3];
 #pragma unroll
@@ -775,7 +780,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const int bx, cons
   }
   if (!row_ok) return;
   {
-    const float inv = 1.0f / l_run;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;  // 0: every key of the row masked (all skipped)
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       h4 o4;

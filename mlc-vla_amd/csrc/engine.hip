@@ -248,6 +248,7 @@ struct Ctx {
   // MLCV_OPT_XTP = 0 turns it off); activations are per layer and XCD
   bool xt_ok = false;  // the shapes and the device allow it (decided at create)
   bool xt_on = false;  // ... and it is enabled
+  bool attn_noskip = false;  // MLCV_OPT_MASK_SKIP = 0: the attentions compute fully masked key chunks too
   XtArgs xt{};         // buffers and dims; weights filled at bind
   float* nscale = nullptr;  // [steps][2D+1] prescale of each norm's pre-scaled input
   _Float16* ain16 = nullptr;  // action_in weights in fp16 (q4 models: dequantized at bind)
@@ -457,6 +458,7 @@ int enqueue_kv_prep(Ctx& c, const float* keys, const _Float16* values, hipStream
 
 int enqueue_attn(Ctx& c, int L, const float* keys, const _Float16* values, hipStream_t st) {
   AttnArgs a{};
+  a.noskip = c.attn_noskip ? 1 : 0;
   a.q = c.q;
   a.q_ld = c.H * c.HD;
   a.cos = c.cos;
@@ -678,6 +680,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     const bool last = L == c.D - 1;
     AttnArgs pa = prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
                                     c.pf_nsplit, c.pf_kps, c.attn_ws);
+    pa.noskip = c.attn_noskip ? 1 : 0;
     MLCV_TRY(kvq_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, pa.q_scale,
                                pa.rpad, last ? nullptr : c.pqf, st));
     if (last) break;
@@ -1248,8 +1251,13 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
     MLCV_REQUIRE(value == 0 || c.xt_ok, "the XCD tensor-parallel step is not built for this configuration");
     MLCV_REQUIRE(value >= 0 && value <= 2, "XCD step option: 0, 1 or 2");
     c.xt_on = value != 0;
-    c.xt.noskip = value == 2 ? 1 : 0;
+    c.xt.noskip = value == 2 || c.attn_noskip ? 1 : 0;
     if (c.xt_on) c.pk_on = false;
+  } else if (key == MLCV_OPT_MASK_SKIP) {
+    MLCV_REQUIRE(value == 0 || value == 1, "mask skip option: 0 or 1");
+    c.attn_noskip = value == 0;
+    c.pk.noskip = c.attn_noskip ? 1 : 0;
+    c.xt.noskip = c.attn_noskip ? 1 : 0;
   } else if (key == MLCV_OPT_XTP_KEEP) {
     c.xt.ls = value != 0 ? 1 : 0;
   } else if (key == MLCV_OPT_SYNC_WORDS) {

@@ -219,6 +219,7 @@ struct AttnArgs {
   // takes every row block of the splits x, x + 8, ..., then pf.nblocks / 8 prefetch
   // workgroups, so a split's K/V is read into one XCD's L2 for all its row blocks
   int xgroup;
+  int noskip;            // 1: compute key chunks whose keys are all masked too (testing the skip)
 };
 // nsplit = prefix key splits of kps keys (a multiple of 32) + 1 split for the suffix block (Ts > 0)
 // prefix K (split hi/lo), V (transposed) and mask of `layers` consecutive layers (keys /
@@ -367,6 +368,7 @@ struct PkArgs {
   unsigned* cntm;         // [D][KV][row blocks] arrival counters of those meetings (monotonic)
   int prefetch;           // workgroups idle in the attention phase prefetch the layer's later weights
   unsigned* sink;         // null (keeps the prefetch loads)
+  int noskip;             // 1: compute key chunks whose keys are all masked too (testing the skip)
 };
 // device-scope error codes of the persistent step
 constexpr unsigned PK_ERR_TIMEOUT = 1;

@@ -543,6 +543,7 @@ __device__ __forceinline__ AttnArgs pk_attn_args(CPk& p, int L) {
   a.out = p.attn + L * p.s_attn;
   a.out_ld = p.nq;
   a.out_frag = 1;
+  a.noskip = p.noskip;
   a.nsplit = p.nsplit;
   a.kps = p.kps;
   a.rows = p.rows;

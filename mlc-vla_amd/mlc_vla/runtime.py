@@ -219,6 +219,11 @@ class VirtualMachine:
         a value just below 2**32 makes the next launches wrap them)."""
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_SYNC_WORDS, int(value) & 0xFFFFFFFF)
 
+    def set_mask_skip(self, on: bool) -> None:
+        """Skip key chunks whose mask is entirely <= -1e9 in every attention (default; the
+        results are bit-identical), or compute them (testing)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_MASK_SKIP, int(bool(on)))
+
     def set_persist_spin(self, polls: int) -> None:
         """Polls before a wait of the persistent or XCD step gives up."""
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_PERSIST_SPIN, int(polls))

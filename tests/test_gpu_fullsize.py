@@ -154,3 +154,44 @@ def test_fullsize_q4_step_vs_oracle_and_fp16():
               (np.linalg.norm(vq.astype(np.float64)) * np.linalg.norm(vf.astype(np.float64))))
     print(f"q4 step vs fp16 step: cos {c:.5f}", flush=True)
     assert c >= 0.97
+
+
+def test_masked_chunk_skip_is_bit_exact_at_800_valid():
+    """Prefill and the step attentions skip the 32-key chunks whose keys are all masked
+    (MLCV_OPT_MASK_SKIP, default on): at 800 valid of 968 prefix keys (6 of the prefill's 31 key
+    chunks), every layer's K / V and the velocity of each step form are bit-identical to the same
+    calls computing those chunks (gemma_dual.py:97-122: exp of a -1e9 logit is 0 in fp32)."""
+    cfg = Pi0Config(dtype="float16", action_horizon=50)
+    d = O.dims_from_config(cfg)
+    print("mask skip: drawing the full-size parameters on the GPU", flush=True)
+    runner = PiZeroRunner(cfg, "rocm", cuda_graph=True)
+    p = _gpu_params(O.param_specs(d), seed=7)
+    params = [p[n] for n, _ in runner.named_params]
+    rng = np.random.default_rng(4)
+    prefix = rng.standard_normal((1, 968, 2048)).astype(np.float16)
+    pm = make_prefix_mask_np(968, num_valid=800)
+    cos, sin = make_rope_np(50, 256, cfg.rope_theta, offset=800)
+    x_t = rng.standard_normal((1, 50, 32)).astype(np.float16)
+    te = O.sinusoidal_time_emb(0.7, d.ae_width).astype(np.float16)
+    dv = lambda a: runtime.tensor(a, runner.dev)  # noqa: E731
+    args = [dv(a) for a in (x_t, te, cos, sin, pm)]
+    forms = ["chain", "persistent", "xtp"]
+
+    def run(skip):
+        runner.vm.set_mask_skip(skip)
+        k, v = runner.vm["prefill"](dv(prefix), args[4], params)
+        out = {"keys": k.numpy(), "values": v.numpy()}
+        for form in forms:
+            runner.vm.set_step_form(form)
+            out[form] = runner.vm["denoise_step_kv"](k, v, *args, params).numpy()
+        runner.vm.set_step_form("xtp")
+        return out
+
+    print("mask skip: with the skip", flush=True)
+    a = run(True)
+    print("mask skip: without the skip", flush=True)
+    b = run(False)
+    runner.vm.set_mask_skip(True)
+    for name in ["keys", "values"] + forms:
+        assert np.all(np.isfinite(a[name])), name
+        np.testing.assert_array_equal(a[name], b[name], err_msg=name)
