@@ -182,10 +182,13 @@ def test_vm_embed_language(tiny):
     dict(image_size=56, patch_size=14, hidden_size=128, intermediate_size=96, num_hidden_layers=1,
          num_attention_heads=2, projection_dim=32),
     dict(num_hidden_layers=1),  # one layer of So400m/14 at 224 x 224: 256 patches, hd 72, projector to 2048
-], ids=["hd72", "hd64", "so400m_1layer"])
+    dict(),  # the whole So400m/14 tower (27 layers) + projector, as pi0.5 runs it
+], ids=["hd72", "hd64", "so400m_1layer", "so400m_27layers"])
 def test_vm_embed_image_vs_oracle(sig, tiny):
-    """vm["embed_image"] (SigLIP tower + projector) against the oracle at the reference's fp16
-    cast points (siglip_oracle, pinned to torch conv2d / layer_norm / SDPA in float64)."""
+    """vm["embed_image"] (SigLIP tower + projector, siglip.py:20-120, pi0_model.py:97-99) against
+    the oracle at the reference's fp16 cast points (siglip_oracle, pinned to torch conv2d /
+    layer_norm / SDPA in float64), up to the full 27-layer So400m/14 tower."""
+    print(f"embed_image {sig}", flush=True)
     from mlc_vla.compile import compile_model
     from mlc_vla.model.pi0 import Pi0Config, SiglipConfig
     from mlc_vla.runtime import VirtualMachine
@@ -202,6 +205,8 @@ def test_vm_embed_image_vs_oracle(sig, tiny):
     assert got.shape == (1, sc.num_patches, sc.projection_dim) and got.dtype == np.float16
     ref = S.embed_image(P, sc, img, "f16")
     g = got[0].astype(np.float64)
+    print(f"embed_image: cos {cosine(g, ref):.7f} max_abs {max_abs(g, ref):.3e} max|ref| {np.abs(ref).max():.3f}",
+          flush=True)
     assert np.all(np.isfinite(g))
     assert cosine(g, ref) >= 0.9999, cosine(g, ref)
     assert max_abs(g, ref) <= 2e-2 * float(np.abs(ref).max()), (max_abs(g, ref), float(np.abs(ref).max()))
