@@ -55,9 +55,10 @@ def parse():
     ap.add_argument("--only-op", choices=sorted(set(OPS_PER_STEP) | set(OPS_PER_STEP_CHAIN) | {"attention_only", "prefill"}),
                     default=None,
                     help="after set-up, run --op-iters launches of one op of the step and exit (for --pmc runs)")
-    ap.add_argument("--xt-timeline", action="store_true",
+    ap.add_argument("--xt-timeline", nargs="?", const="fp16", choices=["fp16", "q4"], default=None,
                     help="with MLCV_LIB naming the phase-stamp build (mlc-vla_amd/build.py --trace): run the "
-                         "step and print the XCD step's per-phase timeline as markdown, then exit")
+                         "fp16 (default) or q4f16_1 step and print the XCD step's per-phase timeline as "
+                         "markdown, then exit")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run --op-iters device copies of this many MiB and exit (counter calibration)")
     return ap.parse_args()
@@ -140,6 +141,27 @@ def xt_timeline_report(tr, depth):
                  f"A to B {np.mean(gaps[0::2]):.2f}, B to A {np.mean(gaps[1::2]):.2f}")
     lines.append(f"- the {2 * depth} layer launches, first start to last end: {total:.1f} us")
     return "\n".join(lines)
+
+
+def q4_model(cfg, dev, npar, params):
+    """The q4f16_1 model of `cfg` (compile_quant.py:71-103) on the fp16 parameters quantized on
+    the GPU: (its VM, its parameter list)."""
+    from mlc_vla import runtime
+    from mlc_vla.compile_quant import compile_model_quant
+
+    exq, qnp, qmap, quant = compile_model_quant(cfg, "rocm", None, "q4f16_1", cuda_graph=True)
+    vmq = runtime.VirtualMachine(exq, dev)
+    by_name = {n: t for (n, _), t in zip(npar, params)}
+    qparams, cache = [], {}
+    for n, _ in qnp:
+        if n.endswith(".q_weight") or n.endswith(".q_scale"):
+            base = n.rsplit(".", 1)[0]
+            if base not in cache:
+                cache[base] = quant.quantize_weight(by_name[base + ".weight"])
+            qparams.append(cache[base][0 if n.endswith(".q_weight") else 1])
+        else:
+            qparams.append(by_name[n])
+    return vmq, qparams
 
 
 def summarize_trace(path):
@@ -384,8 +406,12 @@ def main():
         lib = N.load()
         if not hasattr(lib, "mlcv_xt_trace_ptr"):
             sys.exit("--xt-timeline needs MLCV_LIB naming the phase-stamp build (mlc-vla_amd/build.py --trace)")
+        if args.xt_timeline == "q4":
+            vmt, tparams = q4_model(cfg, dev, npar, params)
+        else:
+            vmt, tparams = vm, params
         for _ in range(10):
-            vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)
+            vmt["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, tparams)
         torch.cuda.synchronize()
         lib.mlcv_xt_trace_ptr.restype = ctypes.c_void_p
         buf = np.zeros(64 * 256 * 16, np.uint64)
@@ -605,20 +631,7 @@ def main():
                            "flops": int(pf_flops), "counted": "executed: q/k/v x 18 layers, the rest x 17"}
 
     if not args.no_q4:
-        exq, qnp, qmap, quant = compile_model_quant(cfg, "rocm", None, "q4f16_1", cuda_graph=True)
-        vmq = runtime.VirtualMachine(exq, dev)
-        by_name = {n: t for (n, _), t in zip(npar, params)}
-        qparams = []
-        cache = {}
-        for n, p in qnp:
-            if n.endswith(".q_weight") or n.endswith(".q_scale"):
-                base = n.rsplit(".", 1)[0]
-                if base not in cache:
-                    cache[base] = quant.quantize_weight(by_name[base + ".weight"])
-                qparams.append(cache[base][0 if n.endswith(".q_weight") else 1])
-            else:
-                qparams.append(by_name[n])
-        del cache
+        vmq, qparams = q4_model(cfg, dev, npar, params)
         vq = vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams)
         qstep = lambda: vmq["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, qparams)  # noqa: E731
         q_ms, _ = timed(qstep, args.steps, args.warmup)

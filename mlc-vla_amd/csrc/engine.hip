@@ -1108,7 +1108,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   // XCD tensor-parallel step: the shape it is built for, on a part of 8 XCDs x 32 CUs
   {
     const char* e = std::getenv("MLCV_XTP");
-    c.xt_ok = !c.q4 && c.frag && xt_shape_ok(W1, c.F1, c.H, c.KV, hd, T, (int)P, c.A) && device_cus() == 256;
+    c.xt_ok = c.frag && xt_shape_ok(W1, c.F1, c.H, c.KV, hd, T, (int)P, c.A) && device_cus() == 256;
     c.xt_on = c.xt_ok && !(e && std::atoi(e) == 0) && !c.pk_on;
     if (c.xt_ok) {
       XtArgs& x = c.xt;
@@ -1117,6 +1117,7 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       x.P = (int)P;
       x.A = c.A;
       x.eps = cfg->rms_norm_eps;
+      x.q4 = c.q4 ? 1 : 0;
       x.spin = 1u << 22;
       const size_t D8 = (size_t)c.D * 8, TW = (size_t)T * W1;
       ALLOC(x.x, D8 * TW);

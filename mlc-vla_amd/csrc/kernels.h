@@ -421,6 +421,7 @@ struct XtArgs {
   int D, T, P, A, L;
   int ls;           // layer stride of the per-layer buffers (0 or 1)
   int noskip;       // 1: compute key chunks whose keys are all masked too (testing the skip)
+  int q4;           // the weight table holds q4f16_1 blocks (qw / qs) instead of fp16 slabs
   float eps;
   // the final reduce's outputs in the launch chain's layout (the head reads them)
   _Float16* x16;    // [T][W1]

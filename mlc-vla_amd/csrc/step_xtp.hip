@@ -84,6 +84,15 @@ typedef __attribute__((address_space(4))) const PkLin CPkLinX;
 __device__ __forceinline__ const _Float16* xt_weights(const XtArgs& a, int L, int which) {
   return ((CPkLinX*)a.lw)[(size_t)L * PK_NLIN + which].w;
 }
+// q4f16_1 models (quant.py:176-193, 301-325): per 16-row slab and 128-k chunk, a 1 KB block of
+// nibbles (lane l: row l & 15, the 32 k of quantization group l >> 4 of the chunk, as the
+// fragment-major shuffle packs them) and a 128-byte block of the 64 lanes' fp16 scales
+__device__ __forceinline__ const uint32_t* xt_qw(const XtArgs& a, int L, int which) {
+  return ((CPkLinX*)a.lw)[(size_t)L * PK_NLIN + which].qw;
+}
+__device__ __forceinline__ const _Float16* xt_qs(const XtArgs& a, int L, int which) {
+  return ((CPkLinX*)a.lw)[(size_t)L * PK_NLIN + which].qs;
+}
 
 // ---- LDS layouts (bytes) --------------------------------------------------------------
 constexpr int XT_KVB = ((int)sizeof(AttnSmem<XT_HD>) + 255) / 256 * 256;
@@ -98,6 +107,9 @@ constexpr int XA_DEN = XA_RED + 4 * 2 * 4 * 64 * 16;
 constexpr int XA_BYTES = XA_DEN + 4 * 64 * 4;
 static_assert(XA_STAGE + 4 * 16 * XT_PLD * 2 <= XA_WO && XA_WO + 16384 <= XA_KV, "launch A LDS");
 static_assert(XA_BYTES <= 160 * 1024, "launch A LDS");
+// q4: nibble blocks (1 KB per slab and 128-k chunk) at the same offsets, their scales after them
+constexpr int XA_WSC = XA_W + 16384;              // q/k/v: 2 slabs x 8 chunks; scales 2 KB
+constexpr int XA_WOSC = XA_WO + 4096;             // o_proj: 2 slabs x 2 chunks; scales 512 B
 // launch B
 constexpr int XB_GU = 0;                          // gate_up weights: 2 slabs x 32 KB
 constexpr int XB_DN = 65536;                      // down weights: 2 slabs x 16 KB
@@ -105,6 +117,10 @@ constexpr int XB_RED = XB_DN + 32768;
 constexpr int XB_DEN = XB_RED + 4 * 2 * 4 * 64 * 16;
 constexpr int XB_BYTES = XB_DEN + 4 * 64 * 4;
 static_assert(XB_BYTES <= 160 * 1024, "launch B LDS");
+constexpr int XB_GUSC = XB_GU + 16384;            // q4 gate_up: 2 slabs x 8 chunks; scales 2 KB
+constexpr int XB_DNSC = XB_DN + 8192;             // q4 down: 2 slabs x 4 chunks; scales 1 KB
+static_assert(XA_WSC + 2048 <= XA_WO && XA_WOSC + 512 <= XA_KV && XB_GUSC + 2048 <= XB_DN && XB_DNSC + 1024 <= XB_RED,
+              "q4 LDS");
 
 struct XtSh {
   unsigned base;  // this workgroup's barrier word at launch start (equal across the XCD)
@@ -191,18 +207,39 @@ __device__ __forceinline__ void xt_dma(__amdgpu_buffer_rsrc_t r, int blk, char* 
 #endif
 }
 
+// 256 bytes (64 lanes x 4 B) at byte `off` of the run into LDS at dst: two chunks' q4 scales
+__device__ __forceinline__ void xt_dma4(__amdgpu_buffer_rsrc_t r, int off, char* dst, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)dst, 4, off + lane * 4, 0, 0, 0);
+#endif
+}
+// the q4 blocks of `nch` consecutive chunks from chunk c0 of 16-row slab `slab` of a matrix of
+// kcn chunks per slab, into LDS slot `slot` of an area of `lch` chunks per slab (nibbles at wq,
+// scales at wsc); stream wave v of nv takes every nv-th 1 KB block and 256-byte scale piece
+__device__ __forceinline__ void xt_dma_q4(const uint32_t* qw, const _Float16* qs, int slab, int kcn, int c0, int nch,
+                                          char* wq, char* wsc, int slot, int lch, int v, int nv, int lane) {
+  const size_t b0 = (size_t)slab * kcn + c0;  // first block of the run
+  const __amdgpu_buffer_rsrc_t rq = dev_rsrc(qw + b0 * 256, nch * 1024);
+  const __amdgpu_buffer_rsrc_t rs = dev_rsrc(qs + b0 * 64, nch * 128);
+  for (int c = v; c < nch; c += nv) xt_dma(rq, c, wq + (slot * lch + c) * 1024, lane);
+  for (int c = 2 * v; c < nch; c += 2 * nv) xt_dma4(rs, c * 128, wsc + (slot * lch + c) * 128, lane);
+}
+
 // ---- compute waves: the skinny GEMM pieces ---------------------------------------------------
 // this wave's X fragments (fragment-major [64][K], device-scope loads): k steps ks0 .. ks0 + KPW - 1
 // of the 4 m tiles; rows past xlast read zeros (an offset past the buffer)
-template <int KPW>
+// q4 (ks0 a multiple of 4): the weights' k order, k step kk of chunk kk / 4 taking 32-k block
+// ks0 + 4 (kk / 4) + g of the lane's group g and its 8-k piece kk & 3 (perm8 before the MFMA)
+template <int KPW, bool Q4 = false>
 __device__ __forceinline__ void xt_load_x(h8 (&xf)[KPW][4], const _Float16* x, int K, int ks0, int xlast, int lane) {
-  const int r16 = lane & 15;
+  const int r16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t rx = dev_rsrc(x, (uint32_t)(64 * K * 2));
 #pragma unroll
   for (int kk = 0; kk < KPW; ++kk)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const int off = 16 * mt + r16 <= xlast ? (((ks0 + kk) * 4 + mt) * 64 + lane) * 16 : 0x7FFFFF00;
+      const int ks = Q4 ? ks0 + 4 * (kk >> 2) + g : ks0 + kk, piece = Q4 ? 16 * (kk & 3) + r16 : lane;
+      const int off = 16 * mt + r16 <= xlast ? ((ks * 4 + mt) * 64 + piece) * 16 : 0x7FFFFF00;
       xf[kk][mt] = load_dev<h8, LOC>(rx, off);
     }
 }
@@ -226,6 +263,44 @@ __device__ __forceinline__ void xt_mma(f4 (&acc)[2][4], const h8 (&xf)[KPW][4], 
     }
   }
 }
+// q4: the same product from q4 blocks in LDS (nibbles at wq, scales at wsc, lch chunks per slab):
+// chunks c0 .. c0 + KPW / 4 - 1 of slab SL0 (and of slab SL0 + 1 when nsl > 1); the other
+// slab's sums stay 0
+template <int KPW, int SL0 = 0>
+__device__ __forceinline__ void xt_mma_q4(f4 (&acc)[2][4], const h8 (&xf)[KPW][4], const char* wq, const char* wsc,
+                                          int lch, int c0, int nsl, int lane) {
+  static_assert(KPW % 4 == 0 && (SL0 == 0 || SL0 == 1), "whole 128-k chunks");
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[sl][mt] = (f4){0.f, 0.f, 0.f, 0.f};
+  const bool two = SL0 == 0 && nsl > 1;
+#pragma unroll
+  for (int c = 0; c < KPW / 4; ++c) {
+    u4 q[2] = {};
+    _Float16 sc[2] = {};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i == 1 && !two) continue;
+      const int blk = (SL0 + i) * lch + c0 + c;
+      q[i] = *reinterpret_cast<const u4*>(wq + (blk * 64 + lane) * 16);
+      sc[i] = *reinterpret_cast<const _Float16*>(wsc + (blk * 64 + lane) * 2);
+    }
+#pragma unroll
+    for (int word = 0; word < 4; ++word) {
+      const h8 a0 = dequant_word(q[0][word], sc[0]);
+      const h8 a1 = two ? dequant_word(q[1][word], sc[1]) : a0;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const h8 b = perm8(xf[4 * c + word][mt]);
+        acc[SL0][mt] = mfma16x16x32(a0, b, acc[SL0][mt]);
+        if constexpr (SL0 == 0)
+          if (two) acc[1][mt] = mfma16x16x32(a1, b, acc[1][mt]);
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ void xt_red_store(const f4 (&acc)[2][4], char* red, int w, int lane) {
   f4* r = reinterpret_cast<f4*>(red);
 #pragma unroll
@@ -554,7 +629,7 @@ __device__ __forceinline__ void xt_store_suffix(const XtArgs& a, int L, int h, c
 }
 
 // ---- launch A: layer L's attention half -----------------------------------------------------
-template <bool FIRST>
+template <bool FIRST, bool Q4>
 __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[XA_BYTES];
   __shared__ XtSh sh;
@@ -592,12 +667,15 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   } else if (v < 2) {
     for (int sl = 0; sl < nsl; ++sl) {
       const int j = s + XT_NS * sl;
-      const _Float16* base = j < 16 ? xt_weights(a, L, PK_Q) + (size_t)(16 * h + j) * 32 * 512
-                             : j < 32 ? xt_weights(a, L, PK_K) + (size_t)(j - 16) * 32 * 512
-                                      : xt_weights(a, L, PK_V) + (size_t)(j - 32) * 32 * 512;
-      const __amdgpu_buffer_rsrc_t rw = dev_rsrc(base, 32 * 1024);
+      const int which = j < 16 ? PK_Q : j < 32 ? PK_K : PK_V, slab = j < 16 ? 16 * h + j : j < 32 ? j - 16 : j - 32;
+      if constexpr (Q4) {
+        xt_dma_q4(xt_qw(a, L, which), xt_qs(a, L, which), slab, XT_W / 128, 0, XT_W / 128, lds + XA_W, lds + XA_WSC,
+                  sl, XT_W / 128, v, 2, lane);
+      } else {
+        const __amdgpu_buffer_rsrc_t rw = dev_rsrc(xt_weights(a, L, which) + (size_t)slab * 32 * 512, 32 * 1024);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xt_dma(rw, v + 2 * i, lds + XA_W + (sl * 32 + v + 2 * i) * 1024, lane);
+        for (int i = 0; i < 16; ++i) xt_dma(rw, v + 2 * i, lds + XA_W + (sl * 32 + v + 2 * i) * 1024, lane);
+      }
     }
   } else {
     xt_load_chunk<128>(R, a, L, h, ck, false, tid - XT_NC - 128);
@@ -614,9 +692,10 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   f4 acc[2][4];
   if (comp) {
     h8 xf[8][4];
-    xt_load_x<8>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
+    xt_load_x<8, Q4>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
     const float part = xt_rss_quarter(a.rss + (size_t)h * T * XT_RSS, T, w, lane);
-    xt_mma<8>(acc, xf, lds + XA_W, 32, 8 * w, nsl, lane);
+    if constexpr (Q4) xt_mma_q4<8>(acc, xf, lds + XA_W, lds + XA_WSC, XT_W / 128, 2 * w, nsl, lane);
+    else xt_mma<8>(acc, xf, lds + XA_W, 32, 8 * w, nsl, lane);
     xt_red_store(acc, lds + XA_RED, w, lane);
     reinterpret_cast<float*>(lds + XA_DEN)[w * 64 + lane] = part;
   }
@@ -701,11 +780,17 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   xt_sync();
   XT_STAMP(2 * L, 13, 0);
   if (!comp) {  // o_proj weights (slabs 2s, 2s + 1, k steps [8h, 8h + 8)) into LDS, during the attention
-    const _Float16* wo = xt_weights(a, L, PK_O);
+    if constexpr (Q4) {
+      for (int sl = 0; sl < 2; ++sl)  // chunks [2h, 2h + 2) of the 16 per slab
+        xt_dma_q4(xt_qw(a, L, PK_O), xt_qs(a, L, PK_O), 2 * s + sl, 2 * XT_W / 128, 2 * h, 2, lds + XA_WO,
+                  lds + XA_WOSC, sl, 2, v, 4, lane);
+    } else {
+      const _Float16* wo = xt_weights(a, L, PK_O);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = v + 4 * i, sl = b >> 3, kk = b & 7;
-      xt_dma(dev_rsrc(wo + ((size_t)(2 * s + sl) * 64 + 8 * h) * 512, 8 * 1024), kk, lds + XA_WO + b * 1024, lane);
+      for (int i = 0; i < 4; ++i) {
+        const int b = v + 4 * i, sl = b >> 3, kk = b & 7;
+        xt_dma(dev_rsrc(wo + ((size_t)(2 * s + sl) * 64 + 8 * h) * 512, 8 * 1024), kk, lds + XA_WO + b * 1024, lane);
+      }
     }
   }
   if (comp) {
@@ -853,9 +938,17 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
 
   // ---- 5. o_proj, row-parallel: this XCD's 256 columns of K, outputs [32 s, 32 s + 32) ------
   if (comp) {
-    h8 xf[2][4];
-    xt_load_x<2>(xf, a.attn + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_HD, XT_HD, 2 * w, T - 1, lane);
-    xt_mma<2>(acc, xf, lds + XA_WO, 8, 2 * w, 2, lane);
+    const _Float16* ab = a.attn + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_HD;
+    if constexpr (Q4) {  // 2 slabs x 2 chunks: wave w takes slab w >> 1, chunk w & 1
+      h8 xf[4][4];
+      xt_load_x<4, true>(xf, ab, XT_HD, 4 * (w & 1), T - 1, lane);
+      if (w < 2) xt_mma_q4<4, 0>(acc, xf, lds + XA_WO, lds + XA_WOSC, 2, w & 1, 1, lane);
+      else xt_mma_q4<4, 1>(acc, xf, lds + XA_WO, lds + XA_WOSC, 2, w & 1, 1, lane);
+    } else {
+      h8 xf[2][4];
+      xt_load_x<2>(xf, ab, XT_HD, 2 * w, T - 1, lane);
+      xt_mma<2>(acc, xf, lds + XA_WO, 8, 2 * w, 2, lane);
+    }
     xt_red_store(acc, lds + XA_RED, w, lane);
   }
   xt_sync();
@@ -871,6 +964,7 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
 }
 
 // ---- launch B: layer L's MLP half ----------------------------------------------------------
+template <bool Q4>
 __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[XB_BYTES];
   __shared__ XtSh sh;
@@ -896,9 +990,15 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   } else {
     const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
     // gate_up slabs 64 h + 2 s, + 1 (8 gate + 8 up rows each): 64 contiguous blocks
-    const __amdgpu_buffer_rsrc_t rg = dev_rsrc(xt_weights(a, L, PK_GU) + (size_t)(XT_FX / 8 * h + 2 * s) * 32 * 512, 64 * 1024);
+    if constexpr (Q4) {
+      for (int sl = 0; sl < 2; ++sl)
+        xt_dma_q4(xt_qw(a, L, PK_GU), xt_qs(a, L, PK_GU), XT_FX / 8 * h + 2 * s + sl, XT_W / 128, 0, XT_W / 128,
+                  lds + XB_GU, lds + XB_GUSC, sl, XT_W / 128, v, 4, lane);
+    } else {
+      const __amdgpu_buffer_rsrc_t rg = dev_rsrc(xt_weights(a, L, PK_GU) + (size_t)(XT_FX / 8 * h + 2 * s) * 32 * 512, 64 * 1024);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) xt_dma(rg, v + 4 * i, lds + XB_GU + (v + 4 * i) * 1024, lane);
+      for (int i = 0; i < 16; ++i) xt_dma(rg, v + 4 * i, lds + XB_GU + (v + 4 * i) * 1024, lane);
+    }
   }
   XT_STAMP(2 * L + 1, 1, 0);
   xt_arrive(a, h, s, comp, 1, sh);
@@ -914,22 +1014,29 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   h8 xf[8][4];
   float part = 0.f;
   if (comp) {
-    xt_load_x<8>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
+    xt_load_x<8, Q4>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
     part = xt_rss_quarter(a.rss + (size_t)h * T * XT_RSS, T, w, lane);
     xt_vm_wait<0>();
   }
   xt_sync();
   if (!comp) {  // down slabs 2 s, 2 s + 1, k steps [16 h, 16 h + 16)
     const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
+    if constexpr (Q4) {
+      for (int sl = 0; sl < 2; ++sl)  // chunks [4h, 4h + 4) of the 32 per slab
+        xt_dma_q4(xt_qw(a, L, PK_DN), xt_qs(a, L, PK_DN), 2 * s + sl, XT_F / 128, 4 * h, 4, lds + XB_DN, lds + XB_DNSC,
+                  sl, 4, v, 4, lane);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int b = v + 4 * i, sl = b >> 4, kk = b & 15;
-      xt_dma(dev_rsrc(xt_weights(a, L, PK_DN) + ((size_t)(2 * s + sl) * 128 + 16 * h) * 512, 16 * 1024), kk,
-             lds + XB_DN + b * 1024, lane);
+      for (int i = 0; i < 8; ++i) {
+        const int b = v + 4 * i, sl = b >> 4, kk = b & 15;
+        xt_dma(dev_rsrc(xt_weights(a, L, PK_DN) + ((size_t)(2 * s + sl) * 128 + 16 * h) * 512, 16 * 1024), kk,
+               lds + XB_DN + b * 1024, lane);
+      }
     }
   }
   if (comp) {
-    xt_mma<8>(acc, xf, lds + XB_GU, 32, 8 * w, 2, lane);
+    if constexpr (Q4) xt_mma_q4<8>(acc, xf, lds + XB_GU, lds + XB_GUSC, XT_W / 128, 2 * w, 2, lane);
+    else xt_mma<8>(acc, xf, lds + XB_GU, 32, 8 * w, 2, lane);
     xt_red_store(acc, lds + XB_RED, w, lane);
     reinterpret_cast<float*>(lds + XB_DEN)[w * 64 + lane] = part;
   }
@@ -968,9 +1075,10 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
 
   // ---- 3. down, row-parallel: this XCD's 512 columns of K, outputs [32 s, 32 s + 32) ---------
   h8 xd[4][4];
-  if (comp) xt_load_x<4>(xd, a.h + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_FX, XT_FX, 4 * w, T - 1, lane);
+  if (comp) xt_load_x<4, Q4>(xd, a.h + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_FX, XT_FX, 4 * w, T - 1, lane);
   if (comp) {
-    xt_mma<4>(acc, xd, lds + XB_DN, 16, 4 * w, 2, lane);
+    if constexpr (Q4) xt_mma_q4<4>(acc, xd, lds + XB_DN, lds + XB_DNSC, 4, w, 2, lane);
+    else xt_mma<4>(acc, xd, lds + XB_DN, 16, 4 * w, 2, lane);
     xt_red_store(acc, lds + XB_RED, w, lane);
   }
   xt_sync();
@@ -1030,15 +1138,21 @@ static int xt_check(const XtArgs& a) {
 
 int xt_attn_launch(const XtArgs& a, hipStream_t st) {
   MLCV_TRY(xt_check(a));
-  if (a.L == 0) xt_attn_kernel<true><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
-  else xt_attn_kernel<false><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+  if (a.q4) {
+    if (a.L == 0) xt_attn_kernel<true, true><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+    else xt_attn_kernel<false, true><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+  } else {
+    if (a.L == 0) xt_attn_kernel<true, false><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+    else xt_attn_kernel<false, false><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+  }
   MLCV_HIP(hipGetLastError());
   return 0;
 }
 
 int xt_mlp_launch(const XtArgs& a, hipStream_t st) {
   MLCV_TRY(xt_check(a));
-  xt_mlp_kernel<<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+  if (a.q4) xt_mlp_kernel<true><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
+  else xt_mlp_kernel<false><<<XT_NX * XT_NS, XT_NT, 0, st>>>(a);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

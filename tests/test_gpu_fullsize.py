@@ -4,8 +4,9 @@
   tokens, then the 10-step in-graph Euler loop of the pi0.5 action expert), against the
   float32 oracle: every layer's prefix K / V, then the actions (pi0_model.py:128-194,
   gemma_dual.py:398-415; the pad recipe of compare_pad.py:62-91);
-- the q4f16_1 ``denoise_step_kv`` at the full shape, against the oracle on the same
-  dequantized weights and against the fp16 step (compare_quant.py:76-117, cos >= 0.97 at :115).
+- the q4f16_1 ``denoise_step_kv`` at the full shape (the XCD step, and the launch chain it is
+  checked against), against the oracle on the same dequantized weights and against the fp16
+  step (compare_quant.py:76-117, cos >= 0.97 at :115).
 
 Weights are 0.02 N(0, 1) drawn on the GPU with a seeded torch generator (drawing the 2.4 G
 parameters with numpy on the host would take minutes); the oracle reads the same fp16 values.
@@ -138,8 +139,16 @@ def test_fullsize_q4_step_vs_oracle_and_fp16():
     cos, sin = make_rope_np(50, 256, 10_000.0, offset=968)
     dv = lambda a: runtime.tensor(a, runner.dev)  # noqa: E731
     args = [dv(a) for a in (keys, values, x_t, te, cos, sin, pm)]
-    print("full-size q4 step: GPU q4 and fp16 steps", flush=True)
-    vq = vm["denoise_step_kv"](*args, qparams).numpy()
+    print("full-size q4 step: GPU q4 (XCD step and launch chain) and fp16 steps", flush=True)
+    vq = vm["denoise_step_kv"](*args, qparams).numpy()  # the default form: the XCD step
+    vm.set_step_form("chain")
+    vqc = vm["denoise_step_kv"](*args, qparams).numpy()
+    vm.set_step_form("xtp")
+    cq = float(np.dot(vq.ravel().astype(np.float64), vqc.ravel()) /
+               (np.linalg.norm(vq.astype(np.float64)) * np.linalg.norm(vqc.astype(np.float64))))
+    mq = float(np.max(np.abs(vq.astype(np.float64) - vqc)))
+    print(f"q4 XCD step vs q4 launch chain: cos {cq:.8f} max_abs {mq:.3e}", flush=True)
+    assert np.all(np.isfinite(vq)) and cq >= 0.99999 and mq <= 5e-3, (cq, mq)
     vf = runner.vm["denoise_step_kv"](*args, fparams).numpy()
     ae_names = [n for n, _ in specs if _is_ae(n)]
     host = _host(p, ae_names)
