@@ -143,6 +143,39 @@ def xt_timeline_report(tr, depth):
     return "\n".join(lines)
 
 
+def f32_chunk_timing(dev):
+    """The float32 model (Pi0Config(dtype="float32")) of the 2-layer configuration: one chunk
+    (prefill + the 10-step loop through PiZeroRunner.sample_graph), weights 0.02 N(0,1)."""
+    import numpy as np
+    import torch
+
+    from mlc_vla import runtime
+    from mlc_vla.model.pi0 import Pi0Config
+    from mlc_vla.sample import PiZeroRunner
+
+    cfg = Pi0Config(paligemma_variant="tiny_vlm", action_expert_variant="tiny_action", image_keys=(),
+                    max_token_len=32, action_horizon=8, action_dim=32, num_denoise_steps=10, dtype="float32")
+    runner = PiZeroRunner(cfg, "rocm")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    params = [runtime.Tensor(torch.randn(sp.shape, generator=g, device="cuda").mul_(0.02), "float32")
+              for _, sp in runner.named_params]
+    rng = np.random.default_rng(6)
+    prefix = rng.standard_normal((1, cfg.prefix_len, cfg.vlm.width)).astype(np.float32)
+    noise = rng.standard_normal((1, 8, 32)).astype(np.float32)
+    for _ in range(3):
+        runner.sample_graph(params, prefix, noise=noise)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        runner.sample_graph(params, prefix, noise=noise)
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return {"ms_p50": round(sorted(ts)[len(ts) // 2], 3), "iters": len(ts),
+            "workload": "2-layer model, fp32 (prefix 32, horizon 8, action 32): prefill + 10 Euler steps "
+                        "through PiZeroRunner.sample_graph, host time per chunk incl. transfers"}
+
+
 def q4_model(cfg, dev, npar, params):
     """The q4f16_1 model of `cfg` (compile_quant.py:71-103) on the fp16 parameters quantized on
     the GPU: (its VM, its parameter list)."""
@@ -644,6 +677,10 @@ def main():
                                "cos_vs_fp16": round(cosq, 5), "cold_p50_us": round(_pct(q_cold, 0.5), 1),
                                "cold_p90_us": round(_pct(q_cold, 0.9), 1)}
         del vmq, qparams
+
+    # the float32 model at the 2-layer CPU-sized configuration (prefix expert 256 / 1024, action
+    # expert 128 / 512, 2 heads of 64, prefix 32, horizon 8): prefill + 10 Euler steps
+    out["f32_2layer_chunk"] = f32_chunk_timing(dev)
 
     if not args.no_embed:
         out["embed_image"] = embed_image_timing(cfg, dev)

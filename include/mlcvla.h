@@ -33,6 +33,12 @@ extern "C" {
 #endif
 
 #define MLCV_DTYPE_F16 1
+/* float32 models (Pi0Config(dtype="float32"), pi0_config.py:97): prefill, denoise_step_kv,
+ * denoise_loop_kv and mlcv_chunk in float32 throughout (values, prefix_embs, x_t and time
+ * embeddings are then float32 too), on generic kernels meant for the small shapes the
+ * reference runs in float32; the other entry points and options of the step forms report that
+ * they are not built for them. */
+#define MLCV_DTYPE_F32 2
 #define MLCV_QUANT_NONE 0
 #define MLCV_QUANT_Q4F16_1 1
 
@@ -53,7 +59,7 @@ typedef struct mlcv_config {
   int32_t num_steps;     /* num_denoise_steps (10)                       */
   float rms_norm_eps;    /* 1e-6                                         */
   float rope_theta;      /* 10000                                        */
-  int32_t dtype;         /* MLCV_DTYPE_F16                               */
+  int32_t dtype;         /* MLCV_DTYPE_F16 or MLCV_DTYPE_F32             */
   int32_t quant;         /* MLCV_QUANT_NONE or MLCV_QUANT_Q4F16_1        */
 } mlcv_config;
 

@@ -817,6 +817,10 @@ using namespace mlcv;
 
 struct mlcv_ctx {
   Ctx c;
+  F32Model* f32 = nullptr;  // a float32 model: the generic fp32 kernels of model_f32.hip
+  ~mlcv_ctx() {
+    if (f32) f32_destroy(f32);
+  }
 };
 
 // ---- scratch of mlcv_linear_noalloc -------------------------------------------------------
@@ -876,7 +880,25 @@ int mlcv_param_count(const mlcv_config* cfg, int32_t* count) {
 
 int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   MLCV_REQUIRE(cfg && out, "null argument");
-  MLCV_REQUIRE(cfg->dtype == MLCV_DTYPE_F16, "only float16 models are supported on gfx950 in this build");
+  MLCV_REQUIRE(cfg->dtype == MLCV_DTYPE_F16 || cfg->dtype == MLCV_DTYPE_F32, "dtype: MLCV_DTYPE_F16 or MLCV_DTYPE_F32");
+  if (cfg->dtype == MLCV_DTYPE_F32) {
+    MLCV_REQUIRE(cfg->quant == MLCV_QUANT_NONE, "float32 models are not quantized");
+    MLCV_REQUIRE(cfg->depth >= 1 && cfg->prefix_len >= 1 && cfg->suffix_len >= 1 && cfg->num_steps >= 1 &&
+                     cfg->num_heads >= 1 && cfg->num_kv_heads >= 1,
+                 "depth / lengths / steps / heads must be positive");
+    auto* h = new (std::nothrow) mlcv_ctx();
+    if (!h) {
+      set_error("out of host memory");
+      return -1;
+    }
+    h->c.cfg = *cfg;
+    if (const int rc = f32_create(*cfg, &h->f32)) {
+      delete h;
+      return rc;
+    }
+    *out = h;
+    return 0;
+  }
   MLCV_REQUIRE(cfg->quant == MLCV_QUANT_NONE || cfg->quant == MLCV_QUANT_Q4F16_1, "unknown quantization");
   const int hd = cfg->head_dim;
   MLCV_REQUIRE(hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256, "head_dim must be 16/32/64/128/256");
@@ -1241,6 +1263,11 @@ int mlcv_destroy(mlcv_ctx* ctx) {
 
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
   MLCV_REQUIRE(ctx, "null context");
+  if (ctx->f32) {  // the float32 model runs eager launches; the step-form options do not apply
+    MLCV_REQUIRE(key == MLCV_OPT_USE_GRAPH || key == MLCV_OPT_HOIST_MODULATION || key == MLCV_OPT_MASK_SKIP,
+                 "this option is not built for float32 models");
+    return 0;
+  }
   Ctx& c = ctx->c;
   if (key == MLCV_OPT_USE_GRAPH) c.use_graph = value != 0;
   else if (key == MLCV_OPT_HOIST_MODULATION) c.hoist = value != 0;
@@ -1285,6 +1312,14 @@ int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
 
 int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void* stream) {
   MLCV_REQUIRE(ctx, "null argument");
+  if (ctx->f32) {
+    MLCV_REQUIRE(ptrs, "null argument");
+    int32_t want = 0;
+    MLCV_TRY(mlcv_param_count(&ctx->c.cfg, &want));
+    MLCV_REQUIRE(count == want, "parameter count mismatch (expected " + std::to_string(want) + ")");
+    MLCV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+    return f32_bind(*ctx->f32, ptrs, count);
+  }
   Ctx& c = ctx->c;
   // unbound until this call has finished: any failure below (a rejected list included) leaves
   // the context refusing every entry point ("parameters not bound") instead of pointing at
@@ -1489,6 +1524,7 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
 int mlcv_prefill(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
                  void* stream) {
   MLCV_REQUIRE(ctx && prefix_embs && prefix_mask && keys && values, "null argument");
+  if (ctx->f32) return f32_prefill(*ctx->f32, prefix_embs, prefix_mask, keys, values, reinterpret_cast<hipStream_t>(stream));
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1519,6 +1555,7 @@ int mlcv_embed_language(const int32_t* input_ids, int32_t n, const void* table, 
 int mlcv_denoise_step(mlcv_ctx* ctx, const void* prefix_embs, const void* x_t, const void* time_emb, float* v_out,
                       void* stream) {
   MLCV_REQUIRE(ctx && prefix_embs && x_t && time_emb && v_out, "null argument");
+  MLCV_REQUIRE(!ctx->f32, "the joint forward (denoise_step) is not built for float32 models");
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1544,6 +1581,9 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
                          void* stream) {
   MLCV_REQUIRE(ctx && keys && values && x_t && time_emb && suffix_cos && suffix_sin && prefix_mask && v_out,
                "null argument");
+  if (ctx->f32)
+    return f32_step(*ctx->f32, keys, values, x_t, time_emb, suffix_cos, suffix_sin, prefix_mask, v_out,
+                    reinterpret_cast<hipStream_t>(stream));
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1567,6 +1607,9 @@ int mlcv_denoise_loop_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
                          const float* prefix_mask, float* x_out, void* stream) {
   MLCV_REQUIRE(ctx && keys && values && x0 && time_embs && suffix_cos && suffix_sin && prefix_mask && x_out,
                "null argument");
+  if (ctx->f32)
+    return f32_loop(*ctx->f32, keys, values, x0, time_embs, suffix_cos, suffix_sin, prefix_mask, x_out,
+                    reinterpret_cast<hipStream_t>(stream));
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1584,6 +1627,9 @@ int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask,
                const void* time_embs, const float* suffix_cos, const float* suffix_sin, float* x_out, void* stream) {
   MLCV_REQUIRE(ctx && prefix_embs && prefix_mask && x0 && time_embs && suffix_cos && suffix_sin && x_out,
                "null argument");
+  if (ctx->f32)
+    return f32_chunk(*ctx->f32, prefix_embs, prefix_mask, x0, time_embs, suffix_cos, suffix_sin, x_out,
+                     reinterpret_cast<hipStream_t>(stream));
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1606,6 +1652,7 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
   MLCV_REQUIRE(ctx, "null context");
   Ctx& c = ctx->c;
   MLCV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  if (ctx->f32) return 0;  // no bounded device-side waits in the float32 model
   // every error word is read and reset before returning, so that one cause does not leave
   // another's words inconsistent for the calls after this sync
   std::string why;
@@ -1648,6 +1695,7 @@ int mlcv_sync(mlcv_ctx* ctx, void* stream) {
 
 int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_t bytes, void* stream) {
   MLCV_REQUIRE(ctx && out, "null argument");
+  MLCV_REQUIRE(!ctx->f32, "step probes are not built for float32 models");
   Ctx& c = ctx->c;
   // the persistent and XCD steps keep every layer's intermediates; the launch chain reuses one
   // set of buffers, which hold the outputs of the last operation run (layer 0 names them)
@@ -1779,6 +1827,7 @@ int mlcv_step_probe(mlcv_ctx* ctx, int32_t what, int32_t layer, void* out, size_
 int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const float* keys, const void* values,
                   void* stream) {
   MLCV_REQUIRE(ctx && iters >= 0, "bad argument");
+  MLCV_REQUIRE(!ctx->f32, "step ops are not built for float32 models");
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   MLCV_REQUIRE(layer >= 0 && layer < c.D, "layer out of range");

@@ -4,6 +4,8 @@
 #include "common.h"
 #include "plan.h"
 
+struct mlcv_config;  // include/mlcvla.h
+
 namespace mlcv {
 
 // ---------------------------------------------------------------------------
@@ -311,6 +313,20 @@ int euler_init_launch(const float* x0, float* x32, _Float16* x16, int n, hipStre
 // the weights of its next task before it waits for the previous phase, and the phases
 // meet through per-workgroup progress words instead of kernel boundaries.
 // ---------------------------------------------------------------------------
+// The float32 model (model_f32.hip): generic fp32 kernels for prefill / step / loop / chunk.
+struct F32Model;
+int f32_create(const ::mlcv_config& cfg, F32Model** out);
+void f32_destroy(F32Model* m);
+int f32_bind(F32Model& m, const void* const* ptrs, int count);
+int f32_prefill(F32Model& m, const void* prefix_embs, const float* prefix_mask, float* keys, void* values,
+                hipStream_t st);
+int f32_step(F32Model& m, const float* keys, const void* values, const void* x_t, const void* time_emb,
+             const float* cos, const float* sin, const float* prefix_mask, float* v_out, hipStream_t st);
+int f32_loop(F32Model& m, const float* keys, const void* values, const float* x0, const void* time_embs,
+             const float* cos, const float* sin, const float* prefix_mask, float* x_out, hipStream_t st);
+int f32_chunk(F32Model& m, const void* prefix_embs, const float* prefix_mask, const float* x0, const void* time_embs,
+              const float* cos, const float* sin, float* x_out, hipStream_t st);
+
 struct PkLin {
   const _Float16* w;     // fragment-major 16-row slabs (wf_shuffle_launch), fp16, or
   const uint32_t* qw;    // q4f16_1 blocks (wf_shuffle_q4_launch)

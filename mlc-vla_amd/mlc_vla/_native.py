@@ -14,6 +14,7 @@ import threading
 LIB_PATH = os.environ.get("MLCV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlcvla_hip.so")
 
 MLCV_DTYPE_F16 = 1
+MLCV_DTYPE_F32 = 2
 MLCV_QUANT_NONE = 0
 MLCV_QUANT_Q4F16_1 = 1
 MLCV_OPT_USE_GRAPH = 1

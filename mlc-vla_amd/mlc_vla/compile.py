@@ -37,11 +37,17 @@ def resolve_cublas(cublas, target_kind: str) -> bool:
     return False
 
 
-def check_config(config) -> None:
-    if config.dtype != "float16":
-        raise NotImplementedError(
-            f"dtype {config.dtype!r}: the gfx950 kernels compute the float16 model "
-            "(construct Pi0Config(dtype='float16'))")
+def check_config(config, functions=None, quant=None) -> None:
+    """float16 models run every function; float32 models (the reference's default dtype,
+    pi0_config.py:97) run the M1 functions on generic float32 kernels, unquantized."""
+    if config.dtype not in ("float16", "float32"):
+        raise NotImplementedError(f"dtype {config.dtype!r}: float16 or float32")
+    if config.dtype == "float32":
+        if quant is not None:
+            raise NotImplementedError("q4f16_1 quantizes the float16 model (construct Pi0Config(dtype='float16'))")
+        extra = [f for f in (functions if functions is not None else KV_FUNCS) if f not in KV_FUNCS]
+        if extra:
+            raise NotImplementedError(f"functions {extra} are built for float16 models only (float32: {KV_FUNCS})")
     if config.attn_logits_dtype != "float32":
         raise NotImplementedError("attn_logits_dtype must be 'float32' in this build")
 
@@ -52,7 +58,7 @@ def compile_model(config, target: str = "rocm", functions=None, cuda_graph: bool
     embed_language, denoise_step, prefill, denoise_step_kv and denoise_loop_kv; the default is
     the M1 functions (prefill, denoise_step_kv, denoise_loop_kv)."""
     _target_kind(target)
-    check_config(config)
+    check_config(config, functions)
     resolve_cublas(cublas, "rocm")
     funcs = tuple(functions) if functions is not None else KV_FUNCS
     unknown = [f for f in funcs if f not in BUILT_FUNCS]

@@ -25,7 +25,7 @@ def compile_model_quant(config, target: str, functions, quant_name: str, cuda_gr
                         hoist_modulation: bool = True):
     """Return ``(executable, q_named_params, quant_map, quant)`` (compile_quant.py:46-68)."""
     _target_kind(target)
-    check_config(config)
+    check_config(config, functions, quant_name)
     quant = get_quant(quant_name)
     if not quant.supported:
         raise NotImplementedError(f"preset {quant_name}: only q4f16_1 is built on gfx950")

@@ -141,7 +141,7 @@ class Executable:
             depth=vlm.depth, num_heads=vlm.num_heads, num_kv_heads=vlm.num_kv_heads, head_dim=vlm.head_dim,
             prefix_len=c.prefix_len, suffix_len=c.suffix_len, action_dim=c.action_dim,
             num_steps=c.num_denoise_steps, rms_norm_eps=c.rms_norm_eps, rope_theta=c.rope_theta,
-            dtype=N.MLCV_DTYPE_F16,
+            dtype=N.MLCV_DTYPE_F32 if c.dtype == "float32" else N.MLCV_DTYPE_F16,
             quant=N.MLCV_QUANT_Q4F16_1 if self.quant == "q4f16_1" else N.MLCV_QUANT_NONE,
         )
 

@@ -136,3 +136,95 @@ def test_tiny_actions_fixture(tiny_model):
     graph = runner.sample_graph(params, prefix, noise=noise)
     _tol(graph, fx["actions_graph"])
     _tol(graph, fx["actions_graph_f64"])
+
+
+# ---- the float32 model (Pi0Config(dtype="float32"), the reference's default dtype) ----------
+# The fixtures are the float32 oracle (and its float64 twin) on float32 weights; the float32
+# model computes with those weights unrounded, so it is held to float32 accuracy: the tolerance
+# the CPU fixture test gives two float32 BLAS builds (tests/test_golden.py: rtol 2e-4, atol
+# 2e-5 of the largest value), which fp16 weights miss by two orders of magnitude.
+def _f32_tol(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(got)), what
+    np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-5 * float(np.abs(ref).max()), err_msg=what)
+    assert cosine(got, ref) >= 0.9999999, (what, cosine(got, ref))
+
+
+@pytest.fixture(scope="module")
+def tiny_f32():
+    cfg = Pi0Config(**{**TINY_KWARGS, "dtype": "float32"})
+    runner = PiZeroRunner(cfg, "rocm")
+    specs, params, prefix, noise = G.tiny_inputs()
+    assert [n for n, _ in specs] == [n for n, _ in runner.named_params]
+    dev_params = runner.to_params([params[n].astype(np.float32) for n, _ in runner.named_params])
+    return cfg, runner, dev_params, prefix, noise, _load("tiny_e2e.npz")
+
+
+def test_tiny_f32_prefill_and_step_fixture(tiny_f32):
+    print("golden tiny float32 model: prefill, denoise_step_kv t=1", flush=True)
+    cfg, runner, params, prefix, noise, fx = tiny_f32
+    d = G.TINY_DIMS
+    dev = lambda a: runtime.tensor(np.ascontiguousarray(a), runner.dev)  # noqa: E731
+    pm = make_prefix_mask_np(cfg.prefix_len)
+    k, v = runner.vm["prefill"](dev(prefix.astype(np.float32)), dev(pm), params)
+    assert k.dtype == "float32" and v.dtype == "float32"
+    for L in range(2):
+        _f32_tol(k.numpy()[L], fx["keys"][L], f"keys[{L}]")
+        _f32_tol(v.numpy()[L], fx["values"][L], f"values[{L}]")
+    cos, sin = G.O.make_rope_np(d.suffix_len, d.head_dim, d.theta, offset=d.prefix_len)
+    te = G.O.sinusoidal_time_emb(1.0, d.ae_width).astype(np.float32)
+    v1 = runner.vm["denoise_step_kv"](k, v, dev(noise.astype(np.float32)), dev(te), dev(cos), dev(sin), dev(pm), params)
+    _f32_tol(v1.numpy(), fx["v1"], "v1")
+    _f32_tol(v1.numpy(), fx["v1_f64"], "v1 (float64 truth)")
+
+
+def test_tiny_f32_actions_fixture(tiny_f32):
+    print("golden tiny float32 model: sample / sample_graph", flush=True)
+    _, runner, params, prefix, noise, fx = tiny_f32
+    host = runner.sample(params, prefix, noise=noise, num_steps=10)
+    _f32_tol(host, fx["actions"], "actions")
+    _f32_tol(host, fx["actions_f64"], "actions (float64 truth)")
+    graph = runner.sample_graph(params, prefix, noise=noise)
+    _f32_tol(graph, fx["actions_graph"], "actions_graph")
+    _f32_tol(graph, fx["actions_graph_f64"], "actions_graph (float64 truth)")
+
+
+def test_dummy_f32_model_vs_oracle():
+    """The reference's dummy configuration (pi0_config.py: paligemma and action expert
+    "dummy") in float32 against the float32 oracle on the same weights: sample and sample_graph."""
+    from conftest import DUMMY_KWARGS
+    from oracle import pi0_oracle as O
+
+    cfg = Pi0Config(**{**DUMMY_KWARGS, "dtype": "float32"})
+    d = O.dims_from_config(cfg)
+    print(f"dummy float32 model: {d}", flush=True)
+    runner = PiZeroRunner(cfg, "rocm")
+    p = O.make_params(O.param_specs(d), 3, "float32")
+    params = runner.to_params([p[n] for n, _ in runner.named_params])
+    rng = np.random.default_rng(4)
+    prefix = rng.standard_normal((1, cfg.prefix_len, cfg.vlm.width)).astype(np.float32)
+    noise = rng.standard_normal((1, cfg.action_horizon, cfg.action_dim)).astype(np.float32)
+    got = runner.sample(params, prefix, noise=noise, num_steps=cfg.num_denoise_steps)
+    ref = O.sample(p, d, prefix, noise, O.Prec("f32"))
+    _f32_tol(got, ref, "dummy sample")
+    graph = runner.sample_graph(params, prefix, noise=noise)
+    refg = O.sample(p, d, prefix, noise, O.Prec("f32"), graph=True)
+    _f32_tol(graph, refg, "dummy sample_graph")
+
+
+def test_f32_tolerance_rejects_the_fp16_model(tiny_model):
+    """The float32 tolerance above discriminates: the float16 model (the same weights rounded
+    to fp16) passes the action tolerance on this fixture but not the float32 one."""
+    cfg, runner, params, prefix, noise, fx = tiny_model
+    d = G.TINY_DIMS
+    dev = lambda a: runtime.tensor(np.ascontiguousarray(a), runner.dev)  # noqa: E731
+    pm = make_prefix_mask_np(cfg.prefix_len)
+    k, v = runner.vm["prefill"](dev(prefix.astype(np.float16)), dev(pm), params)
+    cos, sin = G.O.make_rope_np(d.suffix_len, d.head_dim, d.theta, offset=d.prefix_len)
+    te = G.O.sinusoidal_time_emb(1.0, d.ae_width).astype(np.float16)
+    v1 = runner.vm["denoise_step_kv"](k, v, dev(noise.astype(np.float16)), dev(te), dev(cos), dev(sin), dev(pm),
+                                      params).numpy()
+    _tol(v1, fx["v1"])
+    with pytest.raises(AssertionError):
+        _f32_tol(v1, fx["v1"], "fp16 model v1")

@@ -101,10 +101,24 @@ def test_default_spec_signatures():
     assert s["prefill"]["prefix_embs"].shape == (1, 968, 2048)
 
 
-def test_compile_rejects_cpu_targets_and_fp32():
+def test_compile_targets_and_dtypes():
+    """CPU targets are refused; float32 models (the reference's default dtype) build the M1
+    functions, float16 ones every function, and q4f16_1 quantizes float16 models only."""
+    from mlc_vla.compile_quant import compile_model_quant
+
     with pytest.raises(NotImplementedError):
         compile_model(Pi0Config(**DUMMY_KWARGS), "c")
+    f32 = Pi0Config(**{**DUMMY_KWARGS, "dtype": "float32"})
+    ex, npar = compile_model(f32, "rocm")
+    assert ex.functions == ("prefill", "denoise_step_kv", "denoise_loop_kv")
+    assert all(sp.dtype == "float32" for _, sp in npar)
+    assert ex.c_config().dtype == 2  # MLCV_DTYPE_F32
     with pytest.raises(NotImplementedError):
-        compile_model(Pi0Config(**{**DUMMY_KWARGS, "dtype": "float32"}), "rocm")
+        compile_model(f32, "rocm", functions=["denoise_step"])
+    with pytest.raises(NotImplementedError):
+        compile_model_quant(f32, "rocm", None, "q4f16_1")
+    with pytest.raises(NotImplementedError):
+        compile_model(Pi0Config(**{**DUMMY_KWARGS, "dtype": "bfloat16"}), "rocm")
     ex, npar = compile_model(Pi0Config(**DUMMY_KWARGS), "rocm")
     assert len(npar) == 18 * 4 + 11 and ex.functions == ("prefill", "denoise_step_kv", "denoise_loop_kv")
+    assert ex.c_config().dtype == 1  # MLCV_DTYPE_F16
