@@ -175,6 +175,15 @@ struct Ctx {
   // the prefill attention's q in fragment order (q_frag_launch; head dims a multiple of 64,
   // else null and the attention ropes the raw q in its loader)
   _Float16* pqf = nullptr;
+  // the head_dim-256 prefill attention (attn_prefill.hip: per-chunk K/V images from the layer's
+  // writer, 32-row MFMA tiles, splits balanced over the valid chunks and combined in-kernel);
+  // MLCV_PF_ATTN=0 runs the general attention instead
+  bool pa_on = false;
+  PaPlan pa{};
+  char* pa_img = nullptr;
+  _Float16 *pa_qf = nullptr, *pa_part = nullptr;
+  float* pa_ml = nullptr;
+  unsigned* pa_ctr = nullptr;
   // the joint forward (denoise_step): suffix RoPE tables at positions P..P+T-1, all-valid mask
   float *m0cos = nullptr, *m0sin = nullptr, *m0mask = nullptr;
   // workspaces
@@ -649,6 +658,28 @@ void gemm_ws_args(const Ctx& c, TgArgs& g) {
   g.meet_polls = c.meet_polls;
 }
 
+PaArgs pa_args(const PaPlan& plan, const _Float16* qf, const char* img, const float* mask, _Float16* out, int out_ld,
+               int P, int H, int KV, _Float16* part, float* ml, unsigned* ctr, bool noskip) {
+  PaArgs a{};
+  a.qf = qf;
+  a.img = img;
+  a.mask = mask;
+  a.out = out;
+  a.out_ld = out_ld;
+  a.P = P;
+  a.H = H;
+  a.KV = KV;
+  a.rows = P * (H / KV);
+  a.nch = plan.nch;
+  a.nrb = plan.nrb;
+  a.nsplit = plan.nsplit;
+  a.part = part;
+  a.part_ml = ml;
+  a.ctr = ctr;
+  a.noskip = noskip ? 1 : 0;
+  return a;
+}
+
 // ---- prefill: expert-0 over the prefix, K/V written per layer ----------------
 int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
   const int W0 = c.W0, P = c.P, HD = c.HD;
@@ -678,14 +709,22 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     // the cache slices of this layer, and (but for the last layer, whose attention feeds no
     // output) q roped, scaled and split into the attention's fragment order, in one launch
     const bool last = L == c.D - 1;
-    AttnArgs pa = prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
-                                    c.pf_nsplit, c.pf_kps, c.attn_ws);
-    pa.noskip = c.attn_noskip ? 1 : 0;
-    MLCV_TRY(kvq_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, pa.q_scale,
-                               pa.rpad, last ? nullptr : c.pqf, st));
-    if (last) break;
-    pa.qf = c.pqf;  // null: the attention ropes the raw q in its loader
-    MLCV_TRY(attn_launch(pa, st));
+    if (c.pa_on && !last) {
+      MLCV_TRY(pa_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.H, c.KV, 1.0f / std::sqrt((float)HD),
+                                kL, vL, c.pa, c.pa_img, c.pa_qf, 0, st));
+      MLCV_TRY(pa_attn_launch(pa_args(c.pa, c.pa_qf, c.pa_img, c.mask, c.pctx, c.H * HD, P, c.H, c.KV, c.pa_part,
+                                      c.pa_ml, c.pa_ctr, c.attn_noskip),
+                              st));
+    } else {
+      AttnArgs pa = prefill_attn_args(c.pqkv, nqkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, c.mask, c.pctx,
+                                      c.pf_nsplit, c.pf_kps, c.attn_ws);
+      pa.noskip = c.attn_noskip ? 1 : 0;
+      MLCV_TRY(kvq_writer_launch(c.pqkv, nqkv, nq, nq + nkv, c.pcos, c.psin, P, c.H, c.KV, HD, kL, vL, pa.q_scale,
+                                 pa.rpad, last ? nullptr : c.pqf, st));
+      if (last) break;
+      pa.qf = c.pqf;  // null: the attention ropes the raw q in its loader
+      MLCV_TRY(attn_launch(pa, st));
+    }
     TgArgs o{};
     o.a = c.pctx;
     o.lda = nq;
@@ -989,6 +1028,22 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.pqkv, P * (nq + 2 * nkv));
   ALLOC(c.pctx, P * nq);
   if (hd % 64 == 0) ALLOC(c.pqf, q_frag_halfs(c.KV, (int)((P * (c.H / c.KV) + 63) / 64 * 64), hd));
+  {
+    const char* e = std::getenv("MLCV_PF_ATTN");
+    c.pa_on = pa_supported(hd, c.P, c.H, c.KV) && !(e && std::atoi(e) == 0);
+  }
+  if (c.pa_on) {
+    c.pa = pa_plan(c.P, c.H, c.KV);
+    ALLOC(c.pa_img, c.pa.img_bytes);
+    ALLOC(c.pa_qf, c.pa.qf_halfs);
+    ALLOC(c.pa_part, c.pa.part_halfs);
+    ALLOC(c.pa_ml, c.pa.ml_floats);
+    ALLOC(c.pa_ctr, c.pa.counters);
+    if (hipMemset(c.pa_ctr, 0, c.pa.counters * sizeof(unsigned)) != hipSuccess) {
+      set_error("prefill attention counters: hipMemset failed");
+      return fail(-1);
+    }
+  }
   ALLOC(c.ph, P * c.F0);
   ALLOC(c.pcos, P * hd / 2);
   ALLOC(c.psin, P * hd / 2);
@@ -1975,6 +2030,26 @@ int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const 
   MLCV_REQUIRE(q && cos && sin && keys && values && out && P > 0 && H > 0 && KV > 0 && hd > 0, "bad argument");
   MLCV_REQUIRE(q_ld >= H * hd && q_ld % 8 == 0, "q row stride");
   const int rows = P * (H / KV);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const char* pe = std::getenv("MLCV_PF_ATTN");
+  if (pa_supported(hd, P, H, KV) && !(pe && std::atoi(pe) == 0)) {
+    // the prefill's head_dim-256 attention: chunk images and q fragments from the cache slices
+    const PaPlan plan = pa_plan(P, H, KV);
+    auto up = [](size_t bytes) { return (bytes + 255) / 256 * 64; };  // floats, 256-byte multiples
+    const size_t o_img = 0, o_qf = o_img + up(plan.img_bytes), o_part = o_qf + up(plan.qf_halfs * 2),
+                 o_ml = o_part + up(plan.part_halfs * 2), n = o_ml + up(plan.ml_floats * 4);
+    std::lock_guard<std::mutex> lk(g_scratch.mu);
+    MLCV_TRY(scratch_reserve(n, plan.counters));
+    float* ws = g_scratch.ws;
+    char* img = reinterpret_cast<char*>(ws + o_img);
+    _Float16* qf = reinterpret_cast<_Float16*>(ws + o_qf);
+    MLCV_TRY(pa_writer_launch(reinterpret_cast<const _Float16*>(q), q_ld, 0, 0, cos, sin, P, H, KV,
+                              1.0f / std::sqrt((float)hd), const_cast<float*>(keys),
+                              reinterpret_cast<_Float16*>(const_cast<void*>(values)), plan, img, qf, 1, st));
+    return pa_attn_launch(pa_args(plan, qf, img, mask, reinterpret_cast<_Float16*>(out), H * hd, P, H, KV,
+                                  reinterpret_cast<_Float16*>(ws + o_part), ws + o_ml, g_scratch.counters, false),
+                          st);
+  }
   int nsplit = 1, kps = 32;
   attn_plan(rows, P, 0, prefill_attn_target(rows), &nsplit, &kps);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
@@ -1984,7 +2059,6 @@ int mlcv_prefill_attention(const void* q, int32_t q_ld, const float* cos, const 
   const int rpad = (rows + 63) / 64 * 64;
   const bool frag = hd % 64 == 0;
   MLCV_TRY(scratch_reserve(ws_n + (frag ? q_frag_halfs(KV, rpad, hd) / 2 : 0), 1));
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   AttnArgs a = prefill_attn_args(reinterpret_cast<const _Float16*>(q), q_ld, cos, sin, P, H, KV, hd, keys,
                                  reinterpret_cast<const _Float16*>(values), mask, reinterpret_cast<_Float16*>(out),
                                  nsplit, kps, g_scratch.ws);

@@ -249,6 +249,42 @@ int kvq_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const flo
                       hipStream_t st);
 
 // ---------------------------------------------------------------------------
+// The prefill's attention at head_dim 256 (attn_prefill.hip): per-chunk K/V images and q fragments
+// from the layer's writer, 128 query rows per workgroup on 32x32x16 MFMAs, key splits balanced
+// over the chunks holding a valid key, the splits combined by the last to arrive.
+struct PaPlan {
+  int nch;            // 32-key chunks
+  int nrb;            // 128-row blocks per kv head
+  int nsplit;         // key splits
+  size_t img_bytes;   // chunk images [KV][nch][48 KB]
+  size_t qf_halfs;    // q fragments [KV][nrb * 128 rows][256][hi, lo]
+  size_t part_halfs;  // the splits' fp16 O / l
+  size_t ml_floats;   // the splits' (m, l)
+  size_t counters;    // arrival counters [KV][nrb] (zero between launches)
+};
+struct PaArgs {
+  const _Float16* qf;   // q fragments (pa_writer_launch)
+  const char* img;      // chunk images of this layer
+  const float* mask;    // [P] additive, or null
+  _Float16* out;        // [P][out_ld], head h at h * 256
+  int out_ld;
+  int P, H, KV, rows;   // rows = P * H / KV per kv head
+  int nch, nrb, nsplit;
+  _Float16* part;
+  float* part_ml;
+  unsigned* ctr;
+  int noskip;           // 1: compute chunks whose keys are all masked too (same splits)
+};
+bool pa_supported(int hd, int P, int H, int KV);
+PaPlan pa_plan(int P, int H, int KV);
+// the layer's K/V cache slices (fp32 roped K, fp16 V from the q/k/v rows), the chunk images and q's
+// fragments in one launch; from_cache: images from the cache slices keys / values (read, not
+// written) and q from the rows [P][ld]
+int pa_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin, int P, int H,
+                     int KV, float q_scale, float* keys, _Float16* values, const PaPlan& plan, char* img, _Float16* qf,
+                     int from_cache, hipStream_t st);
+int pa_attn_launch(const PaArgs& a, hipStream_t st);
+
 // tiled GEMM for prefill: C[M,N] = A[M,K] . B[N,K]^T, MFMA 32x32x16
 // ---------------------------------------------------------------------------
 enum TgEpi : int {

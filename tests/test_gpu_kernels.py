@@ -252,17 +252,26 @@ def test_joint_attention_logits_are_fp32_accurate():
     assert np.any(np.abs(ref16 - ref) > bound)
 
 
+@pytest.mark.parametrize("form", ["hd256", "general"])
 @pytest.mark.parametrize("P,h,kv,hd,valid", [
     (968, 8, 1, 256, 800),   # the pi0.5 prefix: 968 tokens, 800 valid
     (968, 8, 1, 256, 968),   # no padding
+    (300, 8, 1, 256, 250),   # partial 128-row blocks and a partial last chunk, 8 key splits
+    (200, 2, 2, 256, 37),    # one kv head per q head; a valid chunk boundary mid-split
     (100, 2, 1, 64, 77),     # a small ragged case: partial row blocks and chunks
 ])
-def test_prefill_attention_vs_fp64(P, h, kv, hd, valid):
+def test_prefill_attention_vs_fp64(P, h, kv, hd, valid, form, monkeypatch):
     """The prefill's attention instantiation (q roped and scaled in the loader, fp32 roped
     keys from the cache, the prefix pad mask, no suffix block) through mlcv_prefill_attention,
     which builds the arguments and split plan the prefill uses, against float64 SDPA
-    (gemma_dual.py:236-253,334-341; :97-122)."""
-    print(f"prefill attention P={P} H={h} KV={kv} hd={hd} valid={valid}", flush=True)
+    (gemma_dual.py:236-253,334-341; :97-122).  hd256: the head_dim-256 kernel (chunk images,
+    32-row tiles, splits balanced over the valid chunks, in-kernel combine); general: the
+    attention every head dim takes (MLCV_PF_ATTN=0)."""
+    if form == "general":
+        monkeypatch.setenv("MLCV_PF_ATTN", "0")
+    elif hd != 256:
+        pytest.skip("the hd256 form is for head_dim 256")
+    print(f"prefill attention {form} P={P} H={h} KV={kv} hd={hd} valid={valid}", flush=True)
     rng = np.random.default_rng(P + valid + hd)
     nq, nkv = h * hd, kv * hd
     qkv = rng.standard_normal((P, nq + 2 * nkv)).astype(np.float16)  # the q/k/v GEMM output row layout
