@@ -432,26 +432,41 @@ __global__ __launch_bounds__(PA_NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   // ---- output ----------------------------------------------------------------------------------
   const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
   const int grp = a.H / a.KV;
-  const int row = PA_ROWS * b + 32 * w + l32;
-  const bool row_ok = row < a.rows;
-  _Float16* orow = nullptr;
-  if (row_ok) {
-    const int hl = row / a.P, t = row % a.P;
-    orow = a.out + (size_t)t * a.out_ld + (size_t)(kvh * grp + hl) * PA_HD + 4 * lh;
-  }
-  // lane value e of d tile dt is O[row][32 dt + 8 (e / 4) + 4 lh + e % 4]
-  if (S == 1) {
-    if (row_ok) {
+  // The wave's 32 rows x 256 dims in fp16 through LDS (the chunk buffers are free once the last
+  // DMA has landed): lane value e of d tile dt is O[row l32][32 dt + 8 (e / 4) + 4 lh + e % 4];
+  // written to a [32][264] half tile, then stored a row's 512 bytes per 32 lanes, not 8 bytes
+  // of 32 different rows per instruction.
+  constexpr int ORS = PA_HD + 8;  // halfs per staged row
+  _Float16* stg = reinterpret_cast<_Float16*>(sbuf) + w * 32 * ORS;
+  auto stage_out = [&](auto&& val) __attribute__((always_inline)) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          h4 v;
+      for (int i = 0; i < 4; ++i) {
+        h4 v;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = f2h(o[dt][4 * i + r] * inv);
-          *reinterpret_cast<h4*>(orow + 32 * dt + 8 * i) = v;
-        }
+        for (int r = 0; r < 4; ++r) v[r] = f2h(val(dt, 4 * i + r));
+        *reinterpret_cast<h4*>(stg + l32 * ORS + 32 * dt + 8 * i + 4 * lh) = v;
+      }
+  };
+  auto write_out = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + lh;
+      const int row = PA_ROWS * b + 32 * w + r;
+      const h8 v = *reinterpret_cast<const h8*>(stg + r * ORS + 8 * l32);
+      if (row < a.rows) {
+        const int hl = row / a.P, t = row % a.P;
+        *reinterpret_cast<h8*>(a.out + (size_t)t * a.out_ld + (size_t)(kvh * grp + hl) * PA_HD + 8 * l32) = v;
+      }
     }
+  };
+  if (S == 1) {
+    pa_vm_wait0();  // the last (past the list) DMA into the chunk buffers
+    __syncthreads();
+    stage_out([&](int dt, int e) { return o[dt][e] * inv; });
+    write_out();
     return;
   }
   // the split's O / l in fp16 (lane-local order) and its (m, l), through to the memory side
@@ -496,60 +511,57 @@ __global__ __launch_bounds__(PA_NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   float winv = 0.f;
   auto combine = [&](auto aux) __attribute__((always_inline)) {
     constexpr int AUX = decltype(aux)::value;
-    float mm[PA_MAXS], ll[PA_MAXS];
+    // every split's (m, l), then the first two splits' fragments, all in flight at once; each
+    // later split's fragments go out while the one before is accumulated
+    f2 ml[PA_MAXS];
+#pragma unroll
+    for (int sp = 0; sp < PA_MAXS; ++sp)
+      if (sp < S) ml[sp] = load_dev<f2, AUX>(rml, ((sp * PA_ROWS) + 32 * w + l32) * 8);
+    h8 v[2][8][2];
+    auto fetch = [&](int sp, int bb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) v[bb][dt][i2] = load_dev<h8, AUX>(rpart, part_off(sp, dt, i2));
+    };
+    fetch(0, 0);
+    if (S > 1) fetch(1, 1);
+    float ll[PA_MAXS];
     float M = -INFINITY;
 #pragma unroll
-    for (int sp = 0; sp < PA_MAXS; ++sp) {
-      if (sp < S) {
-        const f2 v = load_dev<f2, AUX>(rml, ((sp * PA_ROWS) + 32 * w + l32) * 8);
-        mm[sp] = v[0];
-        ll[sp] = v[1];
-        M = fmaxf(M, mm[sp]);
-      }
-    }
+    for (int sp = 0; sp < PA_MAXS; ++sp)
+      if (sp < S) M = fmaxf(M, ml[sp][0]);
     float wsum = 0.f;
 #pragma unroll
     for (int sp = 0; sp < PA_MAXS; ++sp) {
       if (sp < S) {
-        ll[sp] = ll[sp] * exp_hw(mm[sp] - M);  // the split's weight
+        ll[sp] = ml[sp][1] * exp_hw(ml[sp][0] - M);  // the split's weight
         wsum += ll[sp];
       }
     }
     winv = wsum > 0.f ? 1.0f / wsum : 0.f;
-    // the splits in order, each split's 16 fragments (O / l of every d of this lane's row)
-    // loaded at once and accumulated with the split's weight
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
-    for (int sp = 0; sp < S; ++sp) {
-      h8 v[8][2];
+    // the splits in order, each split's 16 fragments (O / l of every d of this lane's row)
+    // accumulated with the split's weight
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+    for (int sp = 0; sp < PA_MAXS; ++sp) {
+      if (sp < S) {
+        const float ws = ll[sp];
 #pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2) v[dt][i2] = load_dev<h8, AUX>(rpart, part_off(sp, dt, i2));
-      float ws = ll[0];
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int q = 1; q < PA_MAXS; ++q) ws = sp == q ? ll[q] : ws;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[dt][e] += ws * h2f(v[dt][e >> 3][e & 7]);
+          for (int e = 0; e < 16; ++e) acc[dt][e] += ws * h2f(v[sp & 1][dt][e >> 3][e & 7]);
+        if (sp + 2 < S) fetch(sp + 2, sp & 1);
+      }
     }
   };
   if (fl & 2) combine(std::integral_constant<int, 16>{});
   else combine(std::integral_constant<int, 1>{});
-  if (row_ok) {
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        h4 o4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = f2h(acc[dt][4 * i + r] * winv);
-        *reinterpret_cast<h4*>(orow + 32 * dt + 8 * i) = o4;
-      }
-  }
+  stage_out([&](int dt, int e) { return acc[dt][e] * winv; });
+  write_out();
 }
 
 }  // namespace
