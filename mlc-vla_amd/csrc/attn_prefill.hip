@@ -498,7 +498,7 @@ __global__ __launch_bounds__(PA_NT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     const unsigned old = counter_add(ctr, off ? 0x10001u : 1u);
     const bool last = (old & 0xFFFFu) == (unsigned)(S - 1);
     if (last) counter_reset(ctr);
-    slist[PA_MAXCH + 1] = last ? 1 | (off || (old >> 16) ? 2 : 0) : 0;
+    slist[PA_MAXCH + 1] = last ? 1 | (off || (old >> 16) || a.dev_combine ? 2 : 0) : 0;
   }
   __syncthreads();
   const int fl = __builtin_amdgcn_readfirstlane(slist[PA_MAXCH + 1]);

@@ -677,6 +677,10 @@ PaArgs pa_args(const PaPlan& plan, const _Float16* qf, const char* img, const fl
   a.part_ml = ml;
   a.ctr = ctr;
   a.noskip = noskip ? 1 : 0;
+  // MLCV_PA_DEV_COMBINE=1: the device-scope combine (the path taken when a split runs on another
+  // XCD than the dispatch order places it on), for the tests
+  const char* dc = std::getenv("MLCV_PA_DEV_COMBINE");
+  a.dev_combine = dc && std::atoi(dc) != 0 ? 1 : 0;
   return a;
 }
 

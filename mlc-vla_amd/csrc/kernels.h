@@ -274,6 +274,7 @@ struct PaArgs {
   float* part_ml;
   unsigned* ctr;
   int noskip;           // 1: compute chunks whose keys are all masked too (same splits)
+  int dev_combine;      // 1: the combine reads at device scope even with every split on one XCD
 };
 bool pa_supported(int hd, int P, int H, int KV);
 PaPlan pa_plan(int P, int H, int KV);

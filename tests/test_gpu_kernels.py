@@ -252,6 +252,31 @@ def test_joint_attention_logits_are_fp32_accurate():
     assert np.any(np.abs(ref16 - ref) > bound)
 
 
+def test_prefill_attention_device_scope_combine_is_bit_identical(monkeypatch):
+    """The head_dim-256 prefill attention combines its key splits in the last split to arrive,
+    reading the others from its XCD's L2 when every split ran on the XCD the dispatch order
+    places it on, else at device scope.  MLCV_PA_DEV_COMBINE=1 forces the device-scope reads:
+    the output is bit-identical (same stored partials, same arithmetic)."""
+    P, h, kv, hd, valid = 968, 8, 1, 256, 800
+    print("prefill attention: L2 vs device-scope combine", flush=True)
+    rng = np.random.default_rng(5)
+    nq, nkv = h * hd, kv * hd
+    qkv = _dev(rng.standard_normal((P, nq + 2 * nkv)).astype(np.float16))
+    keys = _dev(rng.standard_normal((kv, P, hd)).astype(np.float32) * 2.0)
+    vals = _dev(rng.standard_normal((kv, P, hd)).astype(np.float16))
+    cos, sin = (_dev(a.reshape(P, hd // 2)) for a in make_rope_np(P, hd, 10000.0))
+    mask = _dev(make_prefix_mask_np(P, num_valid=valid).reshape(P))
+    outs = []
+    for dev_combine in ("0", "1"):
+        monkeypatch.setenv("MLCV_PA_DEV_COMBINE", dev_combine)
+        out = torch.empty((P, nq), dtype=torch.float16, device="cuda")
+        N.call("mlcv_prefill_attention", _p(qkv), nq + 2 * nkv, _p(cos), _p(sin), P, h, kv, hd, _p(keys), _p(vals),
+               _p(mask), _p(out), _st())
+        outs.append(_host(out))
+    assert np.all(np.isfinite(outs[0]))
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("form", ["hd256", "general"])
 @pytest.mark.parametrize("P,h,kv,hd,valid", [
     (968, 8, 1, 256, 800),   # the pi0.5 prefix: 968 tokens, 800 valid
