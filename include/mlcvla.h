@@ -123,6 +123,11 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
  * probabilities underflow to 0 in fp32, so the results are bit-identical; 0 computes them
  * (testing). */
 #define MLCV_OPT_MASK_SKIP 9
+/* MLCV_OPT_STEP_GRAPH (default 0): denoise_step_kv replays a captured hipGraph (1) or launches
+ * its kernels directly (0).  A graph launch ends with about 8 us before the stream's next work
+ * starts, more than the graph saves on a step of about 45 launches while the host stays ahead of
+ * the GPU; denoise_loop_kv and the chunk (MLCV_OPT_USE_GRAPH) keep their graphs. */
+#define MLCV_OPT_STEP_GRAPH 10
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value);
 
 /* Synchronize `stream` and report a persistent step that ended early (a wait between its

@@ -60,6 +60,7 @@ struct Tiling {
 struct LayerTilings {
   Tiling qkv = {16, 1}, o = {16, 1, 4}, gu = {16, 1}, down = {16, 4};
   Tiling head = {16, 1}, tmlp = {16, 1};  // action_out and the time MLP (16-row tiles)
+  Tiling mod = {16, 1};                   // the adaRMS modulation GEMV (16, 32 or 64 rows)
 };
 constexpr Tiling ROWMAJOR_QKV = {16, 1}, ROWMAJOR_O = {32, 4}, ROWMAJOR_GU = {32, 1}, ROWMAJOR_DOWN = {32, 8};
 constexpr int TR_AIN = 32, SPLIT_AIN = 1;
@@ -79,13 +80,16 @@ enum : unsigned {
 };
 constexpr unsigned PF_DEFAULT = PF_ATTN_O | PF_ATTN_GU;
 
-// MLCV_TILING="qkv=16:S[:G],o=TR:S[:G],gu=TR:S[:G],down=TR:S[:G],head=16:S[:G],tmlp=16:S"
+// MLCV_TILING="qkv=16:S[:G],o=TR:S[:G],gu=TR:S[:G],down=TR:S[:G],head=16:S[:G],tmlp=16:S,mod=TR:1"
 // overrides the tile rows (16, or 32 for o / gate_up / down), K slices and, for 16-row
 // tiles, the m groups (1, 2 or 4) of the fragment-major GEMMs (the time MLP's K slices apply
 // to its small-M tiles) for tuning (read at context creation; 0 = planner).
 LayerTilings read_tilings(bool q4) {
   LayerTilings lt;
   if (!q4) lt.gu = {32, 1};
+  // q4 modulations on 64-row tiles: 4x the weight bytes per workgroup (one tile is only 9 KB of
+  // nibbles and scales at 16 rows): 33 vs 39 us per step; fp16 stays on 16 rows (39 vs 62 us)
+  if (q4) lt.mod = {64, 1};
   const char* e = std::getenv("MLCV_TILING");
   if (!e) return lt;
   std::string spec(e);
@@ -102,7 +106,8 @@ LayerTilings read_tilings(bool q4) {
       const size_t colon2 = item.find(':', colon + 1);
       int mg = colon2 == std::string::npos ? 1 : std::atoi(item.substr(colon2 + 1).c_str());
       if (!(mg == 2 || mg == 4) || tr != 16 || name == "tmlp") mg = 1;
-      if (tr == 16 || (tr == 32 && (name == "o" || name == "gu" || name == "down"))) {
+      if (name == "mod" && (tr == 16 || tr == 32 || tr == 64)) lt.mod = Tiling{tr, 1};
+      else if (tr == 16 || (tr == 32 && (name == "o" || name == "gu" || name == "down"))) {
         Tiling t{tr, sp, mg};
         if (name == "qkv") lt.qkv = t;
         else if (name == "head") lt.head = t;
@@ -142,6 +147,7 @@ struct Ctx {
   int W0, F0, W1, F1, D, H, KV, HD, P, T, A, NS, NM;
   bool bound = false;
   bool use_graph = true, hoist = true;
+  bool step_graph = false;  // denoise_step_kv as a graph replay (else direct launches)
 
   std::vector<Layer> layers;
   Lin final_mod, ain, aout, tin, tout;
@@ -261,6 +267,7 @@ struct Ctx {
   XtArgs xt{};         // buffers and dims; weights filled at bind
   float* nscale = nullptr;  // [steps][2D+1] prescale of each norm's pre-scaled input
   _Float16* ain16 = nullptr;  // action_in weights in fp16 (q4 models: dequantized at bind)
+  _Float16* aout16 = nullptr;  // action_out weights in fp16 (the XCD step's head; q4: dequantized at bind)
 
   hipStream_t cap = nullptr;
   Graph g_step, g_loop, g_prefill, g_chunk, g_m0;
@@ -580,8 +587,13 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
       MLCV_TRY(xt_attn_launch(a, st));
       MLCV_TRY(xt_mlp_launch(a, st));
     }
-    MLCV_TRY(xt_final_launch(a, st));
-    return enqueue_head(c, modp, euler, st);
+    // the final reduce, the final norm and action_out_proj (or the Euler update) in one launch
+    a.vout = c.vout;
+    a.x32 = c.x32;
+    a.xnext = c.xin16;
+    a.dt = (float)(-1.0 / c.NS);
+    a.euler = euler ? 1 : 0;
+    return xt_head_launch(a, st);
   }
   if (c.pk_on) {
     PkArgs p = c.pk;
@@ -1217,8 +1229,6 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       ALLOC(x.flags, (size_t)8 * 32);
       ALLOC(x.err, 1);
       x.x16 = c.x16;
-      x.xu = c.xu;
-      x.rowss = c.rowss;
       const std::pair<void*, size_t> zero_fill[] = {
           {x.x, D8 * TW * 2}, {x.xm, D8 * TW * 2}, {x.qf, D8 * XT_QF * 2}, {x.k32, D8 * T * hd * 4},
           {x.v, D8 * T * hd * 2}, {x.attn, D8 * 64 * hd * 2}, {x.h, D8 * 64 * (c.F1 / 8) * 2},
@@ -1323,12 +1333,14 @@ int mlcv_destroy(mlcv_ctx* ctx) {
 int mlcv_set_option(mlcv_ctx* ctx, int32_t key, int64_t value) {
   MLCV_REQUIRE(ctx, "null context");
   if (ctx->f32) {  // the float32 model runs eager launches; the step-form options do not apply
-    MLCV_REQUIRE(key == MLCV_OPT_USE_GRAPH || key == MLCV_OPT_HOIST_MODULATION || key == MLCV_OPT_MASK_SKIP,
+    MLCV_REQUIRE(key == MLCV_OPT_USE_GRAPH || key == MLCV_OPT_HOIST_MODULATION || key == MLCV_OPT_MASK_SKIP ||
+                     key == MLCV_OPT_STEP_GRAPH,
                  "this option is not built for float32 models");
     return 0;
   }
   Ctx& c = ctx->c;
   if (key == MLCV_OPT_USE_GRAPH) c.use_graph = value != 0;
+  else if (key == MLCV_OPT_STEP_GRAPH) c.step_graph = value != 0;
   else if (key == MLCV_OPT_HOIST_MODULATION) c.hoist = value != 0;
   else if (key == MLCV_OPT_PERSIST) {
     MLCV_REQUIRE(value == 0 || c.pk_ok, "the persistent step is not built for this configuration");
@@ -1530,8 +1542,9 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
       }
     }
     c.mod_ops.assign(2, OpDesc{});
-    seg_ops(c, c.mod_ops[0], first, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
-    seg_ops(c, c.mod_ops[1], rest, W1, EPI_STORE, c.q4, gtr, c.small_m ? MOD_SPLITS : 0);
+    const int mtr = c.small_m ? c.tilings.mod.tr : gtr;  // modulation tile rows
+    seg_ops(c, c.mod_ops[0], first, W1, EPI_STORE, c.q4, mtr, c.small_m ? MOD_SPLITS : 0);
+    seg_ops(c, c.mod_ops[1], rest, W1, EPI_STORE, c.q4, mtr, c.small_m ? MOD_SPLITS : 0);
     for (OpDesc& d : c.mod_ops) d.xrow = c.small_m;
     // one launch instead of two: the second piece's grid waits for the first anyway without
     // the side stream, and each tile's arithmetic is the same in either grouping
@@ -1539,7 +1552,7 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     if (c.small_m && MOD_SPLITS == 1) {
       std::vector<SkSeg> all(first);
       all.insert(all.end(), rest.begin(), rest.end());
-      seg_ops(c, c.mod_all, all, W1, EPI_STORE, c.q4, gtr, MOD_SPLITS);
+      seg_ops(c, c.mod_all, all, W1, EPI_STORE, c.q4, mtr, MOD_SPLITS);
       c.mod_all.xrow = true;
     }
   }
@@ -1567,6 +1580,13 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
     c.xt.lw = c.d_pklin;
     c.xt.ain_w = c.ain16;
     c.xt.ain_b = c.ain.b;
+    c.aout16 = const_cast<_Float16*>(c.aout.w);
+    if (c.q4) {
+      MLCV_TRY(dalloc(&c.aout16, (size_t)c.A * W1, c.bind_owned));
+      MLCV_TRY(q4_dequant_launch(c.aout.qw, c.aout.qs, c.aout16, c.A, W1, st));
+    }
+    c.xt.aout_w = c.aout16;
+    c.xt.aout_b = c.aout.b;
   }
 
   if (c.d_segs) {
@@ -1631,7 +1651,10 @@ int mlcv_denoise_step(mlcv_ctx* ctx, const void* prefix_embs, const void* x_t, c
                        return enqueue_step(c, c.pkeys, c.pvalues, c.mod, false, s, c.fork_mod);
                      },
                      st));
-  MLCV_HIP(hipMemcpyAsync(v_out, c.vout, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  {  // a kernel, not hipMemcpyAsync: its copy started about 8 us after the graph had ended
+    const CopyJob out{c.vout, v_out, (size_t)c.T * c.A * 4};
+    MLCV_TRY(copy_list_launch(&out, 1, st));
+  }
   return 0;
 }
 
@@ -1650,14 +1673,17 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
   MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
-  MLCV_TRY(run_graph(c, c.g_step, {keys, values},
-                     [&](hipStream_t s) {
-                       c.use_img = false;
-                       MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
-                       return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod);
-                     },
-                     st));
-  MLCV_HIP(hipMemcpyAsync(v_out, c.vout, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  auto body = [&](hipStream_t s) {
+    c.use_img = false;
+    MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
+    return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod);
+  };
+  if (c.step_graph) MLCV_TRY(run_graph(c, c.g_step, {keys, values}, body, st));
+  else MLCV_TRY(body(st));
+  {  // a kernel, not hipMemcpyAsync: its copy started about 8 us after the graph had ended
+    const CopyJob out{c.vout, v_out, (size_t)c.T * c.A * 4};
+    MLCV_TRY(copy_list_launch(&out, 1, st));
+  }
   return 0;
 }
 
@@ -1678,7 +1704,10 @@ int mlcv_denoise_loop_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
   MLCV_TRY(run_graph(c, c.g_loop, {keys, values}, [&](hipStream_t s) { return enqueue_loop(c, keys, vals, s); },
                      st));
-  MLCV_HIP(hipMemcpyAsync(x_out, c.x32, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  {  // a kernel, not hipMemcpyAsync: its copy started about 8 us after the graph had ended
+    const CopyJob out{c.x32, x_out, (size_t)c.T * c.A * 4};
+    MLCV_TRY(copy_list_launch(&out, 1, st));
+  }
   return 0;
 }
 
@@ -1703,7 +1732,10 @@ int mlcv_chunk(mlcv_ctx* ctx, const void* prefix_embs, const float* prefix_mask,
                        return enqueue_loop(c, c.pkeys, c.pvalues, s);
                      },
                      st));
-  MLCV_HIP(hipMemcpyAsync(x_out, c.x32, (size_t)c.T * c.A * 4, hipMemcpyDeviceToDevice, st));
+  {  // a kernel, not hipMemcpyAsync: its copy started about 8 us after the graph had ended
+    const CopyJob out{c.x32, x_out, (size_t)c.T * c.A * 4};
+    MLCV_TRY(copy_list_launch(&out, 1, st));
+  }
   return 0;
 }
 
@@ -1920,7 +1952,18 @@ int mlcv_bench_op(mlcv_ctx* ctx, int32_t op, int32_t layer, int32_t iters, const
       case MLCV_OP_OPROJ: MLCV_TRY(enqueue_oproj(c, layer, c.mod, st)); break;
       case MLCV_OP_GATEUP: MLCV_TRY(enqueue_gateup(c, layer, c.mod, st)); break;
       case MLCV_OP_DOWN: MLCV_TRY(enqueue_down(c, layer, c.mod, st)); break;
-      case MLCV_OP_HEAD: MLCV_TRY(enqueue_head(c, c.mod, false, st)); break;
+      case MLCV_OP_HEAD:
+        if (c.xt_on) {  // the XCD step's head: final reduce + norm + action_out_proj in one launch
+          XtArgs x = c.xt;
+          x.modp = c.mod;
+          x.nscale = c.nscale;
+          x.vout = c.vout;
+          x.euler = 0;
+          MLCV_TRY(xt_head_launch(x, st));
+        } else {
+          MLCV_TRY(enqueue_head(c, c.mod, false, st));
+        }
+        break;
       case MLCV_OP_ACTION_IN: MLCV_TRY(enqueue_action_in(c, c.mod, st)); break;
       case MLCV_OP_XT_ATTN:
       case MLCV_OP_XT_MLP: {

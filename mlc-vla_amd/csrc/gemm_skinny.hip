@@ -320,7 +320,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
 #pragma unroll
       for (int c = 0; c < LCPW; ++c) {
         const int kcs = kr + chunk_of(lkg, c) * KC;
-        const size_t wsl = (size_t)SLABS * lt + sl;  // 16-row slab of the shuffled weights
+        // 16-row slab of the shuffled weights (multi-slab tiles without MSD: the wave's own slab)
+        const size_t wsl = (size_t)SLABS * lt + (MSD ? sl : slab);
         if constexpr (!Q4) {
           const __amdgpu_buffer_rsrc_t rw = dev_rsrc(seg.w + wsl * KS * 512, (uint32_t)KS * 1024);
 #pragma unroll
@@ -781,7 +782,9 @@ constexpr bool sk_combo() {
     return !TABLE && ((TR == 16 && ((NORM == 2 && EPI != EPI_GATED_RES && EPI != EPI_STORE_SILU) ||
                                     (NORM == 0 && EPI == EPI_GATED_RES))) ||
                       (TR == 32 && ((NORM == 2 && EPI == EPI_GEGLU) || (NORM == 0 && EPI == EPI_GATED_RES))));
-  if (XM == 2) return TR == 16 && NORM == 0 && (EPI == EPI_STORE || (EPI == EPI_STORE_SILU && !TABLE));
+  if (XM == 2)
+    return NORM == 0 && ((TR == 16 && (EPI == EPI_STORE || (EPI == EPI_STORE_SILU && !TABLE))) ||
+                         ((TR == 32 || TR == 64) && TABLE && EPI == EPI_STORE));
   if (TABLE) return TR == 64 && NORM == 0 && EPI == EPI_STORE;
   if (TR == 16) return NORM == 1 && EPI == EPI_STORE;
   if (TR == 32) return (NORM == 1 && EPI == EPI_GEGLU) || (NORM == 0 && (EPI == EPI_GATED_RES || EPI == EPI_STORE));
@@ -909,8 +912,9 @@ int sk_launch(const SkOp& op, bool q4, hipStream_t st) {
   if (nc16 && cps >= 16 && op.mg == 4 && op.frag && norm == 0) nc = 16;
   const bool direct = op.frag || op.xrow;  // operands straight into registers, little LDS
   MLCV_REQUIRE(!(op.frag && op.xrow), "fragment-major and row-major X at once");
-  MLCV_REQUIRE(!direct || op.tr == 16 || (op.frag && op.tr == 32),
-               "register-direct operands need 16-row tiles (fragment-major X: 16 or 32)");
+  MLCV_REQUIRE(!direct || op.tr == 16 || (op.frag && op.tr == 32) || (op.xrow && (op.tr == 32 || op.tr == 64)),
+               "register-direct operands need 16-row tiles (fragment-major X: 16 or 32; small-M row-major X: "
+               "16, 32 or 64)");
   MLCV_REQUIRE(!op.xrow || (op.M <= 16 && op.K % 128 == 0 && norm == 0),
                "row-major direct X needs M <= 16, K % 128 == 0 and no prologue");
   MLCV_REQUIRE(!op.frag || (op.M < MB && op.K % 128 == 0 && op.nseg <= 3),

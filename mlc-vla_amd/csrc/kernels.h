@@ -476,19 +476,27 @@ struct XtArgs {
   int noskip;       // 1: compute key chunks whose keys are all masked too (testing the skip)
   int q4;           // the weight table holds q4f16_1 blocks (qw / qs) instead of fp16 slabs
   float eps;
-  // the final reduce's outputs in the launch chain's layout (the head reads them)
+  // the residual stream after the last layer in the launch chain's layout (the head writes it)
   _Float16* x16;    // [T][W1]
-  _Float16* xu;     // [64][W1] fragment-major, shift in row T
-  float* rowss;     // [T][W1/16]
+  // the head after the last layer (xt_head_launch): final adaRMS + action_out_proj
+  const _Float16* aout_w;  // action_out, row-major [A][W1] fp16 (q4 models: dequantized at bind)
+  const _Float16* aout_b;  // [A] or null
+  float* vout;             // [T][A] velocity (euler == 0)
+  float* x32;              // [T][A] Euler state, updated in place (euler == 1)
+  _Float16* xnext;         // [T][A] fp16 copy of the updated state: the next step's action input
+  float dt;                // Euler step
+  int euler;
 };
 constexpr int XT_QF = 4 * 8 * 2 * 512;  // halfs of one head's q fragments (64 rows, 256 dims)
 // the shape the XCD tensor-parallel step is built for
 bool xt_shape_ok(int W1, int F1, int H, int KV, int HD, int T, int P, int A);
 // layer L's attention half (reduce or action_in, q/k/v, attention, combine, o_proj) and MLP
-// half (reduce, gate_up, down); the final reduce into x16 / xu / rowss
+// half (reduce, gate_up, down)
 int xt_attn_launch(const XtArgs& a, hipStream_t st);
 int xt_mlp_launch(const XtArgs& a, hipStream_t st);
-int xt_final_launch(const XtArgs& a, hipStream_t st);
+// the last layer's down partials -> residual stream (into x16) -> final adaRMS -> action_out_proj
+// -> velocity (vout) or Euler update (x32, xnext): one launch after the last layer
+int xt_head_launch(const XtArgs& a, hipStream_t st);
 
 // a batch of device-to-device copies in one launch (the entry points stage their inputs
 // into the context's buffers with one kernel instead of one copy launch per buffer)

@@ -1093,19 +1093,91 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   XT_STAMP(2 * L + 1, 6, 0);
 }
 
-// ---- the last layer's down partials -> the residual stream in the launch chain's layout --------
-__global__ __launch_bounds__(256) void xt_final_kernel(const XtArgs a) {
-  const int D = a.D;
-  XtRed r;
-  r.part = a.dpart;
-  r.xold = a.xm + xt_tw(a, D - 1, 0);
-  r.gate = xt_mod(a, 2 * D - 1) + 2 * XT_W;
-  r.mnext = xt_mod(a, 2 * D);
-  r.nsc = load_global(a.nscale + 2 * D);
-  r.x = a.x16;
-  r.rss = a.rowss;
-  r.u = a.xu;
-  xt_reduce(a, r, blockIdx.x, threadIdx.x);
+// ---- the head: last layer's down partials -> residual stream -> final adaRMS -> action_out_proj ----
+// decode_e1's final norm (gemma_dual.py:417-433), action_out_proj (pi0_model.py:142-163) and, in the
+// loop, the Euler update (pi0_model.py:165-194).  One workgroup per token row m:
+//   - the row's residual stream: the 8 XCDs' partials summed in XCD order, then the gated residual,
+//     as every layer's reduce does (stored into x16 in the launch chain's layout);
+//   - its adaRMS in the reference's order: fp32 statistics, x / sqrt(mean(x^2) + eps), times
+//     (1 + scale), plus shift, each op rounded in fp32, one rounding to fp16;
+//   - the A outputs of action_out_proj: fp32 sums over K (8 lanes per output, 128 k each), one
+//     rounding to fp16, the fp16 bias add; then the velocity in fp32, or the Euler update.
+__global__ __launch_bounds__(256) void xt_head_kernel(const XtArgs a) {
+  __shared__ float red[4];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[XT_W];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int D = a.D, T = a.T, A = a.A, n = 4 * tid;  // this thread's columns n .. n + 3
+  const int s = n >> 5, cc = n & 31;                 // residual column slice and offset in it
+  f4 p[XT_NX];
+#pragma unroll
+  for (int hx = 0; hx < XT_NX; ++hx) {
+    const size_t off = (((size_t)hx * XT_NS + s) * T + m) * 32 + cc;
+    if constexpr (XT_P16) {
+      const h4 q = load_global(reinterpret_cast<const h4*>(reinterpret_cast<const _Float16*>(a.dpart) + off));
+      p[hx] = (f4){h2f(q[0]), h2f(q[1]), h2f(q[2]), h2f(q[3])};
+    } else {
+      p[hx] = load_global(reinterpret_cast<const f4*>(a.dpart + off));
+    }
+  }
+  const h4 xo = load_global(reinterpret_cast<const h4*>(a.xm + xt_tw(a, D - 1, 0) + (size_t)m * XT_W + n));
+  const h4 g = load_global(reinterpret_cast<const h4*>(xt_mod(a, 2 * D - 1) + 2 * XT_W + n));
+  const _Float16* fin = xt_mod(a, 2 * D);
+  const h4 sc = load_global(reinterpret_cast<const h4*>(fin + n));
+  const h4 sh = load_global(reinterpret_cast<const h4*>(fin + XT_W + n));
+  h4 x;
+  float s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float acc = p[0][e];
+#pragma unroll
+    for (int hx = 1; hx < XT_NX; ++hx) acc += p[hx][e];
+    x[e] = hadd(xo[e], hmul(f2h(acc), g[e]));
+    s2 += h2f(x[e]) * h2f(x[e]);
+  }
+  if (a.x16) *reinterpret_cast<h4*>(a.x16 + (size_t)m * XT_W + n) = x;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s2 += __shfl_xor(s2, o);
+  if (lane == 0) red[w] = s2;
+  __syncthreads();
+  const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const float den = __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, (float)XT_W), a.eps));
+  h4 xn;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float nv = __fdiv_rn(h2f(x[e]), den);
+    xn[e] = f2h(__fadd_rn(__fmul_rn(nv, __fadd_rn(1.0f, h2f(sc[e]))), h2f(sh[e])));
+  }
+  *reinterpret_cast<h4*>(xs + n) = xn;
+  __syncthreads();
+  // action_out_proj: output j on lanes 8 (tid >> 3) .. +7, lane part k range [128 part, +128)
+  const int part = tid & 7;
+  for (int j = tid >> 3; j < A; j += 32) {
+    const _Float16* wr = a.aout_w + (size_t)j * XT_W + 128 * part;
+    float acc = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < 128; k += 8) {
+      const h8 wv = load_global(reinterpret_cast<const h8*>(wr + k));
+      const h8 xv = *reinterpret_cast<const h8*>(xs + 128 * part + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(h2f(xv[e]), h2f(wv[e]), acc);
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (part == 0) {
+      _Float16 y = f2h(acc);
+      if (a.aout_b) y = hadd(y, a.aout_b[j]);
+      const float v = h2f(y);
+      const size_t o = (size_t)m * A + j;
+      if (a.euler) {
+        const float nx = euler_update(a.x32[o], a.dt, v);
+        a.x32[o] = nx;
+        a.xnext[o] = f2h(nx);
+      } else {
+        a.vout[o] = v;
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -1157,10 +1229,11 @@ int xt_mlp_launch(const XtArgs& a, hipStream_t st) {
   return 0;
 }
 
-int xt_final_launch(const XtArgs& a, hipStream_t st) {
-  MLCV_REQUIRE(a.x16 && a.xu && a.rowss && a.dpart && a.xm && a.modp && a.nscale, "XCD step: final buffers");
-  MLCV_REQUIRE(a.T >= 1 && a.T < 64 && a.D >= 1, "XCD step: final shape");
-  xt_final_kernel<<<XT_NS, 256, 0, st>>>(a);
+int xt_head_launch(const XtArgs& a, hipStream_t st) {
+  MLCV_REQUIRE(a.dpart && a.xm && a.modp && a.aout_w && (a.euler ? a.x32 && a.xnext : a.vout != nullptr),
+               "XCD step: head buffers");
+  MLCV_REQUIRE(a.T >= 1 && a.T < 64 && a.D >= 1 && a.A >= 1, "XCD step: head shape");
+  xt_head_kernel<<<a.T, 256, 0, st>>>(a);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

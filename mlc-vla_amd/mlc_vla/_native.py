@@ -26,6 +26,7 @@ MLCV_OPT_XTP = 6
 MLCV_OPT_XTP_KEEP = 7
 MLCV_OPT_SYNC_WORDS = 8
 MLCV_OPT_MASK_SKIP = 9
+MLCV_OPT_STEP_GRAPH = 10
 PROBES = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "x_mid": 5, "h": 6, "mod": 7, "vout": 8, "xcd_x": 9}
 
 _vp = ctypes.c_void_p

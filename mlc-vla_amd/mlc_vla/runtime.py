@@ -187,6 +187,11 @@ class VirtualMachine:
     def set_graph(self, on: bool) -> None:
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_USE_GRAPH, int(bool(on)))
 
+    def set_step_graph(self, on: bool) -> None:
+        """denoise_step_kv as a captured hipGraph replay (off by default: direct launches, whose
+        step ends sooner than a graph replay's; the loop and the chunk keep their graphs)."""
+        N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_STEP_GRAPH, int(bool(on)))
+
     def set_hoist(self, on: bool) -> None:
         N.call("mlcv_set_option", self._ctx, N.MLCV_OPT_HOIST_MODULATION, int(bool(on)))
 

@@ -66,14 +66,19 @@ def test_xtp_matches_reused_buffers_and_launch_chain(xstep):
 
 def test_xtp_graph_replays_and_device_loop(xstep):
     """Replays of the captured step (barrier words advance across launches) with eager work in
-    between give the same velocity, and the in-graph 10-step loop equals the host loop."""
+    between give the same velocity as the direct launches, and the in-graph 10-step loop equals
+    the host loop."""
     s = xstep
     s.runner.vm.set_xtp_keep(False)
     try:
         v0 = s.run()
-        for _ in range(4):
-            torch.randn(1000, device="cuda").sum().item()
-            np.testing.assert_array_equal(s.run(), v0)
+        s.runner.vm.set_step_graph(True)
+        try:
+            for _ in range(4):
+                torch.randn(1000, device="cuda").sum().item()
+                np.testing.assert_array_equal(s.run(), v0)
+        finally:
+            s.runner.vm.set_step_graph(False)
         prefix = np.random.default_rng(1).standard_normal((1, s.cfg.prefix_len, s.cfg.vlm.width)).astype(np.float16)
         noise = np.random.default_rng(2).standard_normal((1, s.cfg.action_horizon, s.cfg.action_dim)).astype(np.float32)
         params0 = [s.p[n] if is_ae(n) else torch.zeros_like(s.p[n]) for n, _ in s.runner.named_params]
