@@ -498,6 +498,14 @@ def main():
             ts.append(e0.elapsed_time(e1) * 1e3)
         return ts
 
+    def stage_step_inputs():
+        """The op hooks read the context's staged copies of a step's inputs; a directly launched
+        step reads the caller's tensors in place, so one step runs as a graph replay (staged)."""
+        vm.set_step_graph(True)
+        vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)
+        vm.set_step_graph(False)
+        torch.cuda.synchronize()
+
     if args.only_op == "prefill":  # the prefill graph alone (MFMA counters of the prefill GEMMs)
         for _ in range(args.op_iters):
             vm["prefill"](prefix, pm_800, params)
@@ -507,9 +515,8 @@ def main():
     if args.only_op:
         op = N.OPS[args.only_op]
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        if args.only_op.startswith("xt_"):  # the XCD launches read the inputs of a step
-            vm["denoise_step_kv"](keys, values, x_t, te, c968, s968, pm_all, params)
-            torch.cuda.synchronize()
+        if args.only_op.startswith("xt_") or args.only_op == "head":
+            stage_step_inputs()
         N.call("mlcv_bench_op", vm._ctx, op, OP_LAYER.get(args.only_op, 0), args.op_iters, runtime._ptr(keys),
                runtime._ptr(values), st)
         torch.cuda.synchronize()
@@ -563,6 +570,7 @@ def main():
                          "GBps": round(b / (us * 1e-6) / 1e9, 1), "bytes": int(b), "flops": int(f)}
         return tab
 
+    stage_step_inputs()
     per_op = op_table(OPS_PER_STEP)
     per_op_chain = op_table(OPS_PER_STEP_CHAIN)
     dom = max(per_op, key=lambda k: per_op[k]["us_per_step"])

@@ -566,10 +566,20 @@ int enqueue_action_in(Ctx& c, const _Float16* modp, hipStream_t st) {  // action
   return run_op(c, c.op_ain, ain, st);
 }
 
+// the caller's own step inputs and output, read and written in place by the XCD step when it is
+// launched directly (no graph holds the pointers); null members: the context's staged copies
+struct StepIO {
+  const _Float16* x_t = nullptr;
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  const float* mask = nullptr;
+  float* vout = nullptr;
+};
+
 // ---- one suffix-only velocity evaluation (modulations already in modp) -------
 // forked: the modulation pieces run on the side stream (enqueue_time_mod with fork)
 int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float16* modp, bool euler,
-                 hipStream_t st, bool forked = false) {
+                 hipStream_t st, bool forked = false, const StepIO& io = StepIO{}) {
   if (c.xt_on) {
     // the XCD tensor-parallel layers, then the launch chain's head on the residual stream
     XtArgs a = c.xt;
@@ -578,10 +588,11 @@ int enqueue_step(Ctx& c, const float* keys, const _Float16* values, const _Float
     a.nscale = c.nscale + mi;
     a.keys = keys;
     a.values = values;
-    a.mask = c.mask;
-    a.cos = c.cos;
-    a.sin = c.sin;
-    a.xin = c.xin16;
+    a.mask = io.mask ? io.mask : c.mask;
+    a.cos = io.cos ? io.cos : c.cos;
+    a.sin = io.sin ? io.sin : c.sin;
+    a.xin = io.x_t ? io.x_t : c.xin16;
+    a.vout_user = io.vout;
     for (int L = 0; L < c.D; ++L) {
       a.L = L;
       MLCV_TRY(xt_attn_launch(a, st));
@@ -1669,17 +1680,33 @@ int mlcv_denoise_step_kv(mlcv_ctx* ctx, const float* keys, const void* values, c
   Ctx& c = ctx->c;
   MLCV_REQUIRE(c.bound, "parameters not bound");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  std::vector<CopyJob> jobs = {{x_t, c.xin16, (size_t)c.T * c.A * 2}, {time_emb, c.te, (size_t)c.W1 * 2}};
-  suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
-  MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
+  // launched directly, the XCD step reads the caller's inputs and writes its output in place
+  // (its vector loads and stores need 16-byte alignment); otherwise they are staged
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool in_place = !c.step_graph && c.xt_on && a16(x_t) && a16(time_emb) && a16(suffix_cos) &&
+                        a16(suffix_sin) && a16(prefix_mask) && a16(v_out);
+  StepIO io;
+  if (in_place) {
+    io.x_t = reinterpret_cast<const _Float16*>(x_t);
+    io.cos = suffix_cos;
+    io.sin = suffix_sin;
+    io.mask = prefix_mask;
+    io.vout = v_out;
+  } else {
+    std::vector<CopyJob> jobs = {{x_t, c.xin16, (size_t)c.T * c.A * 2}, {time_emb, c.te, (size_t)c.W1 * 2}};
+    suffix_jobs(c, suffix_cos, suffix_sin, prefix_mask, jobs);
+    MLCV_TRY(copy_list_launch(jobs.data(), (int)jobs.size(), st));
+  }
   const _Float16* vals = reinterpret_cast<const _Float16*>(values);
+  const _Float16* te = in_place ? reinterpret_cast<const _Float16*>(time_emb) : c.te;
   auto body = [&](hipStream_t s) {
     c.use_img = false;
-    MLCV_TRY(enqueue_time_mod(c, c.te, 1, s, c.fork_mod));
-    return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod);
+    MLCV_TRY(enqueue_time_mod(c, te, 1, s, c.fork_mod));
+    return enqueue_step(c, keys, vals, c.mod, false, s, c.fork_mod, io);
   };
   if (c.step_graph) MLCV_TRY(run_graph(c, c.g_step, {keys, values}, body, st));
   else MLCV_TRY(body(st));
+  if (in_place) return 0;  // the head wrote v_out
   {  // a kernel, not hipMemcpyAsync: its copy started about 8 us after the graph had ended
     const CopyJob out{c.vout, v_out, (size_t)c.T * c.A * 4};
     MLCV_TRY(copy_list_launch(&out, 1, st));

@@ -482,6 +482,7 @@ struct XtArgs {
   const _Float16* aout_w;  // action_out, row-major [A][W1] fp16 (q4 models: dequantized at bind)
   const _Float16* aout_b;  // [A] or null
   float* vout;             // [T][A] velocity (euler == 0)
+  float* vout_user;        // a second copy of the velocity (the caller's output) or null
   float* x32;              // [T][A] Euler state, updated in place (euler == 1)
   _Float16* xnext;         // [T][A] fp16 copy of the updated state: the next step's action input
   float dt;                // Euler step

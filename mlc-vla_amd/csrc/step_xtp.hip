@@ -1175,6 +1175,7 @@ __global__ __launch_bounds__(256) void xt_head_kernel(const XtArgs a) {
         a.xnext[o] = f2h(nx);
       } else {
         a.vout[o] = v;
+        if (a.vout_user) a.vout_user[o] = v;
       }
     }
   }
