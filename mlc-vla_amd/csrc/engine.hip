@@ -23,6 +23,7 @@ namespace {
 
 struct Lin {
   const _Float16* w = nullptr;
+  const _Float16* wt = nullptr;  // tile-major copy for the prefill's 32-k tiles (TgArgs::bt) or null
   const uint32_t* qw = nullptr;
   const _Float16* qs = nullptr;
   const _Float16* b = nullptr;
@@ -185,6 +186,7 @@ struct Ctx {
   // writer, 32-row MFMA tiles, splits balanced over the valid chunks and combined in-kernel);
   // MLCV_PF_ATTN=0 runs the general attention instead
   bool pa_on = false;
+  bool pf_wtile = true;  // prefill gate_up / down on tile-major weight copies (MLCV_PF_WTILE=0: row-major)
   PaPlan pa{};
   char* pa_img = nullptr;
   _Float16 *pa_qf = nullptr, *pa_part = nullptr;
@@ -780,6 +782,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     gu.K = W0;
     gu.epi = TG_GEGLU;
     gu.F = c.F0;
+    gu.bt = ly.gu[0].wt;
     gemm_ws_args(c, gu);
     MLCV_TRY(tg_launch(gu, st));
     TgArgs dn{};
@@ -794,6 +797,7 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     dn.N = W0;
     dn.K = c.F0;
     dn.epi = TG_RESIDUAL;
+    dn.bt = ly.dn[0].wt;
     gemm_ws_args(c, dn);
     MLCV_TRY(tg_launch(dn, st));
   }
@@ -1470,6 +1474,21 @@ int mlcv_bind_params(mlcv_ctx* ctx, const void* const* ptrs, int32_t count, void
         MLCV_TRY(dalloc(&w, (size_t)l->N * l->K, c.bind_owned));
         MLCV_TRY(q4_dequant_launch(l->qw, l->qs, w, l->N, l->K, st));
         l->w = w;
+      }
+    }
+  }
+
+  // tile-major copies of the prefill's gate_up and down weights: the 256 x 256 tiles read them
+  // 32 k at a time, 64 bytes per weight row; in this layout one DMA instruction of 16 rows reads
+  // one contiguous 1 KB (whole 128-byte lines) instead of 16 half lines
+  if (const char* e = std::getenv("MLCV_PF_WTILE")) c.pf_wtile = std::atoi(e) != 0;
+  if (c.pf_wtile && c.W0 % 32 == 0 && c.F0 % 32 == 0 && c.W0 % 16 == 0) {
+    for (int L = 0; L < c.D; ++L) {
+      for (Lin* l : {&c.layers[L].gu[0], &c.layers[L].dn[0]}) {
+        _Float16* t = nullptr;
+        MLCV_TRY(dalloc(&t, (size_t)l->N * l->K, c.bind_owned));
+        MLCV_TRY(wtile_shuffle_launch(l->w, t, l->N, l->K, st));
+        l->wt = t;
       }
     }
   }

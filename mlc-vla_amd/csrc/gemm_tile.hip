@@ -260,6 +260,9 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     apc[i] = ls ^ tile_swz<BK>(r);
     aoff[i] = ((m0 + r) * a.lda + apc[i] * 8) * 2;
   }
+  // tile-major weights (32-k tiles with TgArgs::bt): block (row / 16, k / 32) is 1 KB, the lane's
+  // piece at (row % 16) * 64 + 16 piece; the k tile moves the scalar offset by 1 KB per 32 k
+  const bool wt = BK == 32 && a.bt != nullptr;
   const _Float16* bbase[NBI];  // per instruction (wave-uniform): segment base and bytes
   int bbytes[NBI], boff[NBI], bpc[NBI];
 #pragma unroll
@@ -281,10 +284,10 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
       rows = (n0 < a.n1 ? a.n1 : n0 < a.n2 ? a.n2 : a.N) - seg0;
       row = n0 - seg0 + lr;
     }
-    bbase[i] = base;
+    bbase[i] = wt ? a.bt : base;
     bbytes[i] = (int)min((size_t)rows * a.ldb * 2, (size_t)0x7fffffff);
     bpc[i] = ls ^ tile_swz<BK>(r0 + lr);
-    boff[i] = (row * a.ldb + bpc[i] * 8) * 2;
+    boff[i] = wt ? ((row - lr) / 16 * (a.K / 32) * 1024 + lr * 64 + bpc[i] * 16) : (row * a.ldb + bpc[i] * 8) * 2;
   }
   // DMA instruction i (A rows for i < NAI, then B rows) of k tile kt into a stage
   // K past the last multiple of BK: this lane's 8-half piece at k >= K gets an offset past the
@@ -302,7 +305,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     else
       buffer_to_lds16(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i - NAI]), 0, bbytes[i - NAI], 0x00020000),
-          (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), kin ? boff[i - NAI] : OOB, ko);
+          (lptr_t)(sb + ASZ + (NBI * w + i - NAI) * 1024), kin ? boff[i - NAI] : OOB, wt ? ko * 16 : ko);
   };
   auto dma = [&](int kt, int stage, bool live) __attribute__((always_inline)) {
 #pragma unroll
@@ -511,7 +514,20 @@ bool big_plan(const TgArgs& a, GemmPlan& p) {
   return true;
 }
 
+__global__ void wtile_shuffle_kernel(const _Float16* __restrict__ w, _Float16* __restrict__ wt, int K, long n8) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;  // one 8-half piece of the copy
+  if (i >= n8) return;
+  const int KT = K / 32;
+  const long blk = i / 64;  // 1 KB block (row / 16, k tile)
+  const int e = (int)(i % 64), r = e / 4, q = e % 4;
+  const long rb = blk / KT;
+  const int kt = (int)(blk % KT);
+  *reinterpret_cast<h8*>(wt + i * 8) = *reinterpret_cast<const h8*>(w + (rb * 16 + r) * (long)K + kt * 32 + 8 * q);
+}
+
 int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
+  MLCV_REQUIRE(!a.bt || ((a.epi == TG_GEGLU || (a.n1 >= a.N && a.n2 >= a.N)) && a.ldb == a.K && a.K % 32 == 0),
+               "tile-major weights need one segment (or GeGLU) and K-contiguous rows, K % 32 == 0");
   const int tiles = p.mtiles * p.ntiles;
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
   // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
@@ -585,6 +601,14 @@ int tg_launch(const TgArgs& a, hipStream_t st) {
   const int ngroups = (ntiles + NXCD - 1) / NXCD;
   const unsigned blocks = (unsigned)(mtiles * ngroups * NXCD);
   tile_gemm_kernel<<<blocks, 256, 0, st>>>(a, mtiles, ntiles);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int wtile_shuffle_launch(const _Float16* w, _Float16* wt, int rows, int K, hipStream_t st) {
+  MLCV_REQUIRE(w && wt && rows > 0 && rows % 16 == 0 && K > 0 && K % 32 == 0, "tile-major copy: shape");
+  const long n8 = (long)rows * K / 8;
+  wtile_shuffle_kernel<<<(unsigned)((n8 + 255) / 256), 256, 0, st>>>(w, wt, K, n8);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

@@ -316,7 +316,13 @@ struct TgArgs {
   // entry points read back), when err is set
   unsigned meet_polls = TG_MEET_POLLS;
   unsigned* err = nullptr;
+  // optional tile-major copy of b0 for the 32-k tiles: [rows / 16][K / 32][16][32] halfs (one
+  // DMA instruction of 16 rows x 64 B then reads one contiguous 1 KB); only with one weight
+  // segment or GeGLU; null: b0 row-major
+  const _Float16* bt = nullptr;
 };
+// the tile-major copy of a row-major [rows][K] fp16 matrix (rows % 16 == 0, K % 32 == 0)
+int wtile_shuffle_launch(const _Float16* w, _Float16* wt, int rows, int K, hipStream_t st);
 // out[t] = fp16(table[ids[t]] * fp16(sqrt(width))) for n tokens (ids clamped into the table)
 int embed_language_launch(const int32_t* ids, int n, const _Float16* table, int vocab, int width, _Float16* out,
                           hipStream_t st);

@@ -204,3 +204,28 @@ def test_masked_chunk_skip_is_bit_exact_at_800_valid():
     for name in ["keys", "values"] + forms:
         assert np.all(np.isfinite(a[name])), name
         np.testing.assert_array_equal(a[name], b[name], err_msg=name)
+
+
+def test_prefill_tile_major_weights_bit_exact(monkeypatch):
+    """The prefill's gate_up and down read tile-major copies of their weights (one contiguous
+    1 KB per DMA instruction of 16 rows x 32 k, made at bind): the same fp16 values land in the
+    same LDS slots as with the row-major weights, so every layer's K / V is bit-identical
+    (gemma_dual.py:125-135, the prefix expert's GeGLU MLP at P = 968)."""
+    cfg = Pi0Config(dtype="float16", action_horizon=50)
+    d = O.dims_from_config(cfg)
+    runner = PiZeroRunner(cfg, "rocm", cuda_graph=True)
+    p = _gpu_params(O.param_specs(d), seed=9)
+    params = [p[n] for n, _ in runner.named_params]
+    rng = np.random.default_rng(6)
+    prefix = runtime.tensor(rng.standard_normal((1, 968, 2048)).astype(np.float16), runner.dev)
+    pm = runtime.tensor(make_prefix_mask_np(968, num_valid=800), runner.dev)
+    out = {}
+    for wt in ("1", "0"):  # read at bind: each pass binds the parameters again
+        monkeypatch.setenv("MLCV_PF_WTILE", wt)
+        runner.vm._bound = None  # the binding is cached by pointer: force the bind to run again
+        print(f"prefill with MLCV_PF_WTILE={wt}", flush=True)
+        k, v = runner.vm["prefill"](prefix, pm, params)
+        out[wt] = (k.numpy(), v.numpy())
+    assert np.all(np.isfinite(out["1"][0])) and np.all(np.isfinite(out["1"][1]))
+    np.testing.assert_array_equal(out["1"][0], out["0"][0])
+    np.testing.assert_array_equal(out["1"][1], out["0"][1])
