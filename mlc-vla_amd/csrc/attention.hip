@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) void kvq_writer_kernel(const _Float16* __restr
 // passes, one 16-byte load per piece.
 template <int NP>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const _Float16* __restrict__ x, const _Float16* __restrict__ w,
-                                                          _Float16* __restrict__ out, int dim, float eps) {
+                                                          _Float16* __restrict__ out, int dim, float eps, int tile) {
   __shared__ float red[4];
   const int r = blockIdx.x, tid = threadIdx.x, n8 = dim / 8;
   const _Float16* xr = x + (size_t)r * dim;
@@ -266,7 +266,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const _Float16* __rest
     h8 o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = f2h(h2f(v[p][e]) / dn * (1.0f + h2f(wv[e])));
-    *reinterpret_cast<h8*>(out + (size_t)r * dim + 8 * i) = o;
+    // tile-major: [rows / 16][dim / 32][16][32] (the 32-k tiles of the prefill GEMM)
+    const size_t oi = tile ? ((size_t)(r >> 4) * (dim >> 5) + (8 * i >> 5)) * 512 + (r & 15) * 32 + (8 * i & 31)
+                           : (size_t)r * dim + 8 * i;
+    *reinterpret_cast<h8*>(out + oi) = o;
   }
 }
 
@@ -494,11 +497,12 @@ int q_frag_launch(const _Float16* q, int ld, const float* cos, const float* sin,
 }
 
 int rmsnorm_launch(const _Float16* x, const _Float16* w, _Float16* out, int rows, int dim, float eps,
-                   hipStream_t st) {
+                   hipStream_t st, bool tile) {
   const bool vec = dim % 8 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-  if (vec && dim <= 256 * 8) rmsnorm_vec_kernel<1><<<rows, 256, 0, st>>>(x, w, out, dim, eps);
-  else if (vec && dim <= 256 * 8 * 4) rmsnorm_vec_kernel<4><<<rows, 256, 0, st>>>(x, w, out, dim, eps);
+  MLCV_REQUIRE(!tile || (vec && dim % 32 == 0 && dim <= 256 * 8 * 4), "tile-major RMSNorm output: dim % 32 == 0");
+  if (vec && dim <= 256 * 8) rmsnorm_vec_kernel<1><<<rows, 256, 0, st>>>(x, w, out, dim, eps, tile ? 1 : 0);
+  else if (vec && dim <= 256 * 8 * 4) rmsnorm_vec_kernel<4><<<rows, 256, 0, st>>>(x, w, out, dim, eps, tile ? 1 : 0);
   else rmsnorm_kernel<<<rows, 256, 0, st>>>(x, w, out, dim, eps);
   MLCV_HIP(hipGetLastError());
   return 0;

@@ -768,7 +768,6 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     o.epi = TG_RESIDUAL;
     gemm_ws_args(c, o);
     MLCV_TRY(tg_launch(o, st));
-    MLCV_TRY(rmsnorm_launch(c.px, ly.ln_post0, c.pxn, P, W0, c.cfg.rms_norm_eps, st));
     TgArgs gu{};
     gu.a = c.pxn;
     gu.lda = W0;
@@ -784,7 +783,6 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     gu.F = c.F0;
     gu.bt = ly.gu[0].wt;
     gemm_ws_args(c, gu);
-    MLCV_TRY(tg_launch(gu, st));
     TgArgs dn{};
     dn.a = c.ph;
     dn.lda = c.F0;
@@ -799,6 +797,13 @@ int enqueue_prefill(Ctx& c, float* keys, _Float16* values, hipStream_t st) {
     dn.epi = TG_RESIDUAL;
     dn.bt = ly.dn[0].wt;
     gemm_ws_args(c, dn);
+    // with the weights tile-major, the MLP's activations are too: the post-attention norm writes
+    // gate_up's X and gate_up writes down's X in the 32-k tiles' layout (whole 1 KB per DMA
+    // instruction on both operands), when both GEMMs run on those tiles
+    const bool xtile = c.pf_wtile && gu.bt && dn.bt && tg_plan_k32(gu) && tg_plan_k32(dn);
+    gu.at = gu.ct = dn.at = xtile ? 1 : 0;
+    MLCV_TRY(rmsnorm_launch(c.px, ly.ln_post0, c.pxn, P, W0, c.cfg.rms_norm_eps, st, xtile));
+    MLCV_TRY(tg_launch(gu, st));
     MLCV_TRY(tg_launch(dn, st));
   }
   return 0;
@@ -1055,7 +1060,8 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
   ALLOC(c.k32, (size_t)T * nkv);
   const size_t P = c.P;
   ALLOC(c.px, P * c.W0);
-  ALLOC(c.pxn, P * c.W0);
+  const size_t P16 = (P + 15) / 16 * 16;  // whole 16-row blocks of the tile-major MLP activations
+  ALLOC(c.pxn, P16 * c.W0);
   ALLOC(c.pqkv, P * (nq + 2 * nkv));
   ALLOC(c.pctx, P * nq);
   if (hd % 64 == 0) ALLOC(c.pqf, q_frag_halfs(c.KV, (int)((P * (c.H / c.KV) + 63) / 64 * 64), hd));
@@ -1075,7 +1081,12 @@ int mlcv_create(const mlcv_config* cfg, mlcv_ctx** out) {
       return fail(-1);
     }
   }
-  ALLOC(c.ph, P * c.F0);
+  ALLOC(c.ph, P16 * c.F0);
+  // rows past P of the tile-major blocks are read (their products are never stored): keep them finite
+  if (hipMemset(c.pxn, 0, P16 * c.W0 * 2) != hipSuccess || hipMemset(c.ph, 0, P16 * c.F0 * 2) != hipSuccess) {
+    set_error("prefill activations: hipMemset failed");
+    return fail(-1);
+  }
   ALLOC(c.pcos, P * hd / 2);
   ALLOC(c.psin, P * hd / 2);
   ALLOC(c.pkeys, (size_t)c.D * kv_slice(c));

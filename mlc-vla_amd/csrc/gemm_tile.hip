@@ -251,14 +251,19 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   static_assert(NAI * RPI * NWV == BM && NBI * RPI * NWV == BN, "whole DMA instructions per wave");
   // row in the instruction and LDS slot of this lane; the piece it loads depends on the tile row
   const int lr = lane / LPR, ls = lane % LPR;
+  // tile-major X (32-k tiles with TgArgs::at): whole 16-row blocks, so the buffer ends at the
+  // last block's end (rows past M inside it are finite data whose products are never stored)
+  const bool xt = BK == 32 && a.at != 0;
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<_Float16*>(a.a), 0, (int)min((size_t)a.M * a.lda * 2, (size_t)0x7fffffff), 0x00020000);
+      const_cast<_Float16*>(a.a), 0,
+      (int)min(xt ? (size_t)((a.M + 15) / 16) * 16 * a.lda * 2 : (size_t)a.M * a.lda * 2, (size_t)0x7fffffff),
+      0x00020000);
   int aoff[NAI], apc[NAI];
 #pragma unroll
   for (int i = 0; i < NAI; ++i) {
     const int r = (NAI * w + i) * RPI + lr;
     apc[i] = ls ^ tile_swz<BK>(r);
-    aoff[i] = ((m0 + r) * a.lda + apc[i] * 8) * 2;
+    aoff[i] = xt ? (m0 + r - lr) / 16 * (a.K / 32) * 1024 + lr * 64 + apc[i] * 16 : ((m0 + r) * a.lda + apc[i] * 8) * 2;
   }
   // tile-major weights (32-k tiles with TgArgs::bt): block (row / 16, k / 32) is 1 KB, the lane's
   // piece at (row % 16) * 64 + 16 piece; the k tile moves the scalar offset by 1 KB per 32 k
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     const int ko = (kbeg + kt * BK) * 2;
     const bool kin = live && kbeg + kt * BK + (i < NAI ? apc[i] : bpc[i - NAI]) * 8 < a.K;
     if (i < NAI)
-      buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), kin ? aoff[i] : OOB, ko);
+      buffer_to_lds16(rA, (lptr_t)(sb + (NAI * w + i) * 1024), kin ? aoff[i] : OOB, xt ? ko * 16 : ko);
     else
       buffer_to_lds16(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(bbase[i - NAI]), 0, bbytes[i - NAI], 0x00020000),
@@ -430,7 +435,9 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
             const _Float16 gv = f2h(acc[2 * hb][mb][4 * q + i]), uv = f2h(acc[2 * hb + 1][mb][4 * q + i]);
             y[i] = hmul(f2h(gelu_tanh_hw(h2f(gv))), uv);
           }
-          *reinterpret_cast<h4*>(a.c + (size_t)m * a.ldc + jo) = y;
+          const size_t ci = a.ct ? ((size_t)(m >> 4) * (a.ldc >> 5) + (jo >> 5)) * 512 + (m & 15) * 32 + (jo & 31)
+                                 : (size_t)m * a.ldc + jo;
+          *reinterpret_cast<h4*>(a.c + ci) = y;
         }
       }
     return;
@@ -528,6 +535,10 @@ __global__ void wtile_shuffle_kernel(const _Float16* __restrict__ w, _Float16* _
 int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   MLCV_REQUIRE(!a.bt || ((a.epi == TG_GEGLU || (a.n1 >= a.N && a.n2 >= a.N)) && a.ldb == a.K && a.K % 32 == 0),
                "tile-major weights need one segment (or GeGLU) and K-contiguous rows, K % 32 == 0");
+  // the tile-major X / output layouts exist only in the 32-k tiles of 256 x 256
+  const bool k32 = p.bm == 256 && (p.bn == 256 || a.epi == TG_GEGLU);
+  MLCV_REQUIRE(!(a.at || a.ct) || (k32 && a.lda == a.K && a.K % 32 == 0 && (!a.ct || (a.epi == TG_GEGLU && a.ldc % 32 == 0))),
+               "tile-major X / GeGLU output: only on the 256 x 256 tiles of 32 k");
   const int tiles = p.mtiles * p.ntiles;
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
   // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
@@ -603,6 +614,12 @@ int tg_launch(const TgArgs& a, hipStream_t st) {
   tile_gemm_kernel<<<blocks, 256, 0, st>>>(a, mtiles, ntiles);
   MLCV_HIP(hipGetLastError());
   return 0;
+}
+
+bool tg_plan_k32(const TgArgs& a) {
+  GemmPlan p{};
+  return a.K % 8 == 0 && a.lda % 8 == 0 && a.ldb % 8 == 0 && big_plan(a, p) && p.bm == 256 &&
+         (p.bn == 256 || a.epi == TG_GEGLU);
 }
 
 int wtile_shuffle_launch(const _Float16* w, _Float16* wt, int rows, int K, hipStream_t st) {

@@ -232,8 +232,9 @@ int attn_img_prep_launch(const void* keys, int k_f32, const _Float16* values, co
 int attn_launch(const AttnArgs& a, hipStream_t st);
 
 // prefill helpers
+// tile: the output in the prefill GEMM's tile-major layout [ceil(rows / 16)][dim / 32][16][32]
 int rmsnorm_launch(const _Float16* x, const _Float16* w, _Float16* out, int rows, int dim, float eps,
-                   hipStream_t st);
+                   hipStream_t st, bool tile = false);
 int kv_writer_launch(const _Float16* qkv, int ld, int koff, int voff, const float* cos, const float* sin,
                      int P, int KV, int hd, float* keys, _Float16* values, hipStream_t st);
 // q of the prefill [P][ld] (heads of hd columns from column 0) roped with cos / sin [P][hd/2],
@@ -320,7 +321,13 @@ struct TgArgs {
   // DMA instruction of 16 rows x 64 B then reads one contiguous 1 KB); only with one weight
   // segment or GeGLU; null: b0 row-major
   const _Float16* bt = nullptr;
+  // the 32-k tiles' X (a) read / GeGLU output (c) written tile-major [ceil(rows / 16)][K / 32][16][32]
+  // (a: its buffer holds whole 16-row blocks; rows past M are never stored to by c)
+  int at = 0, ct = 0;
 };
+// whether tg_launch runs this GEMM on the 256 x 256 tiles of 32 k (the only tiles that read
+// TgArgs::at and write TgArgs::ct)
+bool tg_plan_k32(const TgArgs& a);
 // the tile-major copy of a row-major [rows][K] fp16 matrix (rows % 16 == 0, K % 32 == 0)
 int wtile_shuffle_launch(const _Float16* w, _Float16* wt, int rows, int K, hipStream_t st);
 // out[t] = fp16(table[ids[t]] * fp16(sqrt(width))) for n tokens (ids clamped into the table)

@@ -207,10 +207,11 @@ def test_masked_chunk_skip_is_bit_exact_at_800_valid():
 
 
 def test_prefill_tile_major_weights_bit_exact(monkeypatch):
-    """The prefill's gate_up and down read tile-major copies of their weights (one contiguous
-    1 KB per DMA instruction of 16 rows x 32 k, made at bind): the same fp16 values land in the
-    same LDS slots as with the row-major weights, so every layer's K / V is bit-identical
-    (gemma_dual.py:125-135, the prefix expert's GeGLU MLP at P = 968)."""
+    """The prefill's gate_up and down read tile-major copies of their weights (made at bind) and
+    tile-major activations (the post-attention norm's output, gate_up's GeGLU output): one
+    contiguous 1 KB per DMA instruction of 16 rows x 32 k.  The same fp16 values land in the same
+    LDS slots as with the row-major operands, so every layer's K / V is bit-identical
+    (gemma_dual.py:125-135, the prefix expert's GeGLU MLP at P = 968 with its 8 pad rows)."""
     cfg = Pi0Config(dtype="float16", action_horizon=50)
     d = O.dims_from_config(cfg)
     runner = PiZeroRunner(cfg, "rocm", cuda_graph=True)
