@@ -110,6 +110,48 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   combine_row<MAXS, false>(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
+// The attention and its split combine in one launch (decode shapes: every workgroup resident
+// at once).  Workgroup id runs row block b = 8 (id / 8 / nsplit) + id % 8 (over the kv heads)
+// against key split (id / 8) % nsplit, so the splits of a row block are dealt to one XCD (the
+// dispatch order is round-robin over the 8 XCDs).  Each split stores its partial (O_s / l_s in
+// fp16, (m, l) in fp32) with device-scope stores; the splits of a row block meet at a counter
+// (group_meet_gen, bounded); then workgroup `split` combines rows split, split + nsplit, ... of
+// the block, one wave per row, with device-scope loads (so a workgroup placed on another XCD
+// than the order gives still reads the right values).  A meeting that gives up raises *err and
+// writes NaN rows instead.
+template <int HD, bool KF32, int MAXS>
+__global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a, unsigned* meet, unsigned polls, unsigned* err) {
+  __shared__ __attribute__((aligned(16))) char lds_raw[2 * attn_buf_bytes<HD, false>()];
+  __shared__ int met;
+  const int id = blockIdx.x, x = id % 8, j = id / 8;
+  const int rbs = (a.rows + ROWS - 1) / ROWS;  // row blocks per kv head
+  const int b = (j / a.nsplit) * 8 + x, split = j % a.nsplit;
+  if (b >= rbs * a.KV) return;  // no row block on this slot: takes part in no meeting
+  const int kvh = b / rbs, bx = b % rbs, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  attn_block<HD, KF32, false, false, false, true, 4>(a, bx, split, kvh, lds_raw, tid);
+  wait_all_memory();  // this wave's partial stores have completed
+  __syncthreads();
+  if (tid == 0) {
+    met = group_meet_gen(meet + 32 * b, (unsigned)a.nsplit, polls) ? 1 : 0;
+    if (!met && err) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();
+  for (int r = split + a.nsplit * w; r < ROWS; r += 4 * a.nsplit) {
+    const int row = bx * ROWS + r;
+    if (row >= a.rows) break;
+    if (met) {
+      combine_row<MAXS, true>(a, kvh, row, lane);
+    } else {
+      const int grp = a.H / a.KV, hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
+      for (int d = 4 * lane; d < a.hd; d += 256) {
+        const float nan = __builtin_nanf("");
+        const h4 o4 = {f2h(nan), f2h(nan), f2h(nan), f2h(nan)};
+        *reinterpret_cast<h4*>(a.out + (size_t)t * a.out_ld + (size_t)h * HD + d) = o4;
+      }
+    }
+  }
+}
+
 // q fragments of the prefill: one thread per (kv head, 16-row tile, k step of the first half
 // of the head dims, lane): lane 16 g + r of k step ks takes row 16 tile + r, dims
 // d = 32 ks + 8 g .. +7 and their RoPE partners d + hd/2, and writes their hi and lo halves,
@@ -334,6 +376,22 @@ int copy_list_launch(const CopyJob* jobs, int n, hipStream_t st) {
   if (k == 0) return 0;
   const unsigned bx = (unsigned)std::min<size_t>(256, (most / 16 + 255) / 256 + 1);
   copy_list_kernel<<<dim3(bx, k), 256, 0, st>>>(L);
+  MLCV_HIP(hipGetLastError());
+  return 0;
+}
+
+int attn_fused_launch(const AttnArgs& a, unsigned* meet, unsigned polls, unsigned* err, hipStream_t st) {
+  MLCV_REQUIRE(a.H % a.KV == 0 && a.rows == a.Tq * (a.H / a.KV) && a.hd == 256 && !a.qf && !a.kimg && !a.cos &&
+                   !a.out_frag && a.ks_roped && a.nsplit >= 2 && a.nsplit <= 32 && a.kps % KCH == 0 &&
+                   a.part_o && a.part_ml && meet,
+               "one-launch attention: head_dim 256, raw q, roped suffix keys, 2..32 splits, workspace");
+  const int nsp = a.nsplit - (a.Ts > 0 ? 1 : 0);
+  MLCV_REQUIRE((long)nsp * a.kps >= (long)a.Sp && (a.Sp > 0 || nsp == 0), "attention splits do not cover the keys");
+  const int nrb = (a.rows + ROWS - 1) / ROWS * a.KV;
+  const unsigned blocks = (unsigned)((nrb + 7) / 8 * a.nsplit * 8);
+  MLCV_REQUIRE((int)blocks <= device_cus(), "one-launch attention: every workgroup must be resident at once");
+  if (a.kp_f32) attn_fused_kernel<256, true, 32><<<blocks, 256, 0, st>>>(a, meet, polls, err);
+  else attn_fused_kernel<256, false, 32><<<blocks, 256, 0, st>>>(a, meet, polls, err);
   MLCV_HIP(hipGetLastError());
   return 0;
 }

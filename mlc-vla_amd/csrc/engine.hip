@@ -2053,6 +2053,8 @@ struct Scratch {
   std::mutex mu;
   float* ws = nullptr;
   size_t ws_n = 0;
+  unsigned* meet = nullptr;  // meeting words of the one-launch attention (32 per row block, zeroed)
+  size_t meet_n = 0;
   unsigned* counters = nullptr;
   size_t counters_n = 0;
   SkSeg* seg = nullptr;
@@ -2060,7 +2062,7 @@ struct Scratch {
 };
 Scratch g_scratch;
 
-int scratch_reserve(size_t ws_n, size_t counters_n) {
+int scratch_reserve(size_t ws_n, size_t counters_n, size_t meet_n = 0) {
   if (!g_scratch.seg) MLCV_HIP(hipMalloc(&g_scratch.seg, sizeof(SkSeg)));
   if (!g_scratch.zero) {
     MLCV_HIP(hipMalloc(&g_scratch.zero, 64 * 64 * sizeof(float)));
@@ -2071,6 +2073,12 @@ int scratch_reserve(size_t ws_n, size_t counters_n) {
     MLCV_HIP(hipMalloc(&g_scratch.ws, ws_n * sizeof(float)));
     g_scratch.ws_n = ws_n;
   }
+  if (meet_n > g_scratch.meet_n) {
+    if (g_scratch.meet) MLCV_HIP(hipFree(g_scratch.meet));
+    MLCV_HIP(hipMalloc(&g_scratch.meet, meet_n * sizeof(unsigned)));
+    MLCV_HIP(hipMemset(g_scratch.meet, 0, meet_n * sizeof(unsigned)));
+    g_scratch.meet_n = meet_n;
+  }
   if (counters_n > g_scratch.counters_n) {
     if (g_scratch.counters) MLCV_HIP(hipFree(g_scratch.counters));
     MLCV_HIP(hipMalloc(&g_scratch.counters, counters_n * sizeof(unsigned)));
@@ -2080,6 +2088,9 @@ int scratch_reserve(size_t ws_n, size_t counters_n) {
   return 0;
 }
 }  // namespace
+
+static int tile_scratch(float** ws_out, unsigned** sync_out, unsigned** err_out, unsigned** err_dev_out);
+static int tile_meet_failed(unsigned* err, const char* what);
 
 int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32_t hd, const void* kp,
                          int32_t k_f32, const void* vp, int32_t Sp, const float* mask, const void* ks,
@@ -2111,6 +2122,30 @@ int mlcv_joint_attention(const void* q, int32_t Tq, int32_t H, int32_t KV, int32
   a.out_ld = H * hd;
   a.rows = Tq * (H / KV);
   a.rpad = ((a.rows + 63) / 64) * 64;
+  // decode shapes (head_dim 256, every workgroup resident at once): the attention and its split
+  // combine in one launch, one 32-key chunk per prefix split (more when that gives more than 31),
+  // the suffix keys as the last split
+  {
+    const int nch = (Sp + 31) / 32;
+    const char* ke = std::getenv("MLCV_ATTN_FUSED_KPS");  // keys per prefix split (tuning)
+    const int kps = ke ? std::max(32, std::atoi(ke) / 32 * 32) : 32 * std::max(1, (nch + 30) / 31);
+    const int nsplit = (Sp + kps - 1) / kps + (Ts > 0 ? 1 : 0), nrb = a.rpad / 64 * KV;
+    const char* fe = std::getenv("MLCV_ATTN_FUSED");
+    if (hd == 256 && nsplit >= 2 && nsplit <= 32 && (nrb + 7) / 8 * nsplit * 8 <= device_cus() &&
+        !(fe && std::atoi(fe) == 0)) {
+      a.nsplit = nsplit;
+      a.kps = kps;
+      float* tws = nullptr;
+      unsigned *tsync = nullptr, *err = nullptr, *err_dev = nullptr;
+      MLCV_TRY(tile_scratch(&tws, &tsync, &err, &err_dev));
+      MLCV_TRY(tile_meet_failed(err, "mlcv_joint_attention (an earlier call)"));
+      std::lock_guard<std::mutex> lk(g_scratch.mu);
+      MLCV_TRY(scratch_reserve(attn_ws_floats(KV, a.rows, hd, nsplit), 1, (size_t)32 * nrb));
+      a.part_o = g_scratch.ws;
+      a.part_ml = g_scratch.ws + (size_t)KV * a.nsplit * a.rpad * hd;
+      return attn_fused_launch(a, g_scratch.meet, TG_MEET_POLLS, err_dev, st);
+    }
+  }
   attn_plan(a.rows, Sp, Ts, 128, &a.nsplit, &a.kps);
   std::lock_guard<std::mutex> lk(g_scratch.mu);
   const size_t need = attn_ws_floats(KV, a.rows, hd, a.nsplit);
@@ -2224,7 +2259,7 @@ static int tile_meet_failed(unsigned* err, const char* what) {
   const unsigned e = __atomic_load_n(err, __ATOMIC_ACQUIRE);
   if (e == 0) return 0;
   __atomic_store_n(err, 0u, __ATOMIC_RELEASE);
-  set_error(std::string(what) + ": a split-K meeting gave up (error word " + std::to_string(e) +
+  set_error(std::string(what) + ": a meeting of split workgroups gave up (error word " + std::to_string(e) +
             "; other work held the CUs the split workgroups need); that output is invalid");
   return -4;
 }

@@ -230,6 +230,11 @@ size_t attn_img_bytes(int KV, int Sp, int hd);
 int attn_img_prep_launch(const void* keys, int k_f32, const _Float16* values, const float* mask, int layers, int KV,
                          int Sp, int hd, char* img, hipStream_t st);
 int attn_launch(const AttnArgs& a, hipStream_t st);
+// the attention and its split combine in one launch (head_dim 256, at most 32 splits, every
+// workgroup resident at once: (row blocks rounded up to 8) x nsplit <= CUs); meet: 32 zeroed
+// words per row block, kept between calls; a meeting that runs out of `polls` raises *err
+// (pinned host memory) and writes NaN rows
+int attn_fused_launch(const AttnArgs& a, unsigned* meet, unsigned polls, unsigned* err, hipStream_t st);
 
 // prefill helpers
 // tile: the output in the prefill GEMM's tile-major layout [ceil(rows / 16)][dim / 32][16][32]
