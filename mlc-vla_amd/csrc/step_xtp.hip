@@ -121,6 +121,19 @@ constexpr int XB_GUSC = XB_GU + 16384;            // q4 gate_up: 2 slabs x 8 chu
 constexpr int XB_DNSC = XB_DN + 8192;             // q4 down: 2 slabs x 4 chunks; scales 1 KB
 static_assert(XA_WSC + 2048 <= XA_WO && XA_WOSC + 512 <= XA_KV && XB_GUSC + 2048 <= XB_DN && XB_DNSC + 1024 <= XB_RED,
               "q4 LDS");
+// q4 with the stream waves unpacking (MLCV_XT_Q4_UNPACK, default on): the nibble blocks and scales
+// land in a staging area and the stream waves write the fp16 slab layout of the fp16 product, so
+// the compute waves run the same product as for fp16 weights.  Staging: launch A, the k-group sum
+// area (free until the q/k/v product ends): 2 slabs x 8 chunks of 1 KB, then their 2 KB of scales;
+// launch B, past its fp16 layout: up to 2 slabs x 8 chunks and 2 KB of scales
+#ifndef MLCV_XT_Q4_UNPACK
+#define MLCV_XT_Q4_UNPACK 3
+#endif
+// bit 0: launch A's q/k/v; bit 1: launch B's gate_up and down
+constexpr bool XT_UNPACK_A = (MLCV_XT_Q4_UNPACK & 1) != 0, XT_UNPACK = (MLCV_XT_Q4_UNPACK & 2) != 0;
+constexpr int XA_ST = XA_RED, XA_STSC = XA_ST + 16384;
+constexpr int XB_ST = XB_BYTES, XB_STSC = XB_ST + 16384, XB_BYTES_Q4 = XB_STSC + 2048;
+static_assert(XA_STSC + 2048 <= XA_RED + 4 * 2 * 4 * 64 * 16 && XB_BYTES_Q4 <= 160 * 1024, "q4 staging LDS");
 
 struct XtSh {
   unsigned base;  // this workgroup's barrier word at launch start (equal across the XCD)
@@ -223,6 +236,58 @@ __device__ __forceinline__ void xt_dma_q4(const uint32_t* qw, const _Float16* qs
   const __amdgpu_buffer_rsrc_t rs = dev_rsrc(qs + b0 * 64, nch * 128);
   for (int c = v; c < nch; c += nv) xt_dma(rq, c, wq + (slot * lch + c) * 1024, lane);
   for (int c = 2 * v; c < nch; c += 2 * nv) xt_dma4(rs, c * 128, wsc + (slot * lch + c) * 128, lane);
+}
+
+// q4 blocks for the stream waves' unpacking: `nch` chunks from chunk c0 of 16-row slab `slab` (kcn
+// chunks per slab) into staging slot sl (nibble blocks at wq + (sl nch + c) KB, scales at wsc +
+// (sl nch + c) 128 B).  Chunk pair p of the slot (2 nibble blocks and their 256 bytes of scales,
+// one 4-byte-per-lane DMA) belongs to stream wave (sl nch / 2 + p) mod nv, which also unpacks it.
+__device__ __forceinline__ void xt_dma_q4_pairs(const uint32_t* qw, const _Float16* qs, int slab, int kcn, int c0,
+                                                int nch, char* wq, char* wsc, int sl, int v, int nv, int lane) {
+  const size_t b0 = (size_t)slab * kcn + c0;
+  const __amdgpu_buffer_rsrc_t rq = dev_rsrc(qw + b0 * 256, nch * 1024);
+  const __amdgpu_buffer_rsrc_t rs = dev_rsrc(qs + b0 * 64, nch * 128);
+  for (int p = 0; p < nch / 2; ++p) {
+    if ((sl * (nch / 2) + p) % nv != v) continue;
+    xt_dma(rq, 2 * p, wq + (sl * nch + 2 * p) * 1024, lane);
+    xt_dma(rq, 2 * p + 1, wq + (sl * nch + 2 * p + 1) * 1024, lane);
+    xt_dma4(rs, 2 * p * 128, wsc + (sl * nch + 2 * p) * 128, lane);
+  }
+}
+// 8 consecutive weights of one q4 word in k order: (n - 7) * scale in fp16 (quant.py:176-193), the
+// same two fp16 roundings as dequant_word (only the element order differs)
+__device__ __forceinline__ h8 dequant_word_nat(uint32_t word, _Float16 s) {
+  h8 r;
+  const h2 bias = {(_Float16)1031.0f, (_Float16)1031.0f};
+  const h2 sc = {s, s};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t bits = ((word >> (8 * p)) & 0xFu) | (((word >> (8 * p + 4)) & 0xFu) << 16) | 0x64006400u;
+    h2 v = __builtin_bit_cast(h2, bits);
+    v = (v - bias) * sc;
+    r[2 * p] = v[0];
+    r[2 * p + 1] = v[1];
+  }
+  return r;
+}
+// this stream wave's chunk pairs of staging slot sl into the fp16 slab layout of xt_mma (block
+// (sl, k step kw) at wl + (sl WKS + kw) KB, lane 16 g + r holding W[r][32 kw + 8 g .. +7]); q4 lane
+// 16 gq + r holds row r's quantization group gq of the chunk, word j its k 8 j .. 8 j + 7
+__device__ __forceinline__ void xt_unpack_q4_pairs(const char* wq, const char* wsc, int nch, char* wl, int WKS, int sl,
+                                                   int v, int nv, int lane) {
+  const int r = lane & 15, gq = lane >> 4;
+  for (int p = 0; p < nch / 2; ++p) {
+    if ((sl * (nch / 2) + p) % nv != v) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = 2 * p + i, kw = 4 * c + gq;
+      const u4 q = *reinterpret_cast<const u4*>(wq + ((sl * nch + c) * 64 + lane) * 16);
+      const _Float16 sc = *reinterpret_cast<const _Float16*>(wsc + ((sl * nch + c) * 64 + lane) * 2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<h8*>(wl + ((sl * WKS + kw) * 64 + 16 * j + r) * 16) = dequant_word_nat(q[j], sc);
+    }
+  }
 }
 
 // ---- compute waves: the skinny GEMM pieces ---------------------------------------------------
@@ -668,7 +733,10 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
     for (int sl = 0; sl < nsl; ++sl) {
       const int j = s + XT_NS * sl;
       const int which = j < 16 ? PK_Q : j < 32 ? PK_K : PK_V, slab = j < 16 ? 16 * h + j : j < 32 ? j - 16 : j - 32;
-      if constexpr (Q4) {
+      if constexpr (Q4 && XT_UNPACK_A) {
+        xt_dma_q4_pairs(xt_qw(a, L, which), xt_qs(a, L, which), slab, XT_W / 128, 0, XT_W / 128, lds + XA_ST,
+                        lds + XA_STSC, sl, v, 2, lane);
+      } else if constexpr (Q4) {
         xt_dma_q4(xt_qw(a, L, which), xt_qs(a, L, which), slab, XT_W / 128, 0, XT_W / 128, lds + XA_W, lds + XA_WSC,
                   sl, XT_W / 128, v, 2, lane);
       } else {
@@ -683,6 +751,13 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   XT_STAMP(2 * L, 1, 0);
   xt_arrive(a, h, s, comp, 1, sh);
   if (v == 0 || v == 1) xt_vm_wait<0>();  // the q/k/v blocks have landed (this wave issued only those)
+  if constexpr (Q4 && XT_UNPACK_A) {
+    // the compute waves wait here for the blocks anyway: all 8 waves unpack them, one chunk
+    // pair each, into the fp16 slab layout (barrier 1's s_barrier publishes the LDS writes)
+    xt_sync();
+    const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int sl = 0; sl < nsl; ++sl) xt_unpack_q4_pairs(lds + XA_ST, lds + XA_STSC, XT_W / 128, lds + XA_W, 32, sl, w8, 8, lane);
+  }
   XT_STAMP(2 * L, 11, XT_NC);
   if (!xt_wait(a, h, 1, sh)) return;
   if (v >= 2) store_chunk<XT_HD, 128>(R, kv, tid - XT_NC - 128);  // nothing reads the chunk before barrier 2
@@ -692,9 +767,9 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
   f4 acc[2][4];
   if (comp) {
     h8 xf[8][4];
-    xt_load_x<8, Q4>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
+    xt_load_x<8, Q4 && !XT_UNPACK_A>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
     const float part = xt_rss_quarter(a.rss + (size_t)h * T * XT_RSS, T, w, lane);
-    if constexpr (Q4) xt_mma_q4<8>(acc, xf, lds + XA_W, lds + XA_WSC, XT_W / 128, 2 * w, nsl, lane);
+    if constexpr (Q4 && !XT_UNPACK_A) xt_mma_q4<8>(acc, xf, lds + XA_W, lds + XA_WSC, XT_W / 128, 2 * w, nsl, lane);
     else xt_mma<8>(acc, xf, lds + XA_W, 32, 8 * w, nsl, lane);
     xt_red_store(acc, lds + XA_RED, w, lane);
     reinterpret_cast<float*>(lds + XA_DEN)[w * 64 + lane] = part;
@@ -966,7 +1041,7 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
 // ---- launch B: layer L's MLP half ----------------------------------------------------------
 template <bool Q4>
 __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[XB_BYTES];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 && XT_UNPACK ? XB_BYTES_Q4 : XB_BYTES];
   __shared__ XtSh sh;
   const int tid = xt_tid();
   const bool comp = tid < XT_NC;
@@ -990,7 +1065,11 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   } else {
     const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
     // gate_up slabs 64 h + 2 s, + 1 (8 gate + 8 up rows each): 64 contiguous blocks
-    if constexpr (Q4) {
+    if constexpr (Q4 && XT_UNPACK) {
+      for (int sl = 0; sl < 2; ++sl)
+        xt_dma_q4_pairs(xt_qw(a, L, PK_GU), xt_qs(a, L, PK_GU), XT_FX / 8 * h + 2 * s + sl, XT_W / 128, 0, XT_W / 128,
+                        lds + XB_ST, lds + XB_STSC, sl, v, 4, lane);
+    } else if constexpr (Q4) {
       for (int sl = 0; sl < 2; ++sl)
         xt_dma_q4(xt_qw(a, L, PK_GU), xt_qs(a, L, PK_GU), XT_FX / 8 * h + 2 * s + sl, XT_W / 128, 0, XT_W / 128,
                   lds + XB_GU, lds + XB_GUSC, sl, XT_W / 128, v, 4, lane);
@@ -1003,6 +1082,11 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   XT_STAMP(2 * L + 1, 1, 0);
   xt_arrive(a, h, s, comp, 1, sh);
   if (!comp) xt_vm_wait<0>();  // the gate_up blocks have landed
+  if constexpr (Q4 && XT_UNPACK) {  // all 8 waves unpack them, one chunk pair each
+    xt_sync();
+    const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int sl = 0; sl < 2; ++sl) xt_unpack_q4_pairs(lds + XB_ST, lds + XB_STSC, XT_W / 128, lds + XB_GU, 32, sl, w8, 8, lane);
+  }
   XT_STAMP(2 * L + 1, 11, XT_NC);
   if (!xt_wait(a, h, 1, sh)) return;
   XT_STAMP(2 * L + 1, 2, 0);
@@ -1014,14 +1098,18 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   h8 xf[8][4];
   float part = 0.f;
   if (comp) {
-    xt_load_x<8, Q4>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
+    xt_load_x<8, Q4 && !XT_UNPACK>(xf, a.u + (size_t)h * 64 * XT_W, XT_W, 8 * w, T, lane);
     part = xt_rss_quarter(a.rss + (size_t)h * T * XT_RSS, T, w, lane);
     xt_vm_wait<0>();
   }
   xt_sync();
   if (!comp) {  // down slabs 2 s, 2 s + 1, k steps [16 h, 16 h + 16)
     const int lt = tid - XT_NC, v = __builtin_amdgcn_readfirstlane(lt >> 6);
-    if constexpr (Q4) {
+    if constexpr (Q4 && XT_UNPACK) {  // chunks [4h, 4h + 4) of the 32 per slab, into the staging area
+      for (int sl = 0; sl < 2; ++sl)
+        xt_dma_q4_pairs(xt_qw(a, L, PK_DN), xt_qs(a, L, PK_DN), 2 * s + sl, XT_F / 128, 4 * h, 4, lds + XB_ST,
+                        lds + XB_STSC, sl, v, 4, lane);
+    } else if constexpr (Q4) {
       for (int sl = 0; sl < 2; ++sl)  // chunks [4h, 4h + 4) of the 32 per slab
         xt_dma_q4(xt_qw(a, L, PK_DN), xt_qs(a, L, PK_DN), 2 * s + sl, XT_F / 128, 4 * h, 4, lds + XB_DN, lds + XB_DNSC,
                   sl, 4, v, 4, lane);
@@ -1035,7 +1123,7 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
     }
   }
   if (comp) {
-    if constexpr (Q4) xt_mma_q4<8>(acc, xf, lds + XB_GU, lds + XB_GUSC, XT_W / 128, 2 * w, 2, lane);
+    if constexpr (Q4 && !XT_UNPACK) xt_mma_q4<8>(acc, xf, lds + XB_GU, lds + XB_GUSC, XT_W / 128, 2 * w, 2, lane);
     else xt_mma<8>(acc, xf, lds + XB_GU, 32, 8 * w, 2, lane);
     xt_red_store(acc, lds + XB_RED, w, lane);
     reinterpret_cast<float*>(lds + XB_DEN)[w * 64 + lane] = part;
@@ -1068,16 +1156,23 @@ __global__ __launch_bounds__(XT_NT) void xt_mlp_kernel(const XtArgs a) {
   }
   XT_STAMP(2 * L + 1, 4, 0);
   xt_arrive(a, h, s, comp, 2, sh);
-  if (!comp) xt_vm_wait<0>();  // the down blocks have landed
+  if (!comp) {
+    xt_vm_wait<0>();  // the down blocks have landed
+    if constexpr (Q4 && XT_UNPACK) {
+      const int v = __builtin_amdgcn_readfirstlane((tid - XT_NC) >> 6);
+      for (int sl = 0; sl < 2; ++sl) xt_unpack_q4_pairs(lds + XB_ST, lds + XB_STSC, 4, lds + XB_DN, 16, sl, v, 4, lane);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    }
+  }
   XT_STAMP(2 * L + 1, 12, XT_NC);
   if (!xt_wait(a, h, 2, sh)) return;
   XT_STAMP(2 * L + 1, 5, 0);
 
   // ---- 3. down, row-parallel: this XCD's 512 columns of K, outputs [32 s, 32 s + 32) ---------
   h8 xd[4][4];
-  if (comp) xt_load_x<4, Q4>(xd, a.h + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_FX, XT_FX, 4 * w, T - 1, lane);
+  if (comp) xt_load_x<4, Q4 && !XT_UNPACK>(xd, a.h + ((size_t)L * a.ls * XT_NX + h) * 64 * XT_FX, XT_FX, 4 * w, T - 1, lane);
   if (comp) {
-    if constexpr (Q4) xt_mma_q4<4>(acc, xd, lds + XB_DN, lds + XB_DNSC, 4, w, 2, lane);
+    if constexpr (Q4 && !XT_UNPACK) xt_mma_q4<4>(acc, xd, lds + XB_DN, lds + XB_DNSC, 4, w, 2, lane);
     else xt_mma<4>(acc, xd, lds + XB_DN, 16, 4 * w, 2, lane);
     xt_red_store(acc, lds + XB_RED, w, lane);
   }
