@@ -294,7 +294,7 @@ def op_bytes_flops(cfg, op):
 OPS_PER_STEP = {"modulation": 1, "xt_attn": 18, "xt_mlp": 18, "head": 1}
 OPS_PER_STEP_CHAIN = {"modulation": 1, "qkv": 18, "attention": 18, "o_proj": 18, "gate_up": 18, "down": 18, "head": 1}
 OP_LAYER = {"xt_attn": 1}  # layer 0's attention launch also computes action_in
-KERNEL_SYMBOLS = {"xt_attn": "xt_attn_kernel<false>", "xt_mlp": "xt_mlp_kernel",
+KERNEL_SYMBOLS = {"xt_attn": "xt_attn_kernel<false, false>", "xt_mlp": "xt_mlp_kernel<false>",
                   "attention": "attn_kernel<256, true, false, false, true, 8> + attn_combine_kernel<24>"}
 
 
