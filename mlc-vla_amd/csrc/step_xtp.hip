@@ -413,6 +413,12 @@ __device__ __forceinline__ float xt_rinv(const char* den, int m, float eps, floa
 #define MLCV_XT_P16 1
 #endif
 constexpr bool XT_P16 = MLCV_XT_P16 != 0;
+// the attention's split partials written through this XCD's L2 (clean lines: the launch's end has
+// less to write back) instead of plain stores
+#ifndef MLCV_XT_AP_WT
+#define MLCV_XT_AP_WT 1
+#endif
+constexpr bool XT_AP_WT = MLCV_XT_AP_WT != 0;
 // this lane's 4 columns (n .. n + 3) of row m of the partial block of (XCD h, slot s)
 __device__ __forceinline__ void xt_store_part(float* part, int h, int s, int T, int m, int n, f4 v) {
   const size_t i = (((size_t)h * XT_NS + s) * T + m) * 32 + n;
@@ -964,9 +970,16 @@ __global__ __launch_bounds__(XT_NT) void xt_attn_kernel(const XtArgs a) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int idx = 64 * it + lane, rr = idx >> 5, cc = (idx & 31) * 8;
-        if (16 * w + rr < T) *reinterpret_cast<h8*>(po + rr * XT_HD + cc) = *reinterpret_cast<const h8*>(pl + rr * XT_PLD + cc);
+        if (16 * w + rr < T) {
+          const h8 pv = *reinterpret_cast<const h8*>(pl + rr * XT_PLD + cc);
+          if constexpr (XT_AP_WT) store_dev<h8>(dev_rsrc(po, 16 * XT_HD * 2), (rr * XT_HD + cc) * 2, pv);
+          else *reinterpret_cast<h8*>(po + rr * XT_HD + cc) = pv;
+        }
       }
-      if (g == 0 && m < T) *reinterpret_cast<f2*>(aml + m * 2) = (f2){mrow, lrow};
+      if (g == 0 && m < T) {
+        if constexpr (XT_AP_WT) store_dev<f2>(dev_rsrc(aml, 64 * 8), m * 8, (f2){mrow, lrow});
+        else *reinterpret_cast<f2*>(aml + m * 2) = (f2){mrow, lrow};
+      }
     }
   }
   XT_STAMP(2 * L, 6, 0);
