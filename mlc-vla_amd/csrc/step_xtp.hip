@@ -420,10 +420,20 @@ constexpr bool XT_P16 = MLCV_XT_P16 != 0;
 #endif
 constexpr bool XT_AP_WT = MLCV_XT_AP_WT != 0;
 // this lane's 4 columns (n .. n + 3) of row m of the partial block of (XCD h, slot s)
+// the cross-XCD partials written through too (tuning switch; measured 660 vs 655 us per step: they
+// are the launch's last stores, so their acknowledgements end the launch later)
+#ifndef MLCV_XT_PART_WT
+#define MLCV_XT_PART_WT 0
+#endif
 __device__ __forceinline__ void xt_store_part(float* part, int h, int s, int T, int m, int n, f4 v) {
   const size_t i = (((size_t)h * XT_NS + s) * T + m) * 32 + n;
-  if constexpr (XT_P16) *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(part) + i) = (h4){f2h(v[0]), f2h(v[1]), f2h(v[2]), f2h(v[3])};
-  else *reinterpret_cast<f4*>(part + i) = v;
+  if constexpr (XT_P16) {
+    const h4 hv = (h4){f2h(v[0]), f2h(v[1]), f2h(v[2]), f2h(v[3])};
+    if constexpr (MLCV_XT_PART_WT != 0) store_dev<h4>(dev_rsrc(part, 0x7FFFFFF0), (int)(i * 2), hv);
+    else *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(part) + i) = hv;
+  } else {
+    *reinterpret_cast<f4*>(part + i) = v;
+  }
 }
 
 struct XtRed {
