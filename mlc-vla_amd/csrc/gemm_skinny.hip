@@ -142,24 +142,26 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
   constexpr int XMT = XM == 2 ? 1 : 4 / MG;  // this workgroup's m tiles (direct path)
   constexpr int EXT = MG > 1 && NORM == 2 ? 1 : 0;  // + the shift row's m tile (local XMT)
   constexpr int PMT = XMT + EXT;              // m tiles loaded and multiplied by the direct path
-  constexpr int RMT = MG > 1 ? PMT : 4;       // m tiles held in the k-group sums
+  constexpr int RMT = XM == 2 ? 1 : MG > 1 ? PMT : 4;  // m tiles held in the k-group sums
+  constexpr int RST = XM == 2 ? 1 : 4;                 // their m-tile stride in LDS
   constexpr int MROWS = MG > 1 ? 16 * XMT : MB;  // rows of X this workgroup covers
   // fragment-major tiles of several slabs: the 4 waves split K as in a 16-row tile and
   // every wave multiplies its X fragments by all the slabs' weights (X is loaded once per
   // workgroup); the 4 k-group partials of each slab are summed before the epilogue, which
   // keeps the (slab, kg) wave roles
-  constexpr bool MSD = XM == 1 && SLABS > 1;
+  // (small-M row-major X, XM 2, likewise: one m tile, so its k-group sums take a quarter of the LDS)
+  constexpr bool MSD = (XM == 1 || XM == 2) && SLABS > 1;
   constexpr int SW = MSD ? SLABS : 1;   // slabs per wave in the product
   constexpr int LKG = MSD ? 4 : KG;     // k groups of the product
   constexpr int LCPW = NC / LKG;        // chunks per wave per round in the product
   static_assert(!MSD || (LCPW >= 1 && LCPW * LKG == NC), "multi-slab tiles need NC >= 4");
-  constexpr int XS_HALFS = DIRECT ? LKG * SLABS * 4 * 64 * 8 : MB * XLD;
+  constexpr int XS_HALFS = DIRECT ? LKG * SLABS * RST * 64 * 8 : MB * XLD;
   __shared__ __attribute__((aligned(16))) _Float16 xs[XS_HALFS];
   __shared__ float denom[4][MB];     // NORM 1: 1 / sqrt(mean(x^2) + eps) per row, per wave;
                                      // NORM 2: each wave's partial sum of squares per row
   __shared__ f4 shiftacc[SLABS * 4]; // NORM 2: the shift row's product, per slab and lane group
   __shared__ int is_last;
-  static_assert(LKG == 1 || (size_t)LKG * SLABS * 4 * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
+  static_assert(LKG == 1 || (size_t)LKG * SLABS * RST * 64 * 4 * 4 <= sizeof(xs), "k-group sums alias the X slice");
   f4* red = reinterpret_cast<f4*>(xs);  // [LKG][SLABS][4 m tiles][64 lanes] after the last round
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -466,16 +468,16 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkOp op) {
     for (int sl = 0; sl < SW; ++sl)
 #pragma unroll
       for (int mt = 0; mt < RMT; ++mt)
-        red[((lkg * SLABS + (MSD ? sl : slab)) * 4 + mt) * 64 + lane] = acc[sl][mt];
+        red[((lkg * SLABS + (MSD ? sl : slab)) * RST + mt) * 64 + lane] = acc[sl][mt];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NOWN; ++i) {
       // with m groups, waves kg >= XMT own no m tile of the output (rows past MROWS: nothing
       // is stored); wave XMT holds the shift row's tile (pre-scaled input)
       const int mt = min(kg + i * KG, RMT - 1);
-      f4 sum = red[((0 * SLABS + slab) * 4 + mt) * 64 + lane];
+      f4 sum = red[((0 * SLABS + slab) * RST + mt) * 64 + lane];
 #pragma unroll
-      for (int q = 1; q < LKG; ++q) sum += red[((q * SLABS + slab) * 4 + mt) * 64 + lane];
+      for (int q = 1; q < LKG; ++q) sum += red[((q * SLABS + slab) * RST + mt) * 64 + lane];
       own[i] = sum;
     }
   }
@@ -793,7 +795,7 @@ constexpr bool sk_combo() {
 
 template <bool Q4, int NORM, int EPI, bool TABLE, int TR, int XM, int MG>
 int launch_nc_mg(const SkOp& op, int nc, dim3 grid, hipStream_t st) {
-  constexpr bool MSD = XM == 1 && TR > 16;  // multi-slab fragment-major tiles: 4 k groups
+  constexpr bool MSD = (XM == 1 || XM == 2) && TR > 16;  // multi-slab register-direct tiles: 4 k groups
   constexpr int KG = MSD ? 4 : 4 / (TR / 16);
   if (nc < KG) nc = KG;
   switch (nc) {
