@@ -128,11 +128,12 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a, unsigned* m
   const int b = (j / a.nsplit) * 8 + x, split = j % a.nsplit;
   if (b >= rbs * a.KV) return;  // no row block on this slot: takes part in no meeting
   const int kvh = b / rbs, bx = b % rbs, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const unsigned gen = tid == 0 ? group_gen(meet + 32 * b) : 0u;
   attn_block<HD, KF32, false, false, false, true, 4>(a, bx, split, kvh, lds_raw, tid);
   wait_all_memory();  // this wave's partial stores have completed
   __syncthreads();
   if (tid == 0) {
-    met = group_meet_gen(meet + 32 * b, (unsigned)a.nsplit, polls) ? 1 : 0;
+    met = group_meet_gen(meet + 32 * b, (unsigned)a.nsplit, polls, gen) ? 1 : 0;
     if (!met && err) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   __syncthreads();
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a, unsigned* m
     const int row = bx * ROWS + r;
     if (row >= a.rows) break;
     if (met) {
-      combine_row<MAXS, true>(a, kvh, row, lane);
+      combine_row<MAXS, true, false>(a, kvh, row, lane);  // the output is read by later launches
     } else {
       const int grp = a.H / a.KV, hl = row / a.Tq, t = row % a.Tq, h = kvh * grp + hl;
       for (int d = 4 * lane; d < a.hd; d += 256) {

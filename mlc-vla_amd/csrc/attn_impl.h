@@ -393,7 +393,9 @@ __device__ __forceinline__ void make_q(const AttnArgs& a, const QRaw<HD>& r, int
 // weight 0).  Lane s holds split s's statistics and normalized weight; each weight reaches
 // the other lanes by one v_readlane where it is used, so no per-split arrays of uniform
 // registers stay live (at 24 or 32 splits they spilled).
-template <int MAXS, bool COH>
+// COH: the partials were stored in this launch (device-scope loads); ST_DEV: the output is
+// read in this launch too (device-scope stores), otherwise by later launches (plain stores)
+template <int MAXS, bool COH, bool ST_DEV = COH>
 __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row, int lane) {
   static_assert(MAXS <= 64, "one split per lane");
   const int hd = a.hd;
@@ -447,7 +449,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int kvh, int row,
     if (d < hd) {
       const int col = h * hd + d;
       const size_t oi = a.out_frag ? xf_index(t, col) : (size_t)t * a.out_ld + col;
-      if constexpr (COH) store_dev<h4>(dev_rsrc(a.out, 0x7FFFFFF0), (int)(oi * 2), o4);
+      if constexpr (ST_DEV) store_dev<h4>(dev_rsrc(a.out, 0x7FFFFFF0), (int)(oi * 2), o4);
       else *reinterpret_cast<h4*>(a.out + oi) = o4;
     }
   }

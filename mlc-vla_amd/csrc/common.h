@@ -217,12 +217,17 @@ __device__ __forceinline__ void counter_reset(unsigned* p) {
 // others poll the generation.  The count is zero after every meeting, so launches with a
 // different n may reuse the counters; meetings over the same counters must be ordered.
 // The poll is bounded: false after `limit` polls (the group did not meet).
-__device__ __forceinline__ bool group_meet_gen(unsigned* ctr, unsigned n, unsigned limit) {
-  const unsigned gen = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// `gen` is the generation read by group_gen at the start of the launch (the meetings of
+// earlier launches over these counters have completed by then), so that read is off the
+// meeting's critical path; the wait below completes it before this arrival counts.
+__device__ __forceinline__ unsigned group_gen(const unsigned* ctr) {
+  return __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool group_meet_gen(unsigned* ctr, unsigned n, unsigned limit, unsigned gen) {
   wait_all_memory();  // the generation is read before this arrival can complete the meeting
   if (counter_add(ctr, 1u) == n - 1) {
+    counter_add(ctr + 1, 1u);  // releases the others first; nothing reads the count again here
     counter_reset(ctr);
-    counter_add(ctr + 1, 1u);
     return true;
   }
   for (unsigned i = 0; i < limit; ++i) {

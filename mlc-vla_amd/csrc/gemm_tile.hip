@@ -240,6 +240,8 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
   const int ntile_all = p.mtiles * p.ntiles, per = (ntile_all + NXCD - 1) / NXCD;
   const int tile = xcd * per + tl;
   if (tile >= ntile_all) return;
+  // split K: the generation of the tile's meeting, read now (off the meeting's critical path)
+  const unsigned gen = SPLIT && tid == 0 ? group_gen(p.sync + 32 * tile) : 0u;
   const int tm = tile % p.mtiles, tn = tile / p.mtiles;
   const int m0 = tm * BM;
   const int kbeg = s * p.kt_per * GBK, nkt = (min(a.K, kbeg + p.kt_per * GBK) - kbeg + BK - 1) / BK;
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(64 * NWV) void big_gemm_kernel(TgArgs a, GemmPlan p
     wait_all_memory();
     __syncthreads();
     if (tid == 0) {
-      met = group_meet_gen(p.sync + 32 * tile, (unsigned)S, a.meet_polls);
+      met = group_meet_gen(p.sync + 32 * tile, (unsigned)S, a.meet_polls, gen);
       if (!met && a.err) __hip_atomic_store(a.err, TG_ERR_MEET, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     __syncthreads();
