@@ -542,6 +542,10 @@ int big_launch(const TgArgs& a, const GemmPlan& p, hipStream_t st) {
   MLCV_REQUIRE(!(a.at || a.ct) || (k32 && a.lda == a.K && a.K % 32 == 0 && (!a.ct || (a.epi == TG_GEGLU && a.ldc % 32 == 0))),
                "tile-major X / GeGLU output: only on the 256 x 256 tiles of 32 k");
   const int tiles = p.mtiles * p.ntiles;
+  // the split-K kernels (every 256 x 256 product but GeGLU) store partials and meet per tile
+  MLCV_REQUIRE(!((p.bm == 256 && p.bn == 256 && a.epi != TG_GEGLU) || p.splitk > 1) ||
+                   (p.ws && p.sync && tiles <= a.sync_tiles),
+               "split-K tile GEMM without a workspace and meeting counters for its tiles");
   const unsigned blocks = (unsigned)(((tiles + NXCD - 1) / NXCD) * NXCD * p.splitk);
   // 256 x 256 tiles: 4 stages of 32 k (128 KB), 8 waves (the prefill at P = 968: down 92 vs
   // 102 us, its split-K reduction spread over twice the waves; gate_up unchanged; 5 stages

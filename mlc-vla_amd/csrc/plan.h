@@ -114,7 +114,11 @@ inline bool tile_plan(const TilePlanIn& a, TilePlan& p) {
     // where 128 x 128 would leave half the CUs idle (o_proj: 256 tiles instead of 128); else
     // 256 x 64; else 256 x 128.
     const int mt = (a.M + TG_BM - 1) / TG_BM, mt2 = (a.M + 127) / 128;
-    if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N)) {
+    // (the 256 x 256 kernel stores every tile's product as a split partial and meets on the
+    // tile's counter, also over one slice: only where the workspace and counters hold its tiles)
+    const long t256 = (long)mt * (a.N / 256);
+    if (a.K >= 8192 && a.N % 256 == 0 && (a.n1 % 16 == 0 || a.n1 == a.N) && (a.n2 % 16 == 0 || a.n2 == a.N) &&
+        a.split_ws && t256 <= a.sync_tiles && (size_t)t256 * tile_part_floats(256) <= a.ws_floats) {
       p.bn = 256;
     } else if (a.K < 8192 && a.m128 && 2 * mt2 * ((a.N + 127) / 128) >= a.cus && a.cus > 0) {
       p.bm = 128;

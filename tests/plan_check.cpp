@@ -120,6 +120,11 @@ static void check_tile() {
                     "K %d: %d slices of %d k tiles", K, p.splitk, p.kt_per);
               CHECK(p.bn == 64 || p.bn == 128 || p.bn == 256, "n tile %d", p.bn);
               if (p.bn == 64) CHECK(p.splitk == 1 && 2 * tiles >= cus, "256 x 64 tiles: %d tiles, %d splits", tiles, p.splitk);
+              // the 256 x 256 kernel (not GeGLU) stores split partials and meets even over one slice
+              if (p.bn == 256 && !geglu) {
+                CHECK(ws_given && tiles <= in.sync_tiles, "256 x 256: %d tiles, workspace %d", tiles, ws_given);
+                CHECK((size_t)tiles * p.splitk * tile_part_floats(p.bn) <= in.ws_floats, "256 x 256 partials overflow");
+              }
               if (p.splitk > 1) {
                 CHECK(!geglu && ws_given, "split-K without a workspace or with the GeGLU epilogue");
                 CHECK(tiles <= in.sync_tiles, "%d tiles, %d meeting counters", tiles, in.sync_tiles);

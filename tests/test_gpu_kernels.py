@@ -84,7 +84,10 @@ TILE_SHAPES = [(968, 2048, 2560, 0), (968, 2048, 2048, 1), (968, 2048, 16384, 2)
                # enough 256 x 64 tiles for the whole-K narrow plan, with N and K tails
                (4096, 1024, 1156, 0), (2000, 200, 1028, 1),
                # 128 x 64 tiles (128 x 128 ones would fill half the CUs), with N and K tails
-               (1000, 1000, 2040, 0)]
+               (1000, 1000, 2040, 0),
+               # K >= 8192 with more 256 x 256 tiles (264) than the split workspace and meeting
+               # counters hold (one per CU): planned on 256 x 128 tiles over the whole K
+               (2048, 8192, 8448, 1)]
 
 
 @pytest.mark.parametrize("m,k,n,epi", TILE_SHAPES)
